@@ -1,0 +1,423 @@
+// The C-ABI of libbrx: validation, the HBM slot pool, the workspace and kernel dispatch.
+// Host-side state only; the kernels live in k_*.hip.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <mutex>
+#include <string>
+
+#include "brx_internal.h"
+
+using namespace brx;
+
+namespace {
+
+thread_local std::string g_err;
+int g_device = -1;
+
+struct Workspace {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+    int device = -1;
+};
+Workspace g_ws;
+std::mutex g_ws_mu;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    return fail(BRX_EHIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+#define HIP_TRY(expr)                                   \
+    do {                                                \
+        hipError_t _e = (expr);                         \
+        if (_e != hipSuccess) return hip_fail(_e, #expr); \
+    } while (0)
+
+int check_desc(const brx_layer_desc* d) {
+    if (!d) return fail(BRX_EINVAL, "layer descriptor is NULL");
+    if (d->hidden <= 0 || d->hidden % 64)
+        return fail(BRX_EINVAL, "hidden %d must be a positive multiple of 64", d->hidden);
+    if (d->inter <= 0 || d->inter % 64)
+        return fail(BRX_EINVAL, "inter %d must be a positive multiple of 64", d->inter);
+    if (d->n_experts < 1 || d->n_experts > 512)
+        return fail(BRX_EINVAL, "n_experts %d outside [1, 512]", d->n_experts);
+    if (d->top_k < 1 || d->top_k > d->n_experts || d->top_k > 64)
+        return fail(BRX_EINVAL, "top_k %d outside [1, min(n_experts, 64)]", d->top_k);
+    if (d->quant_mode == BRX_QUANT_AFFINE) {
+        if (d->bits != 4 || d->group_size != 64)
+            return fail(BRX_EINVAL, "affine kernels take 4-bit weights in groups of 64 (got %d-bit g%d)",
+                        d->bits, d->group_size);
+        if (d->scale_dtype != BRX_SCALE_BF16 && d->scale_dtype != BRX_SCALE_F16)
+            return fail(BRX_EINVAL, "scale_dtype %d unknown", d->scale_dtype);
+    } else if (d->quant_mode == BRX_QUANT_MXFP4) {
+        if (d->bits != 4 || d->group_size != 32)
+            return fail(BRX_EINVAL, "mxfp4 is 4-bit in groups of 32 (got %d-bit g%d)", d->bits,
+                        d->group_size);
+    } else {
+        return fail(BRX_EINVAL, "quant_mode %d unknown", d->quant_mode);
+    }
+    if (d->act != BRX_ACT_SWIGLU && d->act != BRX_ACT_SWIGLU_CLAMPED)
+        return fail(BRX_EINVAL, "act %d unknown", d->act);
+    if (d->route_mode < 0 || d->route_mode > 2) return fail(BRX_EINVAL, "route_mode %d unknown", d->route_mode);
+    if (d->router_dtype != BRX_DT_F32 && d->router_dtype != BRX_DT_BF16)
+        return fail(BRX_EINVAL, "router_dtype %d unknown", d->router_dtype);
+    if (d->shared_inter < 0 || d->shared_inter % 64)
+        return fail(BRX_EINVAL, "shared_inter %d must be 0 or a multiple of 64", d->shared_inter);
+    if (d->shared_inter && d->shared_inter != d->inter)
+        return fail(BRX_EINVAL, "shared_inter %d must equal inter %d", d->shared_inter, d->inter);
+    return BRX_OK;
+}
+
+int ensure_device() {
+    if (g_device < 0) return fail(BRX_ESTATE, "brx_init() has not been called");
+    return BRX_OK;
+}
+
+int ws_reserve(size_t bytes, hipStream_t s, void** out) {
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    if (g_ws.ptr && g_ws.bytes >= bytes) { *out = g_ws.ptr; return BRX_OK; }
+    // growing: work queued on the old buffer must finish before it is released
+    HIP_TRY(hipDeviceSynchronize());
+    if (g_ws.ptr) { HIP_TRY(hipFree(g_ws.ptr)); g_ws.ptr = nullptr; g_ws.bytes = 0; }
+    size_t want = bytes + bytes / 4 + (1 << 20);
+    hipError_t e = hipMalloc(&g_ws.ptr, want);
+    if (e != hipSuccess) { g_ws.ptr = nullptr; return fail(BRX_ENOMEM, "workspace of %zu bytes: %s", want, hipGetErrorString(e)); }
+    g_ws.bytes = want;
+    (void)s;
+    *out = g_ws.ptr;
+    return BRX_OK;
+}
+
+}  // namespace
+
+struct brx_pool {
+    brx_layer_desc d;
+    Layout lay;
+    int capacity;
+    int64_t stride;
+    uint8_t* slots;
+    int32_t* g2s_dev;
+    int32_t* g2s_pinned;
+    hipEvent_t last_read;
+    hipEvent_t refill_done;
+    hipEvent_t g2s_uploaded;
+    bool read_recorded;
+    bool refill_pending;
+    bool g2s_recorded;
+};
+
+extern "C" {
+
+int brx_abi_version(void) { return BRX_ABI_VERSION; }
+
+const char* brx_last_error(void) { return g_err.c_str(); }
+
+int brx_init(int device) {
+    int n = 0;
+    HIP_TRY(hipGetDeviceCount(&n));
+    if (device < 0 || device >= n) return fail(BRX_EINVAL, "device %d outside [0, %d)", device, n);
+    HIP_TRY(hipSetDevice(device));
+    hipDeviceProp_t prop;
+    HIP_TRY(hipGetDeviceProperties(&prop, device));
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(BRX_EINVAL, "device %d is %s; libbrx is built for gfx950 only", device, prop.gcnArchName);
+    g_device = device;
+    return BRX_OK;
+}
+
+int brx_expert_layout_get(const brx_layer_desc* d, int shared, brx_expert_layout* out) {
+    int rc = check_desc(d);
+    if (rc) return rc;
+    if (!out) return fail(BRX_EINVAL, "out is NULL");
+    if (shared && !d->shared_inter) return fail(BRX_EINVAL, "layer has no shared expert");
+    Layout L = make_layout(*d, shared ? d->shared_inter : d->inter);
+    for (int p = 0; p < 3; ++p) {
+        out->weight[p] = L.p[p].w;
+        out->scales[p] = L.p[p].s;
+        out->biases[p] = L.p[p].b;
+        out->bias[p] = L.p[p].bias;
+    }
+    out->bytes_per_expert = L.bytes;
+    return BRX_OK;
+}
+
+int brx_pool_create(const brx_layer_desc* d, int capacity, brx_pool** out) {
+    int rc = check_desc(d);
+    if (rc) return rc;
+    if ((rc = ensure_device())) return rc;
+    if (!out) return fail(BRX_EINVAL, "out is NULL");
+    if (capacity < 1 || capacity > d->n_experts)
+        return fail(BRX_EINVAL, "capacity must be in [1, %d], got %d", d->n_experts, capacity);
+    brx_pool* p = new brx_pool{};
+    p->d = *d;
+    p->lay = make_layout(*d, d->inter);
+    p->capacity = capacity;
+    p->stride = (p->lay.bytes + 255) & ~(int64_t)255;
+    hipError_t e = hipMalloc(&p->slots, (size_t)p->stride * capacity);
+    if (e != hipSuccess) {
+        delete p;
+        return fail(BRX_ENOMEM, "%d slots of %lld bytes: %s", capacity, (long long)p->stride, hipGetErrorString(e));
+    }
+    e = hipMalloc(&p->g2s_dev, sizeof(int32_t) * d->n_experts);
+    if (e == hipSuccess) e = hipMemset(p->g2s_dev, 0, sizeof(int32_t) * d->n_experts);
+    if (e == hipSuccess) e = hipHostMalloc(&p->g2s_pinned, sizeof(int32_t) * d->n_experts, hipHostMallocDefault);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&p->last_read, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&p->refill_done, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&p->g2s_uploaded, hipEventDisableTiming);
+    if (e != hipSuccess) {
+        brx_pool_destroy(p);
+        return fail(BRX_ENOMEM, "pool tables: %s", hipGetErrorString(e));
+    }
+    *out = p;
+    return BRX_OK;
+}
+
+int brx_pool_destroy(brx_pool* p) {
+    if (!p) return BRX_OK;
+    (void)hipDeviceSynchronize();
+    if (p->slots) (void)hipFree(p->slots);
+    if (p->g2s_dev) (void)hipFree(p->g2s_dev);
+    if (p->g2s_pinned) (void)hipHostFree(p->g2s_pinned);
+    if (p->last_read) (void)hipEventDestroy(p->last_read);
+    if (p->refill_done) (void)hipEventDestroy(p->refill_done);
+    if (p->g2s_uploaded) (void)hipEventDestroy(p->g2s_uploaded);
+    delete p;
+    return BRX_OK;
+}
+
+int brx_pool_capacity(const brx_pool* p) { return p ? p->capacity : fail(BRX_EINVAL, "pool is NULL"); }
+
+int brx_pool_slot_ptr(brx_pool* p, int slot, void** out) {
+    if (!p || !out) return fail(BRX_EINVAL, "pool or out is NULL");
+    if (slot < 0 || slot >= p->capacity) return fail(BRX_ERANGE, "slot %d outside [0, %d)", slot, p->capacity);
+    *out = p->slots + (int64_t)slot * p->stride;
+    return BRX_OK;
+}
+
+int brx_pool_g2s_ptr(brx_pool* p, int32_t** out) {
+    if (!p || !out) return fail(BRX_EINVAL, "pool or out is NULL");
+    *out = p->g2s_dev;
+    return BRX_OK;
+}
+
+static int refill(brx_pool* p, int slot, const void* src, size_t nbytes, void* copy_stream,
+                  hipMemcpyKind kind) {
+    if (!p || !src) return fail(BRX_EINVAL, "pool or source is NULL");
+    if (slot < 0 || slot >= p->capacity) return fail(BRX_ERANGE, "slot %d outside [0, %d)", slot, p->capacity);
+    if ((int64_t)nbytes != p->lay.bytes)
+        return fail(BRX_EINVAL, "the layout accounts for %lld bytes but the region supplied %zu. "
+                    "Refusing to write a partially-filled slot.", (long long)p->lay.bytes, nbytes);
+    hipStream_t cs = (hipStream_t)copy_stream;
+    if (p->read_recorded) HIP_TRY(hipStreamWaitEvent(cs, p->last_read, 0));
+    HIP_TRY(hipMemcpyAsync(p->slots + (int64_t)slot * p->stride, src, nbytes, kind, cs));
+    HIP_TRY(hipEventRecord(p->refill_done, cs));
+    p->refill_pending = true;
+    return BRX_OK;
+}
+
+int brx_pool_refill_async(brx_pool* p, int slot, const void* host_src, size_t nbytes, void* copy_stream) {
+    return refill(p, slot, host_src, nbytes, copy_stream, hipMemcpyHostToDevice);
+}
+
+int brx_pool_refill_from_device_async(brx_pool* p, int slot, const void* dev_src, size_t nbytes,
+                                      void* copy_stream) {
+    return refill(p, slot, dev_src, nbytes, copy_stream, hipMemcpyDeviceToDevice);
+}
+
+int brx_pool_set_g2s(brx_pool* p, const int32_t* g2s_host, int n, void* stream) {
+    if (!p || !g2s_host) return fail(BRX_EINVAL, "pool or table is NULL");
+    if (n != p->d.n_experts) return fail(BRX_EINVAL, "table has %d entries, layer has %d experts", n, p->d.n_experts);
+    for (int e = 0; e < n; ++e)
+        if (g2s_host[e] >= p->capacity)
+            return fail(BRX_ERANGE, "expert %d maps to slot %d outside [0, %d)", e, g2s_host[e], p->capacity);
+    hipStream_t s = (hipStream_t)stream;
+    // the staging copy of the previous upload must have been consumed before it is rewritten
+    if (p->g2s_recorded) HIP_TRY(hipEventSynchronize(p->g2s_uploaded));
+    for (int e = 0; e < n; ++e) p->g2s_pinned[e] = g2s_host[e] > 0 ? g2s_host[e] : 0;
+    HIP_TRY(hipMemcpyAsync(p->g2s_dev, p->g2s_pinned, sizeof(int32_t) * n, hipMemcpyHostToDevice, s));
+    HIP_TRY(hipEventRecord(p->g2s_uploaded, s));
+    p->g2s_recorded = true;
+    return BRX_OK;
+}
+
+int brx_pool_sync(brx_pool* p) {
+    if (!p) return fail(BRX_EINVAL, "pool is NULL");
+    if (p->refill_pending) HIP_TRY(hipEventSynchronize(p->refill_done));
+    if (p->read_recorded) HIP_TRY(hipEventSynchronize(p->last_read));
+    if (p->g2s_recorded) HIP_TRY(hipEventSynchronize(p->g2s_uploaded));
+    return BRX_OK;
+}
+
+int brx_router_topk(const brx_layer_desc* d, const void* x, const void* w_router, const float* bias,
+                    const void* shared_gate_w, int T, int32_t* out_idx, float* out_w,
+                    float* out_shared_gate, void* stream) {
+    int rc = check_desc(d);
+    if (rc) return rc;
+    if ((rc = ensure_device())) return rc;
+    if (T < 0) return fail(BRX_EINVAL, "T %d < 0", T);
+    if (T == 0) return BRX_OK;
+    if (!x || !w_router || !out_idx || !out_w) return fail(BRX_EINVAL, "x, w_router, out_idx and out_w are required");
+    if (((uintptr_t)x | (uintptr_t)w_router) & 15) return fail(BRX_EINVAL, "x and w_router must be 16-byte aligned");
+    if (shared_gate_w && ((uintptr_t)shared_gate_w & 15)) return fail(BRX_EINVAL, "shared_gate_w must be 16-byte aligned");
+    if (shared_gate_w && !out_shared_gate) return fail(BRX_EINVAL, "shared_gate_w given without out_shared_gate");
+    hipError_t e = launch_router(*d, x, w_router, bias, shared_gate_w, T, out_idx, out_w, out_shared_gate,
+                                 (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "router launch");
+    return BRX_OK;
+}
+
+static int forward_impl(const brx_layer_desc* d, brx_pool* p, const void* x, int T, int P,
+                        const int32_t* pexp, const int32_t* ptok, const int32_t* prow, int yrows,
+                        const float* w, const void* shared_expert, const float* shared_gate,
+                        void* out, void* y_rows, unsigned flags, void* stream) {
+    const bool force_dec = flags & BRX_FWD_FORCE_DECODE, force_pf = flags & BRX_FWD_FORCE_PREFILL;
+    if (force_dec && force_pf) return fail(BRX_EINVAL, "FORCE_DECODE and FORCE_PREFILL are exclusive");
+    const bool token_mode = ptok == nullptr;
+    bool decode = force_dec || (!force_pf && (token_mode ? T <= 8 : P <= 8));
+    if (decode && (T > 8 || P > 64))
+        return fail(BRX_EINVAL, "the decode path takes at most 8 token rows and 64 pairs (T=%d, P=%d)", T, P);
+
+    FwdArgs a{};
+    a.x = (const uint16_t*)x;
+    a.P = P;
+    a.pexp = pexp;
+    a.ptok = ptok;
+    a.prow = prow;
+    a.w = w;
+    a.sgate = shared_gate;
+    a.slots = p->slots;
+    a.slot_stride = p->stride;
+    a.g2s = p->g2s_dev;
+    a.capacity = p->capacity;
+    a.shared = (const uint8_t*)shared_expert;
+    a.auto_shared = (token_mode && shared_expert) ? 1 : 0;
+    a.lay = p->lay;
+    a.lay_sh = d->shared_inter ? make_layout(*d, d->shared_inter) : p->lay;
+    a.T = T; a.H = d->hidden; a.I = d->inter; a.I_sh = shared_expert ? d->shared_inter : 0;
+    a.E = d->n_experts; a.k = d->top_k;
+    a.quant_mode = d->quant_mode; a.scale_f16 = d->scale_dtype == BRX_SCALE_F16; a.has_bias = d->has_bias;
+    a.act = d->act; a.alpha = d->alpha; a.limit = d->limit;
+    a.out = (uint16_t*)out;
+    a.yun = (uint16_t*)y_rows;
+    a.yrows = yrows;
+
+    hipStream_t s = (hipStream_t)stream;
+    size_t need = decode ? decode_workspace_bytes(a) : prefill_workspace_bytes(a);
+    void* ws = nullptr;
+    int rc = ws_reserve(need, s, &ws);
+    if (rc) return rc;
+    if (p->refill_pending) HIP_TRY(hipStreamWaitEvent(s, p->refill_done, 0));
+    hipError_t e = decode ? launch_decode(a, (uint16_t*)ws, s) : launch_prefill(a, ws, g_ws.bytes, s);
+    if (e != hipSuccess) return hip_fail(e, decode ? "decode launch" : "prefill launch");
+    HIP_TRY(hipEventRecord(p->last_read, s));
+    p->read_recorded = true;
+    return BRX_OK;
+}
+
+static int check_forward_common(const brx_layer_desc* d, brx_pool* p, const void* x) {
+    int rc = check_desc(d);
+    if (rc) return rc;
+    if ((rc = ensure_device())) return rc;
+    if (!p) return fail(BRX_EINVAL, "pool is NULL");
+    if (memcmp(&p->d, d, sizeof(brx_layer_desc)) != 0)
+        return fail(BRX_EINVAL, "descriptor differs from the one the pool was built with");
+    if (!x) return fail(BRX_EINVAL, "x is required");
+    if ((uintptr_t)x & 15) return fail(BRX_EINVAL, "x must be 16-byte aligned");
+    return BRX_OK;
+}
+
+int brx_moe_forward(const brx_layer_desc* d, brx_pool* p, const void* x, const int32_t* idx, const float* w,
+                    const void* shared_expert, const float* shared_gate, int T, void* out, void* y_unreduced,
+                    unsigned flags, void* stream) {
+    int rc = check_forward_common(d, p, x);
+    if (rc) return rc;
+    if (T < 0) return fail(BRX_EINVAL, "T %d < 0", T);
+    if (T == 0) return BRX_OK;
+    if (!idx) return fail(BRX_EINVAL, "idx is required");
+    if (out && !w) return fail(BRX_EINVAL, "a combined output needs routing weights w");
+    if (!out && !y_unreduced) return fail(BRX_EINVAL, "nothing to write: out and y_unreduced are both NULL");
+    if (((uintptr_t)out & 3) || ((uintptr_t)y_unreduced & 3))
+        return fail(BRX_EINVAL, "out and y_unreduced must be 4-byte aligned");
+    if (shared_expert && !d->shared_inter) return fail(BRX_EINVAL, "layer descriptor has no shared expert");
+    if (shared_expert && out && !shared_gate) return fail(BRX_EINVAL, "shared expert given without its gate values");
+    if (shared_expert && ((uintptr_t)shared_expert & 15)) return fail(BRX_EINVAL, "shared expert must be 16-byte aligned");
+    return forward_impl(d, p, x, T, T * d->top_k, idx, nullptr, nullptr, T * d->top_k, w, shared_expert, shared_gate, out,
+                        y_unreduced, flags, stream);
+}
+
+int brx_moe_forward_pairs(const brx_layer_desc* d, brx_pool* p, const void* x, int T,
+                          const int32_t* pair_token, const int32_t* pair_expert, const int32_t* pair_row,
+                          int n_pairs, int n_rows, const void* shared_expert, void* y_rows, unsigned flags,
+                          void* stream) {
+    int rc = check_forward_common(d, p, x);
+    if (rc) return rc;
+    if (n_pairs < 0 || T < 0) return fail(BRX_EINVAL, "negative size (T=%d, n_pairs=%d)", T, n_pairs);
+    if (n_pairs == 0) return BRX_OK;
+    if (T == 0) return fail(BRX_EINVAL, "pairs given but x has no rows");
+    if (!pair_token || !pair_expert || !y_rows) return fail(BRX_EINVAL, "pair_token, pair_expert and y_rows are required");
+    if ((uintptr_t)y_rows & 3) return fail(BRX_EINVAL, "y_rows must be 4-byte aligned");
+    if (pair_row ? n_rows < 1 : n_rows < n_pairs)
+        return fail(BRX_EINVAL, "y_rows has %d rows for %d pairs", n_rows, n_pairs);
+    if (shared_expert && !d->shared_inter) return fail(BRX_EINVAL, "layer descriptor has no shared expert");
+    if (shared_expert && ((uintptr_t)shared_expert & 15)) return fail(BRX_EINVAL, "shared expert must be 16-byte aligned");
+    return forward_impl(d, p, x, T, n_pairs, pair_expert, pair_token, pair_row, n_rows, nullptr, shared_expert, nullptr,
+                        nullptr, y_rows, flags, stream);
+}
+
+int brx_combine(const brx_layer_desc* d, const void* y_routed, const float* w, const void* y_shared,
+                const float* shared_gate, int T, void* out, void* stream) {
+    int rc = check_desc(d);
+    if (rc) return rc;
+    if ((rc = ensure_device())) return rc;
+    if (T < 0) return fail(BRX_EINVAL, "T %d < 0", T);
+    if (T == 0) return BRX_OK;
+    if (!y_routed || !w || !out) return fail(BRX_EINVAL, "y_routed, w and out are required");
+    if (y_shared && !shared_gate) return fail(BRX_EINVAL, "y_shared given without shared_gate");
+    if (((uintptr_t)y_routed | (uintptr_t)y_shared | (uintptr_t)out) & 3)
+        return fail(BRX_EINVAL, "y_routed, y_shared and out must be 4-byte aligned");
+    hipError_t e = launch_combine((const uint16_t*)y_routed, (const uint16_t*)y_shared, w, shared_gate, T,
+                                  d->top_k, d->hidden, (uint16_t*)out, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "combine launch");
+    return BRX_OK;
+}
+
+int brx_dequant(const brx_layer_desc* d, const void* expert, int proj, int shared, float* out, void* stream) {
+    int rc = check_desc(d);
+    if (rc) return rc;
+    if ((rc = ensure_device())) return rc;
+    if (!expert || !out) return fail(BRX_EINVAL, "expert and out are required");
+    if (proj < 0 || proj > 2) return fail(BRX_EINVAL, "proj %d outside [0, 2]", proj);
+    if (shared && !d->shared_inter) return fail(BRX_EINVAL, "layer has no shared expert");
+    Layout L = make_layout(*d, shared ? d->shared_inter : d->inter);
+    hipError_t e = launch_dequant(*d, L, (const uint8_t*)expert, proj, out, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "dequant launch");
+    return BRX_OK;
+}
+
+int brx_sort_pairs(const brx_layer_desc* d, const int32_t* idx, int T, int32_t* out_order,
+                   int32_t* out_offsets, void* stream) {
+    int rc = check_desc(d);
+    if (rc) return rc;
+    if ((rc = ensure_device())) return rc;
+    if (T <= 0) return fail(BRX_EINVAL, "T %d <= 0", T);
+    if (!idx || !out_order || !out_offsets) return fail(BRX_EINVAL, "idx, out_order, out_offsets are required");
+    void* ws = nullptr;
+    if ((rc = ws_reserve(sizeof(int32_t) * (d->n_experts + 2), (hipStream_t)stream, &ws))) return rc;
+    hipError_t e = launch_sort_pairs(idx, T * d->top_k, d->n_experts, d->n_experts, 0, 128, out_order,
+                                     out_offsets, (int32_t*)ws, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "sort launch");
+    return BRX_OK;
+}
+
+}  // extern "C"

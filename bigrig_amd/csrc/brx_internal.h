@@ -1,0 +1,172 @@
+// Internal declarations of libbrx: expert layout arithmetic, device helpers, kernel launchers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "brx.h"
+
+namespace brx {
+
+constexpr int kWave = 64;
+
+// ------------------------------------------------------------------ layout (host + device)
+struct Proj {
+    int64_t w, s, b, bias;  // byte offsets inside the expert (-1 = absent)
+    int32_t n_out, n_in;
+};
+
+struct Layout {
+    Proj p[3];              // gate, up, down
+    int64_t bytes;
+};
+
+// Offsets in the order stream.pack_experts writes components (weight, scales, biases, bias)
+// for projections gate_proj, up_proj, down_proj (bigrig_engine/stream.py:152-164).
+inline Layout make_layout(const brx_layer_desc& d, int inter) {
+    Layout L{};
+    int64_t pos = 0;
+    for (int p = 0; p < 3; ++p) {
+        int n_out = p < 2 ? inter : d.hidden;
+        int n_in = p < 2 ? d.hidden : inter;
+        int64_t G = n_in / d.group_size;
+        L.p[p].n_out = n_out;
+        L.p[p].n_in = n_in;
+        L.p[p].w = pos;
+        pos += (int64_t)n_out * n_in * d.bits / 8;
+        if (d.quant_mode == BRX_QUANT_AFFINE) {
+            L.p[p].s = pos; pos += (int64_t)n_out * G * 2;
+            L.p[p].b = pos; pos += (int64_t)n_out * G * 2;
+        } else {
+            L.p[p].s = pos; pos += (int64_t)n_out * G;
+            L.p[p].b = -1;
+        }
+        if (d.has_bias) { L.p[p].bias = pos; pos += (int64_t)n_out * 2; }
+        else L.p[p].bias = -1;
+    }
+    L.bytes = pos;
+    return L;
+}
+
+// Everything a forward kernel needs, passed by value.
+struct FwdArgs {
+    const uint16_t* x;          // [T, H] bf16
+    int32_t P;                  // routed (token, expert) pairs
+    const int32_t* pexp;        // [P] expert of each pair (token mode: idx [T, k] flattened)
+    const int32_t* ptok;        // [P] token row of each pair, or null: pair / k
+    const int32_t* prow;        // [P] row of each pair in yun, or null: the pair index
+    const float* w;             // [T, k]
+    const float* sgate;         // [T] or null
+    const uint8_t* slots;       // pool slot array base
+    int64_t slot_stride;        // bytes between slots
+    const int32_t* g2s;         // [E]
+    int32_t capacity;
+    const uint8_t* shared;      // shared expert bytes or null (expert id E)
+    int32_t auto_shared;        // token mode: every token also runs the shared expert
+    Layout lay;                 // routed expert layout
+    Layout lay_sh;              // shared expert layout
+    int32_t T, H, I, I_sh, E, k;
+    int32_t quant_mode, scale_f16, has_bias, act;
+    float alpha, limit;
+    uint16_t* out;              // [T, H] bf16 or null
+    uint16_t* yun;              // [yrows, H] bf16 or null (token mode: [T, k, H])
+    int32_t yrows;              // rows of yun
+};
+
+// Token row of pair p, and the row its result is written to; explicit lists are clamped so a
+// bad entry computes a wrong row rather than reading or writing out of bounds.
+__device__ __forceinline__ int pair_tok(const FwdArgs& a, int p) {
+    return a.ptok ? min(max(a.ptok[p], 0), a.T - 1) : p / a.k;
+}
+__device__ __forceinline__ int pair_row(const FwdArgs& a, int p) {
+    return a.prow ? min(max(a.prow[p], 0), a.yrows - 1) : p;
+}
+
+// ------------------------------------------------------------------ device helpers
+__device__ __forceinline__ float bf2f(uint32_t b16) { return __uint_as_float(b16 << 16); }
+
+__device__ __forceinline__ uint32_t f2bf(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return u >> 16;
+}
+
+__device__ __forceinline__ float h2f(uint32_t h16) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)h16);
+}
+
+__device__ __forceinline__ float load_scale(const uint8_t* base, int64_t idx, int scale_f16) {
+    uint16_t v = *reinterpret_cast<const uint16_t*>(base + 2 * idx);
+    return scale_f16 ? h2f(v) : bf2f(v);
+}
+
+// e2m1 code -> fp32 (OCP FP4 E2M1).
+__device__ __forceinline__ float e2m1_f32(uint32_t c) {
+    uint32_t mag = c & 7u;
+    uint32_t e = mag >> 1, m = mag & 1u;
+    uint32_t bits = e ? (((126u + e) << 23) | (m << 22)) : (m ? 0x3F000000u : 0u);
+    bits |= (c & 8u) << 28;
+    return __uint_as_float(bits);
+}
+
+// e8m0 -> 2^(e-127) (NaN for 0xFF)
+__device__ __forceinline__ float e8m0_f32(uint32_t e) {
+    if (e == 255u) return __uint_as_float(0x7fc00000u);
+    if (e == 0u) return __uint_as_float(0x00400000u);  // 2^-127, subnormal in fp32
+    return __uint_as_float(e << 23);
+}
+
+__device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }
+
+__device__ __forceinline__ float act_apply(int act, float g, float u, float alpha, float limit) {
+    if (act == BRX_ACT_SWIGLU) return silu_mul(g, u);
+    g = fminf(g, limit);
+    u = fminf(fmaxf(u, -limit), limit);
+    return g / (1.0f + expf(-alpha * g)) * (u + 1.0f);
+}
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+// sum_{i} (128 + q_i) * x_i over the 8 nibbles of `wd`, accumulated into acc.
+// xp[i] packs (x_{i}, x_{i+4}) as bf16x2: nibble i and nibble i+4 of the word land in the
+// low and high halves of ((wd >> 4i) & 0x000F000F) | 0x43004300, which is the bf16 pair
+// (128 + q_i, 128 + q_{i+4}) exactly.
+__device__ __forceinline__ float dot8_q4(uint32_t wd, const uint32_t* xp, float acc) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        uint32_t qp = ((wd >> (4 * i)) & 0x000F000Fu) | 0x43004300u;
+        acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, qp),
+                                              __builtin_bit_cast(bf16x2_t, xp[i]), acc, false);
+    }
+    return acc;
+}
+
+// Permute 8 natural-order bf16 (4 words: (x0,x1),(x2,x3),(x4,x5),(x6,x7)) into the pair
+// order dot8_q4 expects: (x0,x4),(x1,x5),(x2,x6),(x3,x7).
+__device__ __forceinline__ void perm8(const uint32_t in[4], uint32_t out[4]) {
+    out[0] = (in[0] & 0xFFFFu) | (in[2] << 16);
+    out[1] = (in[0] >> 16) | (in[2] & 0xFFFF0000u);
+    out[2] = (in[1] & 0xFFFFu) | (in[3] << 16);
+    out[3] = (in[1] >> 16) | (in[3] & 0xFFFF0000u);
+}
+
+// ------------------------------------------------------------------ launchers
+hipError_t launch_router(const brx_layer_desc& d, const void* x, const void* w_router,
+                         const float* bias, const void* sgw, int T, int32_t* out_idx,
+                         float* out_w, float* out_sg, hipStream_t s);
+hipError_t launch_decode(const FwdArgs& a, uint16_t* hbuf, hipStream_t s);
+hipError_t launch_prefill(const FwdArgs& a, void* ws, size_t ws_bytes, hipStream_t s);
+size_t prefill_workspace_bytes(const FwdArgs& a);
+size_t decode_workspace_bytes(const FwdArgs& a);
+hipError_t launch_dequant(const brx_layer_desc& d, const Layout& L, const uint8_t* expert,
+                          int proj, float* out, hipStream_t s);
+hipError_t launch_sort_pairs(const int32_t* pexp, int P, int E, int E_ext, int T_shared, int BM,
+                             int32_t* order, int32_t* offsets, int32_t* tile_start,
+                             hipStream_t s);
+hipError_t launch_combine(const uint16_t* y_routed, const uint16_t* y_shared, const float* w,
+                          const float* sg, int T, int k, int H, uint16_t* out, hipStream_t s);
+
+}  // namespace brx

@@ -1,0 +1,45 @@
+// fp32 dequantization of one projection (test hook; replaces mx.dequantize,
+// bigrig_engine/precision.py:186-189). w = s*q + b for affine (s*q exact in fp32, one
+// rounding), w = e2m1(q) * 2^(e-127) for mxfp4.
+#include "brx_internal.h"
+
+namespace brx {
+namespace {
+
+template <int MODE>
+__global__ __launch_bounds__(256) void k_dequant(const uint8_t* __restrict__ base, Proj P,
+                                                 int scale_f16, float* __restrict__ out) {
+    const int row = blockIdx.x;
+    const int n_in = P.n_in;
+    for (int k = threadIdx.x; k < n_in; k += blockDim.x) {
+        uint32_t byte = base[P.w + (int64_t)row * (n_in / 2) + k / 2];
+        uint32_t q = (byte >> ((k & 1) * 4)) & 0xFu;
+        float v;
+        if constexpr (MODE == BRX_QUANT_AFFINE) {
+            const int G = n_in / 64;
+            float s = load_scale(base + P.s, (int64_t)row * G + k / 64, scale_f16);
+            float b = load_scale(base + P.b, (int64_t)row * G + k / 64, scale_f16);
+            v = fmaf(s, (float)q, b);
+        } else {
+            const int G = n_in / 32;
+            v = e2m1_f32(q) * e8m0_f32(base[P.s + (int64_t)row * G + k / 32]);
+        }
+        out[(int64_t)row * n_in + k] = v;
+    }
+}
+
+}  // namespace
+
+hipError_t launch_dequant(const brx_layer_desc& d, const Layout& L, const uint8_t* expert,
+                          int proj, float* out, hipStream_t s) {
+    const Proj& P = L.p[proj];
+    if (d.quant_mode == BRX_QUANT_AFFINE)
+        hipLaunchKernelGGL(k_dequant<BRX_QUANT_AFFINE>, dim3(P.n_out), dim3(256), 0, s, expert, P,
+                           d.scale_dtype == BRX_SCALE_F16 ? 1 : 0, out);
+    else
+        hipLaunchKernelGGL(k_dequant<BRX_QUANT_MXFP4>, dim3(P.n_out), dim3(256), 0, s, expert, P, 0,
+                           out);
+    return hipGetLastError();
+}
+
+}  // namespace brx

@@ -1,0 +1,370 @@
+"""The bounded expert pool of one layer: HBM slots, expert<->slot tables, eviction policy.
+
+`ExpertPool` restates the residency bookkeeping of the reference's ExpertPool
+(bigrig_engine/stream.py:454-811) -- the same tables, the same free-list order, the same victim
+rules and the same errors, so the same requests produce the same slot numbers -- over slots
+that live in HBM (libbrx `brx_pool_*`). Where the reference wrote an MLX slot tensor
+(`self._slots[...][slot] = arrays[i]`, stream.py:765-769) this issues an asynchronous copy of
+the expert's packed bytes from pinned host memory on a side stream; the library orders that
+copy after every forward that may still read the slot, and the next forward after the copy.
+
+`HostStore` is the pinned host copy of every expert a pool can admit, laid out as the blob
+(stream.py:106-186), and `PinnedFetcher` serves it under the reference fetcher's duck type
+(`fetch(keys) -> {(layer, e): region}`, test_plan_invariance.py:79-87).
+"""
+from __future__ import annotations
+
+import inspect
+import time
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import formats as F
+from .policy import make_policy
+from .spec import LayerSpec
+
+
+@dataclass
+class PinnedRegion:
+    """One expert's packed bytes in pinned host memory."""
+    ptr: int
+    nbytes: int
+    owner: object = None   # keeps the backing allocation alive
+
+    def __len__(self) -> int:
+        return self.nbytes
+
+
+class HostStore:
+    """Packed experts in pinned (page-locked) host memory, one [E, bytes_per_expert] block per
+    layer. Replaces the reference's page-cache reads (WeightStore, fetch.py:161-387): a miss is
+    one PCIe copy from here."""
+
+    def __init__(self):
+        self._layers = {}
+
+    def add_layer(self, layer: int, experts) -> None:
+        """experts: list of equal-length bytes, or a uint8 array [E, bytes_per_expert]."""
+        import torch
+        if isinstance(experts, np.ndarray):
+            arr = np.ascontiguousarray(experts, dtype=np.uint8)
+        else:
+            n = {len(b) for b in experts}
+            if len(n) != 1:
+                raise ValueError(f"layer {layer}: experts differ in size {sorted(n)}")
+            arr = np.frombuffer(b"".join(experts), dtype=np.uint8).reshape(len(experts), -1)
+        t = torch.empty(arr.shape, dtype=torch.uint8, pin_memory=True)
+        t.numpy()[...] = arr
+        self._layers[int(layer)] = t
+
+    def add_layer_tensor(self, layer: int, t) -> None:
+        """A pinned torch uint8 tensor [E, bytes_per_expert] (e.g. filled from the GPU)."""
+        if not t.is_pinned():
+            raise ValueError("HostStore tensors must be pinned")
+        self._layers[int(layer)] = t
+
+    @classmethod
+    def from_blob(cls, path: str, manifest: F.Manifest, layers=None) -> "HostStore":
+        """Read every expert region of `layers` (default: all) from a packed blob."""
+        st = cls()
+        mm = np.memmap(path, dtype=np.uint8, mode="r")
+        for li in sorted(int(x) for x in manifest.layers) if layers is None else layers:
+            e = manifest.layers[str(li)]
+            E, per = int(e["n_experts"]), int(e["bytes_per_expert"])
+            rows = []
+            for x in range(E):
+                o, n = manifest.region(li, x)
+                if n != per:
+                    raise ValueError(f"region {li}:{x} is {n} bytes, layer says {per}")
+                rows.append(np.asarray(mm[o:o + n]))
+            st.add_layer(li, np.stack(rows))
+        return st
+
+    def region(self, layer: int, e: int) -> PinnedRegion:
+        t = self._layers.get(int(layer))
+        if t is None or not 0 <= int(e) < t.shape[0]:
+            raise KeyError((layer, e))
+        row = t[int(e)]
+        return PinnedRegion(row.data_ptr(), row.numel(), t)
+
+    def tensor(self, layer: int):
+        return self._layers[int(layer)]
+
+    def layers(self):
+        return sorted(self._layers)
+
+    @property
+    def nbytes(self) -> int:
+        return sum(t.numel() for t in self._layers.values())
+
+
+class PinnedFetcher:
+    """The fetcher duck type over a HostStore: every expert is already in pinned memory, so
+    prefetch/drop/warm have nothing to do."""
+
+    def __init__(self, store: HostStore):
+        self.store = store
+        self.fetches = 0
+
+    def fetch(self, keys) -> dict:
+        self.fetches += len(keys)
+        return {k: self.store.region(*k) for k in keys}
+
+    def prefetch(self, keys) -> None:
+        pass
+
+    def drop(self, keys) -> None:
+        pass
+
+    def warm(self, keys) -> None:
+        pass
+
+
+class DeviceSlots:
+    """The HBM side of a pool: libbrx slot array + device table, and the side copy stream the
+    refills run on (default priority)."""
+
+    def __init__(self, spec: LayerSpec, capacity: int, device: int = 0, copy_stream=None):
+        import ctypes as C
+
+        import torch
+        from . import lib as L
+        L.init(device)
+        self._L = L
+        self.spec = spec
+        self.desc = spec.desc()
+        h = C.c_void_p()
+        L.check(L.load().brx_pool_create(C.byref(self.desc), capacity, C.byref(h)))
+        self.handle = h
+        self.capacity = capacity
+        self.copy_stream = copy_stream if copy_stream is not None else torch.cuda.Stream(device)
+        self._stage = None          # pinned staging for non-pinned sources, and its event
+        self._stage_ev = None
+
+    def write(self, slot: int, blob) -> int:
+        """Queue the copy of one expert into `slot`; returns the bytes copied."""
+        import torch
+        L = self._L
+        cs = self.copy_stream.cuda_stream
+        if isinstance(blob, PinnedRegion):
+            L.check(L.load().brx_pool_refill_async(self.handle, slot, blob.ptr, blob.nbytes, cs))
+            return blob.nbytes
+        raw = np.frombuffer(blob, dtype=np.uint8)
+        if self._stage is None or self._stage.numel() < raw.nbytes:
+            self._stage = torch.empty(raw.nbytes, dtype=torch.uint8, pin_memory=True)
+            self._stage_ev = None
+        if self._stage_ev is not None:
+            self._stage_ev.synchronize()      # the previous copy out of the staging buffer
+        self._stage.numpy()[:raw.nbytes] = raw
+        L.check(L.load().brx_pool_refill_async(self.handle, slot, self._stage.data_ptr(),
+                                               raw.nbytes, cs))
+        self._stage_ev = torch.cuda.Event()
+        self._stage_ev.record(self.copy_stream)
+        return raw.nbytes
+
+    def write_device(self, slot: int, dev_ptr: int, nbytes: int) -> int:
+        L = self._L
+        L.check(L.load().brx_pool_refill_from_device_async(self.handle, slot, dev_ptr, nbytes,
+                                                           self.copy_stream.cuda_stream))
+        return nbytes
+
+    def set_table(self, g2s: np.ndarray, stream) -> None:
+        import ctypes as C
+        L = self._L
+        t = np.ascontiguousarray(g2s, dtype=np.int32)
+        L.check(L.load().brx_pool_set_g2s(self.handle, t.ctypes.data_as(C.POINTER(C.c_int32)),
+                                          t.size, stream))
+
+    def slot_ptr(self, slot: int) -> int:
+        import ctypes as C
+        L = self._L
+        out = C.c_void_p()
+        L.check(L.load().brx_pool_slot_ptr(self.handle, slot, C.byref(out)))
+        return out.value
+
+    def sync(self) -> None:
+        self._L.check(self._L.load().brx_pool_sync(self.handle))
+
+    def close(self) -> None:
+        if self.handle is not None:
+            self._L.check(self._L.load().brx_pool_destroy(self.handle))
+            self.handle = None
+
+
+class ExpertPool:
+    """C slots of expert weights for ONE layer plus the tables saying which expert is where.
+
+    Bookkeeping restated from stream.py:454-811: `g2s`/`s2g` int32 tables (-1 = absent), a free
+    list popped from the end (so the first admission takes slot C-1), victims from the policy
+    with the current step's experts excluded, else the least recently admitted unprotected
+    slot, and every error raised before a slot is touched.
+    """
+
+    def __init__(self, layer: int, spec: LayerSpec, capacity: int, policy: str = "lfuda",
+                 slots=None, device: int = 0):
+        n_experts = spec.n_experts
+        if not 1 <= capacity <= n_experts:
+            raise ValueError(
+                f"capacity must be in [1, {n_experts}], got {capacity}. A pool larger than the "
+                f"expert count wastes memory; a pool of zero cannot serve any token.")
+        self.layer, self.spec, self.n_experts, self.capacity = layer, spec, n_experts, capacity
+        self.policy = make_policy(policy, capacity, n_experts)
+        try:
+            self._policy_excludes = "exclude" in inspect.signature(self.policy.victim).parameters
+        except (TypeError, ValueError):
+            self._policy_excludes = False
+        self._slot_tick = np.zeros(capacity, dtype=np.int64)
+        self._tick = 0
+        self.g2s = np.full(n_experts, -1, dtype=np.int32)
+        self.s2g = np.full(capacity, -1, dtype=np.int32)
+        self._g2s_dirty = True
+        self._free = list(range(capacity))
+        self._resident = 0
+        self._pending_rank = {}
+        self.hits = 0
+        self.misses = 0
+        self.uses = np.zeros(n_experts, dtype=np.int64)
+        self.admits = 0
+        self.evicts = 0
+        self.admit_seconds = 0.0
+        self.refill_bytes = 0
+        self._slots = slots
+        self._device = device
+        self._built = False
+
+    # -- construction -------------------------------------------------------
+    @property
+    def bytes_per_expert(self) -> int:
+        return self.spec.bytes_per_expert
+
+    def build(self):
+        """Allocate the C slots in HBM (ExpertPool.build, stream.py:570-597)."""
+        if self._slots is None:
+            self._slots = DeviceSlots(self.spec, self.capacity, self._device)
+        self._built = True
+        return self
+
+    @property
+    def device(self):
+        return self._slots
+
+    def nbytes(self) -> int:
+        return self.capacity * self.bytes_per_expert
+
+    # -- residency ----------------------------------------------------------
+    def slot_of(self, e: int) -> int:
+        return int(self.g2s[e])
+
+    def touch(self, experts, ranks=None) -> list:
+        """Record a reference to each expert and return those NOT resident (stream.py:622-642)."""
+        need, nrank = [], []
+        ranks = list(ranks) if ranks is not None else [0] * len(experts)
+        for e, r in zip(experts, ranks):
+            e, r = int(e), int(r)
+            self.uses[e] += 1
+            if self.g2s[e] >= 0:
+                self.hits += 1
+                self.policy.touch(e, r)
+            else:
+                self.misses += 1
+                need.append(e)
+                nrank.append(r)
+        self._pending_rank = dict(zip(need, nrank))
+        return need
+
+    def _victim(self, protect=()) -> int:
+        """Free a slot (stream.py:644-690): the free list first, then the policy's victim
+        outside `protect`, else the least recently admitted unprotected slot."""
+        if self._free:
+            return self._free.pop()
+        protect = {int(x) for x in protect}
+        ev = -1
+        v = (self.policy.victim(exclude=protect) if self._policy_excludes
+             else self.policy.victim())
+        if v is not None and v >= 0 and v not in protect and self.g2s[v] >= 0:
+            ev = int(v)
+        if ev < 0:
+            best, best_t = -1, None
+            for slot in range(self.capacity):
+                g = int(self.s2g[slot])
+                if g < 0 or g in protect:
+                    continue
+                if best_t is None or self._slot_tick[slot] < best_t:
+                    best, best_t = g, self._slot_tick[slot]
+            ev = best
+        if ev < 0:
+            raise RuntimeError(
+                f"layer {self.layer}: every one of {self.capacity} slots holds an expert this "
+                f"step still needs. Capacity must be at least top-k.")
+        slot = int(self.g2s[ev])
+        self.policy.evicted(ev)
+        self.g2s[ev] = -1
+        self.s2g[slot] = -1
+        self._resident -= 1
+        self._g2s_dirty = True
+        self.evicts += 1
+        return slot
+
+    def admit(self, e: int, blob, protect=()) -> int:
+        """Place expert e's packed bytes into a slot and return the slot (stream.py:692-705,
+        757-780). `blob` is a PinnedRegion or any bytes-like object."""
+        if not self._built:
+            raise RuntimeError("build() must run before admit()")
+        want = self.bytes_per_expert
+        if len(blob) != want:
+            raise ValueError(
+                f"layer {self.layer} expert {e}: the manifest accounts for {want} bytes but the "
+                f"region supplied {len(blob)}. Refusing to write a partially-filled slot.")
+        t0 = time.perf_counter()
+        slot = self._victim(protect=protect)
+        self.refill_bytes += self._slots.write(slot, blob)
+        self._place(e, slot, t0)
+        return slot
+
+    def admit_device(self, e: int, dev_ptr: int, protect=()) -> int:
+        """Admit from device memory (an expert staged on the GPU, stream.py:957-961)."""
+        if not self._built:
+            raise RuntimeError("build() must run before admit()")
+        t0 = time.perf_counter()
+        slot = self._victim(protect=protect)
+        self._slots.write_device(slot, dev_ptr, self.bytes_per_expert)
+        self._place(e, slot, t0)
+        return slot
+
+    def _place(self, e: int, slot: int, t0: float) -> None:
+        if self.s2g[slot] < 0:
+            self._resident += 1
+        self.g2s[e] = slot
+        self.s2g[slot] = e
+        self._g2s_dirty = True
+        self._tick += 1
+        self._slot_tick[slot] = self._tick
+        self.policy.admit(e, int(self._pending_rank.get(e, 0)))
+        self.admits += 1
+        self.admit_seconds += time.perf_counter() - t0
+
+    @property
+    def full(self) -> bool:
+        """Every expert resident, so no request can miss (stream.py:782-789). Counted."""
+        return self.capacity == self.n_experts and self._resident == self.n_experts
+
+    def g2s_device(self, stream) -> None:
+        """Upload the table when residency changed (stream.py:791-797); stream-ordered."""
+        if self._g2s_dirty:
+            self._slots.set_table(self.g2s, stream)
+            self._g2s_dirty = False
+
+    def stats(self) -> dict:
+        tot = self.hits + self.misses
+        return {"layer": self.layer, "capacity": self.capacity, "n_experts": self.n_experts,
+                "hits": self.hits, "misses": self.misses,
+                "miss_rate": self.misses / tot if tot else 0.0,
+                "admits": self.admits, "evicts": self.evicts,
+                "resident_bytes": self._resident * self.bytes_per_expert,
+                "refill_bytes": self.refill_bytes, "admit_seconds": self.admit_seconds}
+
+    def close(self) -> None:
+        if self._slots is not None and hasattr(self._slots, "close"):
+            self._slots.close()
+        self._built = False

@@ -1,0 +1,79 @@
+"""One MoE layer's shape, quantization and routing rule, and the C descriptor built from it."""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+from . import formats as F
+
+_ROUTES = {"softmax_topk": 0, "softmax_topk_renorm": 1, "topk_softmax": 2}
+_ACTS = {"swiglu": 0, "swiglu_clamped": 1}
+_RDT = {"float32": 0, "bfloat16": 1}
+
+
+@dataclass(frozen=True)
+class LayerSpec:
+    """A routed-expert layer.
+
+    route: how the block turns logits into (indices, weights) -- the rule adapter.py:75-93
+    records per model: "softmax_topk" (OLMoE: w = softmax(logits)[idx]),
+    "softmax_topk_renorm" (Qwen3 norm_topk_prob: then w /= sum(w)), "topk_softmax"
+    (gpt-oss: w = softmax(logits[idx])).
+    act: "swiglu" = silu(gate) * up; "swiglu_clamped" = gpt-oss's clamped form with
+    alpha/limit.
+    """
+    hidden: int
+    inter: int
+    n_experts: int
+    top_k: int
+    quant: F.QuantSpec = field(default_factory=F.QuantSpec)
+    has_bias: bool = False
+    act: str = "swiglu"
+    alpha: float = 1.702
+    limit: float = 7.0
+    route: str = "softmax_topk_renorm"
+    router_dtype: str = "bfloat16"
+    shared_inter: int = 0
+
+    def __post_init__(self):
+        if self.route not in _ROUTES:
+            raise ValueError(f"route {self.route!r} not in {sorted(_ROUTES)}")
+        if self.act not in _ACTS:
+            raise ValueError(f"act {self.act!r} not in {sorted(_ACTS)}")
+        if self.router_dtype not in _RDT:
+            raise ValueError(f"router_dtype {self.router_dtype!r} not in {sorted(_RDT)}")
+        if not 1 <= self.top_k <= self.n_experts:
+            raise ValueError(f"top_k {self.top_k} outside [1, {self.n_experts}]")
+
+    @property
+    def route_mode(self) -> int:
+        return _ROUTES[self.route]
+
+    def expert_spec(self, shared: bool = False) -> dict:
+        inter = self.shared_inter if shared else self.inter
+        return F.expert_spec(self.hidden, inter, self.quant, self.has_bias)
+
+    @property
+    def bytes_per_expert(self) -> int:
+        return F.spec_bytes(self.expert_spec())
+
+    @property
+    def router_bytes(self) -> int:
+        return self.n_experts * self.hidden * (4 if self.router_dtype == "float32" else 2)
+
+    def desc(self):
+        from .lib import LayerDesc
+        q = self.quant
+        return LayerDesc(self.hidden, self.inter, self.n_experts, self.top_k,
+                         0 if q.mode == "affine" else 1, q.bits, q.group_size,
+                         1 if q.scale_dtype == "float16" else 0, int(self.has_bias),
+                         _ACTS[self.act], self.alpha, self.limit, self.route_mode,
+                         _RDT[self.router_dtype], self.shared_inter, 0)
+
+
+# The synthetic layer shapes the benchmarks and parity tests run (hidden, experts, top-k,
+# intermediate, routing rule, quantization).
+OLMOE_1B_7B = LayerSpec(2048, 1024, 64, 8, route="softmax_topk", router_dtype="float32")
+QWEN3_30B_A3B = LayerSpec(2048, 768, 128, 8, route="softmax_topk_renorm")
+E256_SHARED = LayerSpec(2048, 512, 256, 8, route="softmax_topk_renorm", shared_inter=512)
+GPT_OSS_120B = LayerSpec(2880, 2880, 128, 4, quant=F.QuantSpec(4, 32, "mxfp4"), has_bias=True,
+                         act="swiglu_clamped", route="topk_softmax")

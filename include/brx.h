@@ -1,0 +1,208 @@
+/*
+ * brx.h -- C-ABI of the MI355X (gfx950) routed-expert MoE library, libbrx.so.
+ *
+ * The library replaces the per-layer expert arithmetic and the slot pool behind BigRig's
+ * `StreamingSwitchGLU` (bigrig_engine/stream.py:814-1631) and `ExpertPool`
+ * (bigrig_engine/stream.py:454-811), which the reference runs as MLX ops
+ * (`mx.gather_qmm` stream.py:1623-1625, `mx.quantized_matmul` stream.py:1261-1266,
+ * the router softmax/argpartition the reference restates at stream.py:895 and 1436-1439).
+ *
+ * Conventions
+ *   - Every entry point returns 0 on success or a negative BRX_E* code; brx_last_error()
+ *     returns a message for the last failure on the calling thread. Arguments are validated
+ *     before any device memory is written (the reference validates before touching a slot,
+ *     stream.py:696-703).
+ *   - Device pointers are plain `void*` (from hipMalloc, or torch's data_ptr()); streams are
+ *     `hipStream_t` passed as `void*` (NULL = the null stream). Work is stream-ordered.
+ *   - bf16 tensors are uint16 bit patterns. Shapes are row-major.
+ *   - No entry point is internally thread-safe; use one pool/context per host thread.
+ */
+#ifndef BRX_H
+#define BRX_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define BRX_ABI_VERSION 1
+
+enum {
+    BRX_OK = 0,
+    BRX_EINVAL = -1,   /* bad argument: the reference raises ValueError */
+    BRX_ESTATE = -2,   /* wrong state (not built, freed): RuntimeError */
+    BRX_EHIP = -3,     /* a HIP runtime call failed */
+    BRX_ENOMEM = -4,   /* device or pinned allocation failed */
+    BRX_ERANGE = -5    /* index out of range (expert id, slot): KeyError */
+};
+
+/* quant_mode */
+enum { BRX_QUANT_AFFINE = 0, BRX_QUANT_MXFP4 = 1 };
+/* scale_dtype (affine only) */
+enum { BRX_SCALE_BF16 = 0, BRX_SCALE_F16 = 1 };
+/* act: gated activations of SwitchGLU (stream.py:1164-1166) */
+enum { BRX_ACT_SWIGLU = 0,          /* silu(gate) * up                                   */
+       BRX_ACT_SWIGLU_CLAMPED = 1 }; /* gpt-oss: g=min(g,L); u=clip(u,-L,L);
+                                         g*sigmoid(alpha*g)*(u+1)                          */
+/* route_mode: the router rule of the MoE block (bigrig_engine/adapter.py:75-93) */
+enum { BRX_ROUTE_SOFTMAX_TOPK = 0,        /* p=softmax(logits); w=p[idx] (OLMoE)           */
+       BRX_ROUTE_SOFTMAX_TOPK_RENORM = 1, /* ... then w /= sum(w) (Qwen3 norm_topk_prob)   */
+       BRX_ROUTE_TOPK_SOFTMAX = 2 };      /* w = softmax(logits[idx]) (gpt-oss)            */
+/* router weight dtype */
+enum { BRX_DT_F32 = 0, BRX_DT_BF16 = 1 };
+
+/* One MoE layer's shape and quantization: the manifest's per-layer
+ * {n_experts, spec, quant} record (stream.py:133-151) plus the block's routing rule. */
+typedef struct brx_layer_desc {
+    int32_t hidden;        /* H: model width, input of gate/up, output of down            */
+    int32_t inter;         /* I: expert intermediate width                                  */
+    int32_t n_experts;     /* E                                                             */
+    int32_t top_k;         /* k                                                             */
+    int32_t quant_mode;    /* BRX_QUANT_*                                                   */
+    int32_t bits;          /* 4 (affine kernels support 4 bits)                             */
+    int32_t group_size;    /* 64 (affine) or 32 (mxfp4)                                     */
+    int32_t scale_dtype;   /* BRX_SCALE_* (affine)                                          */
+    int32_t has_bias;      /* projections carry a `bias` [N] bf16 component (gpt-oss)       */
+    int32_t act;           /* BRX_ACT_*                                                     */
+    float   alpha;         /* clamped SwiGLU alpha (1.702)                                  */
+    float   limit;         /* clamped SwiGLU limit (7.0)                                    */
+    int32_t route_mode;    /* BRX_ROUTE_*                                                   */
+    int32_t router_dtype;  /* BRX_DT_*: dtype of the router weight [E, H]                   */
+    int32_t shared_inter;  /* intermediate width of an always-on shared expert, 0 = none    */
+    int32_t reserved;
+} brx_layer_desc;
+
+/* Byte offsets of one expert's components inside its packed region, in the order
+ * pack_experts writes them (projections gate/up/down, components weight/scales/biases/bias,
+ * stream.py:152-164). -1 marks an absent component. */
+typedef struct brx_expert_layout {
+    int64_t weight[3];
+    int64_t scales[3];
+    int64_t biases[3];
+    int64_t bias[3];
+    int64_t bytes_per_expert;
+} brx_expert_layout;
+
+typedef struct brx_pool brx_pool;
+
+/* ---------------------------------------------------------------- library */
+int brx_abi_version(void);
+const char* brx_last_error(void);
+/* Select the device every later call uses and check it is gfx950. */
+int brx_init(int device);
+
+/* Layout of one routed expert (inter = desc->inter) or of the shared expert
+ * (shared != 0: inter = desc->shared_inter). Replaces the manifest arithmetic of
+ * stream.py:133-141 and ExpertPool.bytes_per_expert (stream.py:539-541). */
+int brx_expert_layout_get(const brx_layer_desc* d, int shared, brx_expert_layout* out);
+
+/* ---------------------------------------------------------------- pool
+ * C expert slots for ONE layer in HBM plus a device expert->slot table, the residency
+ * structure of ExpertPool (stream.py:454-811). The host keeps the authoritative tables and
+ * the eviction policy (ExpertPool.touch/_victim/admit, stream.py:622-780); the device only
+ * holds bytes and the table kernels read. */
+
+/* Allocate `capacity` slots of bytes_per_expert each (ExpertPool.build, stream.py:570-597).
+ * 1 <= capacity <= n_experts (stream.py:503-506). The table starts all zero. */
+int brx_pool_create(const brx_layer_desc* d, int capacity, brx_pool** out);
+/* Free the slots (StreamHandle.close, stream.py:2160-2191). Synchronizes the pool's streams. */
+int brx_pool_destroy(brx_pool* p);
+int brx_pool_capacity(const brx_pool* p);
+/* Device address of slot `slot` (the expert's bytes, blob layout). */
+int brx_pool_slot_ptr(brx_pool* p, int slot, void** out);
+/* Device address of the int32 expert->slot table [n_experts] kernels read. */
+int brx_pool_g2s_ptr(brx_pool* p, int32_t** out);
+
+/* Copy one expert's packed bytes from pinned host memory into slot `slot`, asynchronously on
+ * `copy_stream`. The copy first waits for every forward already issued that reads this pool
+ * (write-after-read on the slot), and records an event the next forward waits on
+ * (read-after-write). nbytes must equal bytes_per_expert (stream.py:696-703).
+ * Replaces the slot write of admit_arrays (stream.py:765-769). */
+int brx_pool_refill_async(brx_pool* p, int slot, const void* host_src, size_t nbytes,
+                          void* copy_stream);
+/* Same, from device memory (a staged expert, stream.py:957-961). */
+int brx_pool_refill_from_device_async(brx_pool* p, int slot, const void* dev_src, size_t nbytes,
+                                      void* copy_stream);
+/* Upload the host expert->slot table (int32 [n_experts], -1 = absent, uploaded as max(g2s,0)
+ * like ExpertPool.g2s_device, stream.py:791-797), ordered on `stream` and after any refill. */
+int brx_pool_set_g2s(brx_pool* p, const int32_t* g2s_host, int n, void* stream);
+/* Block until every copy and forward issued against the pool has finished. */
+int brx_pool_sync(brx_pool* p);
+
+/* ---------------------------------------------------------------- compute */
+
+/* Router top-k for T tokens: logits = x . W_r^T (+ bias), then the layer's routing rule.
+ *   x        [T, H] bf16 (device)
+ *   w_router [E, H] fp32 or bf16 per d->router_dtype (device)
+ *   bias     [E] fp32 or NULL: added to the logits (router bias, synthetic Zipf bias)
+ *   shared_gate_w [H] bf16 or NULL: shared-expert gate row; out_shared_gate[t] =
+ *            sigmoid(x_t . w) when given
+ *   out_idx  [T, k] int32: experts by descending logit, ties to the lower id
+ *   out_w    [T, k] fp32: routing weights in the same order
+ * Logits use one fixed fp32 reduction order so indices are reproducible bit for bit.
+ * Replaces the block's gate + softmax + argpartition + take (+ renorm) (stream.py:1436-1439;
+ * adapter.py:75-93). */
+int brx_router_topk(const brx_layer_desc* d, const void* x, const void* w_router,
+                    const float* bias, const void* shared_gate_w, int T,
+                    int32_t* out_idx, float* out_w, float* out_shared_gate, void* stream);
+
+/* flags for brx_moe_forward */
+#define BRX_FWD_FORCE_DECODE  1u  /* take the gather-GEMV path (at most 8 token rows, 64 pairs) */
+#define BRX_FWD_FORCE_PREFILL 2u  /* take the grouped-GEMM path whatever T is              */
+
+/* The routed experts of one MoE layer for T tokens, reading expert bytes from the pool's
+ * slots through its device table (slot = g2s[expert]):
+ *   y[t, j]   = down(act(gate(x_t), up(x_t)))  for expert idx[t, j]       (bf16)
+ *   out[t]    = sum_j w[t, j] * y[t, j]  (+ shared_gate[t] * shared(x_t)) (fp32 sum, bf16)
+ * x [T, H] bf16; idx [T, k] int32; w [T, k] fp32; out [T, H] bf16 or NULL;
+ * y_unreduced [T, k, H] bf16 or NULL (the unreduced rows StreamingSwitchGLU returns,
+ * stream.py:1377-1577); shared_expert: device pointer to the shared expert's packed bytes
+ * (layout brx_expert_layout_get(shared=1)) or NULL; shared_gate [T] fp32 or NULL.
+ * T <= 8 (or FORCE_DECODE) runs the decode gather-GEMV kernels, larger T the prefill
+ * grouped GEMM on MFMA (the reference's per-row `gather_qmm` vs sorted `gather_qmm`,
+ * stream.py:1128-1172, 1320-1336). The library keeps a grown-on-demand workspace. */
+int brx_moe_forward(const brx_layer_desc* d, brx_pool* p, const void* x, const int32_t* idx,
+                    const float* w, const void* shared_expert, const float* shared_gate, int T,
+                    void* out, void* y_unreduced, unsigned flags, void* stream);
+
+/* The expert rows of an explicit list of (token, expert) pairs, unreduced:
+ *   y_rows[pair_row[i]] = down(act(gate(x[pair_token[i]]), up(x[pair_token[i]])))
+ * for expert pair_expert[i], read through the pool's table; expert id n_experts names the
+ * shared expert (`shared_expert`, required then). y_rows has n_rows rows; pair_row may be NULL
+ * (row i, n_rows >= n_pairs); when given, its entries are distinct rows in [0, n_rows)
+ * (entries outside are clamped). This is the span form of the reference's
+ * expert-sorted prefill, StreamingSwitchGLU._forward_pairs (stream.py:1320-1336), used when one
+ * chunk routes to more experts than the pool holds: the caller cuts the pairs into spans of
+ * at most `capacity` experts (_pair_chunks, stream.py:1098-1126), makes each span resident and
+ * calls this once per span, writing straight to the unsorted positions (stream.py:1558-1561).
+ * x [T, H] bf16. Pass the same FORCE flag for every span of one chunk so a row's arithmetic
+ * does not depend on how the chunk was cut (without a flag: decode kernels for n_pairs <= 8). */
+int brx_moe_forward_pairs(const brx_layer_desc* d, brx_pool* p, const void* x, int T,
+                          const int32_t* pair_token, const int32_t* pair_expert,
+                          const int32_t* pair_row, int n_pairs, int n_rows,
+                          const void* shared_expert, void* y_rows, unsigned flags, void* stream);
+
+/* The caller's router-weighted combine of unreduced rows (stream.py:1523-1525):
+ *   out[t] = bf16( sum_j w[t, j] * y_routed[t, j]  (+ shared_gate[t] * y_shared[t]) )
+ * in fp32, j in order. y_routed [T, k, H] bf16, w [T, k] fp32, y_shared [T, H] bf16 or NULL. */
+int brx_combine(const brx_layer_desc* d, const void* y_routed, const float* w, const void* y_shared,
+                const float* shared_gate, int T, void* out, void* stream);
+
+/* Test hook: fp32 dequantized weight of projection `proj` (0 gate, 1 up, 2 down) of the
+ * expert whose packed bytes start at `expert` (device): out [n_out, n_in] fp32.
+ * Replaces mx.dequantize (bigrig_engine/precision.py:186-189). */
+int brx_dequant(const brx_layer_desc* d, const void* expert, int proj, int shared, float* out,
+                void* stream);
+
+/* Test hook: stable bucketing of T*k (token, expert) pairs by expert, as the reference's
+ * np.argsort(pe, kind="stable") (stream.py:1526-1530): out_order [T*k] int32 pair ids sorted
+ * by expert, out_offsets [E+1] int32 start of each expert's run. */
+int brx_sort_pairs(const brx_layer_desc* d, const int32_t* idx, int T, int32_t* out_order,
+                   int32_t* out_offsets, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* BRX_H */

@@ -1,0 +1,134 @@
+"""GPU parity of libbrx's kernels against the oracle (all calls go through the C-ABI).
+
+Bars: dequantized weights bit-exact in fp32; routing indices bit-exact; routing weights to
+1e-5 relative; layer outputs (fp32 accumulate, bf16 out) within 1e-2 relative L2 of the
+oracle, which is the tolerance the layer is specified to. The float64 truth is checked too, so
+the kernels and the C oracle cannot agree by being wrong the same way.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from bigrig_amd import formats as F
+from bigrig_amd import layer as ops
+from bigrig_amd.spec import E256_SHARED, GPT_OSS_120B, OLMOE_1B_7B, QWEN3_30B_A3B, LayerSpec
+from tests.gpu_util import bits, build_gpu_layer, bytes_dev, to_dev_bits
+from tests.helpers import make_layer, make_x, small
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-2
+
+SMALL_AFFINE = small(QWEN3_30B_A3B, hidden=512, inter=256, n_experts=32, top_k=8)
+SMALL_F16 = small(OLMOE_1B_7B, hidden=512, inter=384, n_experts=16, top_k=4,
+                  quant=F.QuantSpec(4, 64, "affine", "float16"))
+SMALL_MXFP4 = small(GPT_OSS_120B, hidden=576, inter=320, n_experts=16, top_k=4)
+SMALL_SHARED = small(E256_SHARED, hidden=512, inter=256, n_experts=64, top_k=8,
+                     shared_inter=256)
+
+
+@pytest.mark.parametrize("spec", [SMALL_AFFINE, SMALL_F16, SMALL_MXFP4], ids=["bf16", "f16", "mxfp4"])
+def test_dequant_bit_exact(gpu, spec):
+    lay = make_layer(spec, seed=3)
+    for e in (0, spec.n_experts - 1):
+        dev = bytes_dev(lay.experts[e], gpu)
+        for p in range(3):
+            got = ops.dequant(spec, dev, p).cpu().numpy()
+            want = oracle.dequant(spec, lay.experts[e], p)
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (e, p)
+
+
+@pytest.mark.parametrize("spec", [OLMOE_1B_7B, QWEN3_30B_A3B, E256_SHARED, GPT_OSS_120B],
+                         ids=["olmoe", "qwen3", "e256", "gptoss"])
+@pytest.mark.parametrize("T", [1, 8, 65, 300])
+def test_router_bit_exact(gpu, spec, T):
+    rng = np.random.default_rng(T)
+    wr = rng.standard_normal((spec.n_experts, spec.hidden), dtype=np.float32) * 0.02
+    w = wr if spec.router_dtype == "float32" else F.f32_to_bf16_bits(wr)
+    bias = (rng.standard_normal(spec.n_experts).astype(np.float32) if spec.n_experts != 64 else None)
+    sgw = F.f32_to_bf16_bits(rng.standard_normal(spec.hidden, dtype=np.float32) * 0.02) \
+        if spec.shared_inter else None
+    x = make_x(T, spec.hidden, seed=T + 5)
+    idx, wt, sg = ops.router_topk(spec, to_dev_bits(x, gpu), to_dev_bits(w, gpu),
+                                  None if bias is None else to_dev_bits(bias, gpu),
+                                  None if sgw is None else to_dev_bits(sgw, gpu))
+    _, oidx, ow, osg = oracle.router(x, w, spec.router_dtype == "float32", bias, spec.top_k,
+                                     spec.route_mode, sgw)
+    assert np.array_equal(idx.cpu().numpy(), oidx)
+    np.testing.assert_allclose(wt.cpu().numpy(), ow, rtol=1e-5, atol=1e-7)
+    if sgw is not None:
+        np.testing.assert_allclose(sg.cpu().numpy(), osg, rtol=1e-5, atol=1e-7)
+
+
+def _layer_check(lay, moe, T, seed, check_f64=True):
+    import torch
+    spec = lay.spec
+    x = make_x(T, spec.hidden, seed=seed)
+    xd = to_dev_bits(x, moe.router_w.device)
+    out = moe(xd)
+    torch.cuda.synchronize()
+    _, idx, w, sg = oracle.router(x, lay.router, spec.router_dtype == "float32", lay.bias,
+                                  spec.top_k, spec.route_mode, lay.sgate_w)
+    ref, _ = oracle.moe_forward(spec, lay.experts, x, idx, w, lay.shared, sg)
+    got = F.bf16_bits_to_f32(bits(out))
+    r = oracle.rel_l2(got, F.bf16_bits_to_f32(ref))
+    assert r < TOL, f"rel L2 vs C oracle {r:.3e}"
+    if check_f64:
+        truth, _ = oracle.moe_forward_f64(spec, lay.experts, x, idx, w, lay.shared, sg)
+        r64 = oracle.rel_l2(got, truth)
+        assert r64 < TOL, f"rel L2 vs float64 truth {r64:.3e}"
+    return r
+
+
+@pytest.mark.parametrize("spec", [SMALL_AFFINE, SMALL_F16, SMALL_MXFP4, SMALL_SHARED],
+                         ids=["bf16", "f16", "mxfp4", "shared"])
+@pytest.mark.parametrize("T", [1, 3, 8])
+def test_decode_layer(gpu, spec, T):
+    lay = make_layer(spec, seed=11)
+    moe, sw, pool, _ = build_gpu_layer(lay, gpu)
+    assert sw._sync_free
+    _layer_check(lay, moe, T, seed=100 + T)
+    pool.close()
+
+
+@pytest.mark.parametrize("spec", [SMALL_AFFINE, SMALL_F16, SMALL_MXFP4, SMALL_SHARED],
+                         ids=["bf16", "f16", "mxfp4", "shared"])
+@pytest.mark.parametrize("T", [9, 64, 257])
+def test_prefill_layer(gpu, spec, T):
+    lay = make_layer(spec, seed=12, zipf=1.1)
+    moe, sw, pool, _ = build_gpu_layer(lay, gpu)
+    _layer_check(lay, moe, T, seed=200 + T, check_f64=T < 100)
+    pool.close()
+
+
+@pytest.mark.parametrize("T", [1, 16])
+def test_unreduced_rows(gpu, T):
+    """The operator's unreduced [T, k, H] rows (the reference boundary) against the oracle."""
+    import torch
+    spec = SMALL_AFFINE
+    lay = make_layer(spec, seed=21)
+    moe, sw, pool, _ = build_gpu_layer(lay, gpu)
+    x = make_x(T, spec.hidden, seed=31)
+    _, idx, w, _ = oracle.router(x, lay.router, False, None, spec.top_k, spec.route_mode)
+    y = sw(to_dev_bits(x, gpu), torch.from_numpy(idx).to(gpu))
+    torch.cuda.synchronize()
+    _, yref = oracle.moe_forward(spec, lay.experts, x, idx, w, want_unreduced=True)
+    got = F.bf16_bits_to_f32(bits(y))
+    ref = F.bf16_bits_to_f32(yref)
+    assert got.shape == ref.shape == (T, spec.top_k, spec.hidden)
+    for t in range(T):
+        for j in range(spec.top_k):
+            assert oracle.rel_l2(got[t, j], ref[t, j]) < TOL, (t, j)
+    pool.close()
+
+
+def test_sort_pairs_matches_stable_argsort(gpu):
+    import torch
+    spec = SMALL_AFFINE
+    rng = np.random.default_rng(4)
+    idx = rng.integers(0, spec.n_experts, size=(333, spec.top_k)).astype(np.int32)
+    order, offsets = ops.sort_pairs(spec, torch.from_numpy(idx).to(gpu))
+    o_ref, off_ref = oracle.sort_pairs(idx, spec.n_experts)
+    assert np.array_equal(order.cpu().numpy(), o_ref)
+    assert np.array_equal(offsets.cpu().numpy(), off_ref)
+    assert np.array_equal(o_ref, np.argsort(idx.reshape(-1), kind="stable"))
