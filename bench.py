@@ -1,0 +1,480 @@
+#!/usr/bin/env python3
+"""MoE-layer throughput on one MI355X: batch-1 decode and 2048-token prefill, with roofline.
+
+Workload (synthetic, seeded; random-init weights of the named architecture):
+  a Qwen3-30B-A3B-shaped routed-expert stack, 48 MoE layers: hidden 2048, 128 experts, softmax
+  top-8 renormalised, expert intermediate 768, SwiGLU, MLX affine 4-bit g64 bf16 scale/bias.
+  Expert weights N(0, 0.02) per (layer, expert, projection), quantized on the GPU; router
+  weights N(0, 0.02) bf16 plus a per-layer Zipf(s=1.1) logit bias; layer inputs N(0, 1) bf16.
+
+One step = one decode token through all 48 layers (router top-k, gate/up + SwiGLU, down +
+router-weighted combine), every expert resident in HBM (the pool's sync-free path), the step
+replayed as a HIP graph. `value` = decode tokens/s of the stack.
+
+Also reported on the same line:
+  roofline      the dominant kernel (decode gate/up) timed with HIP events on its stream:
+                algorithmic bytes per launch / average launch duration vs 8 TB/s
+  prefill       one 2048-token chunk through the 48 layers (bucketing + grouped MFMA GEMMs),
+                tokens/s and the gate/up GEMM's TFLOP/s vs 2.5 PFLOP/s dense bf16
+  bounded_pool  the same decode with 32 of 128 experts per layer resident, misses refilled
+                from pinned host memory over PCIe, one routing read-back per layer (end to end)
+  cpu_baseline  the C restatement (oracle/) on the host cores, on a bounded sample
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "MoE-layer tokens/s at batch 1 and 2048-token prefill; % of HBM/MFMA roofline"
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200, help="timed decode steps")
+    ap.add_argument("--warmup", type=int, default=20, help="untimed decode steps")
+    ap.add_argument("--layers", type=int, default=48)
+    ap.add_argument("--prefill-tokens", type=int, default=2048)
+    ap.add_argument("--prefill-steps", type=int, default=5)
+    ap.add_argument("--pool-capacity", type=int, default=32)
+    ap.add_argument("--pool-tokens", type=int, default=64)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--skip", default="", help="comma list of: prefill,pool,cpu,graph")
+    return ap.parse_args()
+
+
+class Stack:
+    """48 layers of pools, router weights, Zipf biases and input banks on the GPU."""
+
+    def __init__(self, spec, layers: int, bank: int, keep_host_layers: int = 0):
+        import torch
+
+        from bigrig_amd import synth
+        from bigrig_amd.pool import ExpertPool, HostStore
+        self.spec = spec
+        self.layers = layers
+        self.pools, self.routers, self.biases, self.xbank = [], [], [], []
+        self.host = HostStore()
+        t0 = time.time()
+        for l in range(layers):
+            experts = synth.make_layer_experts(spec, seed=1000 + l)
+            pool = ExpertPool(l, spec, spec.n_experts).build()
+            for e in range(spec.n_experts):
+                pool.touch([e], [0])
+                pool.admit_device(e, experts[e].data_ptr())
+            pool.device.sync()
+            if l < keep_host_layers:
+                h = torch.empty(experts.shape, dtype=torch.uint8, pin_memory=True)
+                h.copy_(experts)
+                self.host.add_layer_tensor(l, h)
+            del experts
+            self.pools.append(pool)
+            self.routers.append(synth.router_weights(spec, seed=2000 + l))
+            self.biases.append(synth.zipf_bias_torch(spec.n_experts, 1.1, seed=3000 + l))
+            self.xbank.append(synth.activations(bank, spec.hidden, seed=4000 + l))
+        torch.cuda.synchronize()
+        for p in self.pools:
+            p.g2s_device(torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        log(f"built {layers} layers x {spec.n_experts} experts "
+            f"({layers * spec.n_experts * spec.bytes_per_expert / 1e9:.1f} GB) in {time.time() - t0:.1f}s")
+
+
+def decode_bench(args, st: "Stack"):
+    import torch
+
+    from bigrig_amd import lib as L
+    from bigrig_amd.layer import moe_forward, router_topk
+    spec, Ln = st.spec, st.layers
+    G = st.xbank[0].shape[0]
+    dev = st.xbank[0].device
+    k, H = spec.top_k, spec.hidden
+    idx = [torch.empty((1, k), dtype=torch.int32, device=dev) for _ in range(Ln)]
+    wts = [torch.empty((1, k), dtype=torch.float32, device=dev) for _ in range(Ln)]
+    outs = [torch.empty((1, H), dtype=torch.bfloat16, device=dev) for _ in range(Ln)]
+    lib = L.load()
+    d = spec.desc()
+    import ctypes as C
+    dref = C.byref(d)
+
+    def step(g: int, stream: int, phases: int = 0):
+        for l in range(Ln):
+            x = st.xbank[l][g:g + 1]
+            if phases == 0:
+                L.check(lib.brx_router_topk(dref, x.data_ptr(), st.routers[l].data_ptr(),
+                                            st.biases[l].data_ptr(), None, 1, idx[l].data_ptr(),
+                                            wts[l].data_ptr(), None, stream))
+            L.check(lib.brx_moe_forward(dref, st.pools[l].device.handle, x.data_ptr(),
+                                        idx[l].data_ptr(), wts[l].data_ptr(), None, None, 1,
+                                        outs[l].data_ptr(), None,
+                                        L.FWD_FORCE_DECODE | phases, stream))
+
+    s = torch.cuda.current_stream()
+    sp = s.cuda_stream
+    for g in range(G):
+        step(g, sp)
+    torch.cuda.synchronize()
+
+    use_graph = "graph" not in args.skip
+    graphs = []
+    if use_graph:
+        try:
+            for g in range(G):
+                cg = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(cg):
+                    step(g, torch.cuda.current_stream().cuda_stream)
+                graphs.append(cg)
+            torch.cuda.synchronize()
+        except Exception as ex:   # capture unsupported: fall back to eager launches
+            log(f"graph capture failed ({ex}); timing eager launches")
+            graphs = []
+            torch.cuda.synchronize()
+
+    def run(i):
+        if graphs:
+            graphs[i % G].replay()
+        else:
+            step(i % G, sp)
+
+    for i in range(args.warmup):
+        run(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        run(i)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    tok_s = args.steps / dt
+    # eager (no graph) rate for reference
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    ne = max(10, args.steps // 5)
+    for i in range(ne):
+        step(i % G, sp)
+    torch.cuda.synchronize()
+    eager_tok_s = ne / (time.perf_counter() - t1)
+
+    # per-kernel timing with HIP events on the launch stream: gate/up (phase A) and down
+    # (phase B) of every layer, routing already computed by the steps above
+    ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
+    reps = 20
+    ta = tb = 0.0
+    for r in range(reps):
+        g = r % G
+        for l in range(Ln):       # routing of token g at every layer
+            x = st.xbank[l][g:g + 1]
+            L.check(lib.brx_router_topk(dref, x.data_ptr(), st.routers[l].data_ptr(),
+                                        st.biases[l].data_ptr(), None, 1, idx[l].data_ptr(),
+                                        wts[l].data_ptr(), None, sp))
+        e0, e1, e2 = ev(), ev(), ev()
+        e0.record(s)
+        for l in range(Ln):
+            x = st.xbank[l][g:g + 1]
+            L.check(lib.brx_moe_forward(dref, st.pools[l].device.handle, x.data_ptr(),
+                                        idx[l].data_ptr(), wts[l].data_ptr(), None, None, 1,
+                                        outs[l].data_ptr(), None,
+                                        L.FWD_FORCE_DECODE | L.FWD_PHASE_A, sp))
+        e1.record(s)
+        for l in range(Ln):
+            x = st.xbank[l][g:g + 1]
+            L.check(lib.brx_moe_forward(dref, st.pools[l].device.handle, x.data_ptr(),
+                                        idx[l].data_ptr(), wts[l].data_ptr(), None, None, 1,
+                                        outs[l].data_ptr(), None,
+                                        L.FWD_FORCE_DECODE | L.FWD_PHASE_A, sp))
+            L.check(lib.brx_moe_forward(dref, st.pools[l].device.handle, x.data_ptr(),
+                                        idx[l].data_ptr(), wts[l].data_ptr(), None, None, 1,
+                                        outs[l].data_ptr(), None,
+                                        L.FWD_FORCE_DECODE | L.FWD_PHASE_B, sp))
+        e2.record(s)
+        torch.cuda.synchronize()
+        ta += e0.elapsed_time(e1)
+        tb += e1.elapsed_time(e2)
+    gateup_ms = ta / reps / Ln
+    down_ms = tb / reps / Ln - gateup_ms
+    spec_e = spec.expert_spec()
+    gu = sum(c["nbytes"] for p in ("gate_proj", "up_proj") for c in spec_e[p].values())
+    dn = sum(c["nbytes"] for c in spec_e["down_proj"].values())
+    gu_bytes = k * gu + 2 * H
+    dn_bytes = k * dn + 2 * H + 2 * k * spec.inter
+    layer_bytes = k * spec.bytes_per_expert + spec.router_bytes + 2 * H * 2
+    return {
+        "tok_s": tok_s, "ms_per_step": dt / args.steps * 1e3, "graph": bool(graphs),
+        "eager_tok_s": eager_tok_s,
+        "gateup_us": gateup_ms * 1e3, "down_us": down_ms * 1e3,
+        "gateup_bytes": gu_bytes, "down_bytes": dn_bytes, "layer_bytes": layer_bytes,
+        "gateup_gbs": gu_bytes / (gateup_ms * 1e-3) / 1e9,
+        "down_gbs": dn_bytes / (down_ms * 1e-3) / 1e9 if down_ms > 0 else None,
+        "step_gbs": layer_bytes * Ln * tok_s / 1e9,
+    }
+
+
+def prefill_bench(args, st: "Stack"):
+    import ctypes as C
+
+    import torch
+
+    from bigrig_amd import lib as L
+    from bigrig_amd import synth
+    spec, Ln = st.spec, st.layers
+    T, k, H = args.prefill_tokens, spec.top_k, spec.hidden
+    dev = st.xbank[0].device
+    xs = [synth.activations(T, H, seed=5000 + l) for l in range(Ln)]
+    idx = [torch.empty((T, k), dtype=torch.int32, device=dev) for _ in range(Ln)]
+    wts = [torch.empty((T, k), dtype=torch.float32, device=dev) for _ in range(Ln)]
+    out = torch.empty((T, H), dtype=torch.bfloat16, device=dev)
+    lib = L.load()
+    d = spec.desc()
+    dref = C.byref(d)
+    s = torch.cuda.current_stream()
+    sp = s.cuda_stream
+
+    def route(l):
+        L.check(lib.brx_router_topk(dref, xs[l].data_ptr(), st.routers[l].data_ptr(),
+                                    st.biases[l].data_ptr(), None, T, idx[l].data_ptr(),
+                                    wts[l].data_ptr(), None, sp))
+
+    def fwd(l, phases=0):
+        L.check(lib.brx_moe_forward(dref, st.pools[l].device.handle, xs[l].data_ptr(),
+                                    idx[l].data_ptr(), wts[l].data_ptr(), None, None, T,
+                                    out.data_ptr(), None, L.FWD_FORCE_PREFILL | phases, sp))
+
+    def chunk():
+        for l in range(Ln):
+            route(l)
+            fwd(l)
+
+    chunk()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.prefill_steps):
+        chunk()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / args.prefill_steps
+    ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
+    e0, e1, e2, e3 = ev(), ev(), ev(), ev()
+    e0.record(s)
+    for l in range(Ln):
+        route(l)
+    e1.record(s)
+    for l in range(Ln):
+        fwd(l, L.FWD_PHASE_A)
+    e2.record(s)
+    for l in range(Ln):
+        fwd(l, L.FWD_PHASE_A)
+        fwd(l, L.FWD_PHASE_B)
+    e3.record(s)
+    torch.cuda.synchronize()
+    router_ms = e0.elapsed_time(e1) / Ln
+    gateup_ms = e1.elapsed_time(e2) / Ln
+    down_ms = e2.elapsed_time(e3) / Ln - gateup_ms
+    gu_flop = 2.0 * T * k * 2 * spec.inter * H
+    dn_flop = 2.0 * T * k * spec.inter * H
+    # routing spread: distinct experts hit by the chunk, and the busiest expert's share
+    counts = torch.bincount(idx[0].reshape(-1).long(), minlength=spec.n_experts).cpu()
+    return {
+        "tok_s": T / dt, "ms_per_chunk": dt * 1e3, "layers": Ln, "tokens": T,
+        "router_us": router_ms * 1e3, "gateup_us": gateup_ms * 1e3, "down_us": down_ms * 1e3,
+        "gateup_tflops": gu_flop / (gateup_ms * 1e-3) / 1e12,
+        "down_tflops": dn_flop / (down_ms * 1e-3) / 1e12 if down_ms > 0 else None,
+        "layer_tflops": (gu_flop + dn_flop) / (dt / Ln) / 1e12,
+        "max_expert_rows": int(counts.max()), "experts_hit": int((counts > 0).sum()),
+    }
+
+
+def pool_bench(args, st: "Stack"):
+    """Bounded pool end to end: C of E experts per layer resident, misses copied from pinned
+    host memory, one routing read-back per layer. PCIe-inclusive; never the headline value."""
+    import torch
+
+    from bigrig_amd.layer import MoELayer, StreamingSwitchGLU
+    from bigrig_amd.pool import ExpertPool, PinnedFetcher
+    spec = st.spec
+    layers = st.host.layers()
+    fetcher = PinnedFetcher(st.host)
+    mods = []
+    for l in layers:
+        pool = ExpertPool(l, spec, args.pool_capacity).build()
+        sw = StreamingSwitchGLU(pool, fetcher)
+        sw.refresh()
+        mods.append(MoELayer(spec, st.routers[l], sw, router_bias=st.biases[l]))
+    G = st.xbank[0].shape[0]
+
+    def token(i):
+        for l, m in zip(layers, mods):
+            m(st.xbank[l][i % G:i % G + 1])
+
+    for i in range(8):            # fill the pools
+        token(i)
+    torch.cuda.synchronize()
+    for m in mods:
+        p = m.switch._pool
+        p.hits = p.misses = 0
+    t0 = time.perf_counter()
+    n = args.pool_tokens
+    for i in range(n):
+        token(8 + i)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    hits = sum(m.switch._pool.hits for m in mods)
+    miss = sum(m.switch._pool.misses for m in mods)
+    res = {"capacity": args.pool_capacity, "layers": len(layers),
+           "tok_s_layers": n / dt,
+           "tok_s_48": n / dt * len(layers) / 48.0,
+           "miss_rate": miss / max(1, hits + miss),
+           "pcie_inclusive": True}
+    for m in mods:
+        m.switch._pool.close()
+    return res
+
+
+def cpu_bench(args, st: "Stack"):
+    """The oracle's C restatement (OpenMP) on a bounded sample: decode tokens through two
+    layers until cpu_seconds of work, scaled to the 48-layer stack."""
+    import numpy as np
+    import torch
+
+    import oracle
+    spec = st.spec
+    oracle.build(force=False)
+    nlay = 2
+    experts, routers, biases = [], [], []
+    for l in range(nlay):
+        blob = st.host.tensor(l).numpy()
+        experts.append([blob[e].tobytes() for e in range(spec.n_experts)])
+        routers.append(st.routers[l].view(torch.int16).cpu().numpy().view(np.uint16))
+        biases.append(st.biases[l].cpu().numpy())
+    xs = [st.xbank[l].view(torch.int16).cpu().numpy().view(np.uint16) for l in range(nlay)]
+    G = xs[0].shape[0]
+    n, t0 = 0, time.perf_counter()
+    while True:
+        for l in range(nlay):
+            x = xs[l][n % G:n % G + 1]
+            _, idx, w, _ = oracle.router(x, routers[l], False, biases[l], spec.top_k,
+                                         spec.route_mode)
+            oracle.moe_forward(spec, experts[l], x, idx, w)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= args.cpu_seconds:
+            break
+    per_layer_tok = el / (n * nlay)
+    return {"value": 1.0 / (per_layer_tok * 48), "unit": "tokens/s", "cores": oracle.num_threads(),
+            "kind": "port",
+            "sample": f"{n} decode tokens x {nlay} layers of the same stack (router + 8 experts + "
+                      f"combine per layer-token, OpenMP over (token, expert) rows), "
+                      f"{el:.1f}s, scaled to 48 layers"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (got --gpus "
+              f"{args.gpus}). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    from bigrig_amd import lib as L
+    from bigrig_amd.spec import QWEN3_30B_A3B
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU (no CPU fallback)", file=sys.stderr)
+        sys.exit(1)
+    L.init(0)
+    spec = QWEN3_30B_A3B
+    skip = set(filter(None, args.skip.split(",")))
+    keep = 0 if "pool" in skip else args.layers
+    if "cpu" not in skip:
+        keep = max(keep, 2)
+    st = Stack(spec, args.layers, bank=8, keep_host_layers=keep)
+    log("decode")
+    dec = decode_bench(args, st)
+    pre = None
+    if "prefill" not in skip:
+        log("prefill")
+        pre = prefill_bench(args, st)
+    pool = None
+    if "pool" not in skip:
+        log("bounded pool")
+        pool = pool_bench(args, st)
+    cpu = None
+    if "cpu" not in skip:
+        log("cpu baseline")
+        cpu = cpu_bench(args, st)
+    traffic = None
+    tp = os.path.join(ROOT, "profiles", "traffic_decode_gateup.json")
+    if os.path.exists(tp):
+        try:
+            traffic = json.load(open(tp)).get("traffic_bytes")
+        except (OSError, ValueError):
+            traffic = None
+    rec = {
+        "metric": METRIC,
+        "value": round(dec["tok_s"], 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dec["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": f"qwen3-30b-a3b-shape MoE stack, {args.layers} layers, decode batch 1: "
+                        f"hidden 2048, 128 experts, softmax top-8 renorm, inter 768, SwiGLU, "
+                        f"MLX affine 4-bit g64 bf16 scale/bias, all experts HBM-resident, "
+                        f"Zipf(1.1) router bias, HIP-graph replay" if dec["graph"] else
+                        f"qwen3-30b-a3b-shape MoE stack, {args.layers} layers, decode batch 1 "
+                        f"(eager launches)",
+            "layers": args.layers, "batch": 1, "experts": 128, "top_k": 8,
+            "weights": "4-bit affine g64", "layer_gb_per_token": round(dec["layer_bytes"] / 1e9, 5),
+        },
+        "roofline": {
+            "bound": "hbm", "achieved": round(dec["gateup_gbs"], 1), "peak": HBM_PEAK_GBS,
+            "unit": "GB/s", "frac": round(dec["gateup_gbs"] / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+            "kernel": "k_dec_gateup (8 experts x gate+up, 14.16 MB/launch)",
+            "avg_us": round(dec["gateup_us"], 3),
+        },
+        "decode_kernels": {
+            "gateup_us": round(dec["gateup_us"], 3), "down_us": round(dec["down_us"], 3),
+            "gateup_gbs": round(dec["gateup_gbs"], 1),
+            "down_gbs": None if dec["down_gbs"] is None else round(dec["down_gbs"], 1),
+            "stack_gbs": round(dec["step_gbs"], 1),
+            "stack_frac": round(dec["step_gbs"] / HBM_PEAK_GBS, 4),
+            "eager_tok_s": round(dec["eager_tok_s"], 1),
+        },
+        "cpu_baseline": cpu,
+    }
+    if pre is not None:
+        rec["prefill"] = {
+            "tokens": pre["tokens"], "layers": pre["layers"], "tok_s": round(pre["tok_s"], 1),
+            "ms_per_chunk": round(pre["ms_per_chunk"], 3),
+            "router_us": round(pre["router_us"], 2), "gateup_us": round(pre["gateup_us"], 2),
+            "down_us": round(pre["down_us"], 2),
+            "roofline": {"bound": "mfma", "achieved": round(pre["gateup_tflops"], 1),
+                         "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(pre["gateup_tflops"] / BF16_PEAK_TFLOPS, 4),
+                         "kernel": "k_pf_gateup (+ bucketing)"},
+            "layer_tflops": round(pre["layer_tflops"], 1),
+            "max_expert_rows": pre["max_expert_rows"], "experts_hit": pre["experts_hit"],
+        }
+    if pool is not None:
+        rec["bounded_pool"] = {k2: (round(v, 4) if isinstance(v, float) else v)
+                               for k2, v in pool.items()}
+    print(json.dumps(rec), flush=True)
+
+
+if __name__ == "__main__":
+    main()

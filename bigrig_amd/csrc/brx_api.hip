@@ -113,6 +113,7 @@ struct brx_pool {
     hipEvent_t refill_done;
     hipEvent_t g2s_uploaded;
     bool read_recorded;
+    bool refill_recorded;
     bool refill_pending;
     bool g2s_recorded;
 };
@@ -223,6 +224,7 @@ static int refill(brx_pool* p, int slot, const void* src, size_t nbytes, void* c
     HIP_TRY(hipMemcpyAsync(p->slots + (int64_t)slot * p->stride, src, nbytes, kind, cs));
     HIP_TRY(hipEventRecord(p->refill_done, cs));
     p->refill_pending = true;
+    p->refill_recorded = true;
     return BRX_OK;
 }
 
@@ -253,7 +255,7 @@ int brx_pool_set_g2s(brx_pool* p, const int32_t* g2s_host, int n, void* stream) 
 
 int brx_pool_sync(brx_pool* p) {
     if (!p) return fail(BRX_EINVAL, "pool is NULL");
-    if (p->refill_pending) HIP_TRY(hipEventSynchronize(p->refill_done));
+    if (p->refill_recorded) HIP_TRY(hipEventSynchronize(p->refill_done));
     if (p->read_recorded) HIP_TRY(hipEventSynchronize(p->last_read));
     if (p->g2s_recorded) HIP_TRY(hipEventSynchronize(p->g2s_uploaded));
     return BRX_OK;
@@ -317,8 +319,15 @@ static int forward_impl(const brx_layer_desc* d, brx_pool* p, const void* x, int
     void* ws = nullptr;
     int rc = ws_reserve(need, s, &ws);
     if (rc) return rc;
-    if (p->refill_pending) HIP_TRY(hipStreamWaitEvent(s, p->refill_done, 0));
-    hipError_t e = decode ? launch_decode(a, (uint16_t*)ws, s) : launch_prefill(a, ws, g_ws.bytes, s);
+    if (p->refill_pending) {
+        // forwards of one pool are issued on one stream: once it has waited, later ones follow
+        HIP_TRY(hipStreamWaitEvent(s, p->refill_done, 0));
+        p->refill_pending = false;
+    }
+    int phases = (flags & (BRX_FWD_PHASE_A | BRX_FWD_PHASE_B)) >> 2;
+    if (phases == 0) phases = 3;
+    hipError_t e = decode ? launch_decode(a, (uint16_t*)ws, phases, s)
+                          : launch_prefill(a, ws, g_ws.bytes, phases, s);
     if (e != hipSuccess) return hip_fail(e, decode ? "decode launch" : "prefill launch");
     HIP_TRY(hipEventRecord(p->last_read, s));
     p->read_recorded = true;

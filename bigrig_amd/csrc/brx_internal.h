@@ -157,8 +157,9 @@ __device__ __forceinline__ void perm8(const uint32_t in[4], uint32_t out[4]) {
 hipError_t launch_router(const brx_layer_desc& d, const void* x, const void* w_router,
                          const float* bias, const void* sgw, int T, int32_t* out_idx,
                          float* out_w, float* out_sg, hipStream_t s);
-hipError_t launch_decode(const FwdArgs& a, uint16_t* hbuf, hipStream_t s);
-hipError_t launch_prefill(const FwdArgs& a, void* ws, size_t ws_bytes, hipStream_t s);
+// phases: bit 0 = first half (gate/up), bit 1 = second half (down + combine)
+hipError_t launch_decode(const FwdArgs& a, uint16_t* hbuf, int phases, hipStream_t s);
+hipError_t launch_prefill(const FwdArgs& a, void* ws, size_t ws_bytes, int phases, hipStream_t s);
 size_t prefill_workspace_bytes(const FwdArgs& a);
 size_t decode_workspace_bytes(const FwdArgs& a);
 hipError_t launch_dequant(const brx_layer_desc& d, const Layout& L, const uint8_t* expert,

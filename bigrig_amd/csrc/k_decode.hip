@@ -324,14 +324,14 @@ int pick_cps(int cpr) {
 }
 
 template <int MODE>
-hipError_t launch_mode(const FwdArgs& a, uint16_t* hbuf, hipStream_t s) {
+hipError_t launch_mode(const FwdArgs& a, uint16_t* hbuf, int phases, hipStream_t s) {
     const int P = a.P;
     const int PT = P + (a.auto_shared ? a.T : 0);
     const int nu = P + (a.auto_shared ? 1 : 0);
     const int Imax = a.I > a.I_sh ? a.I : a.I_sh;
     const int hstride = Imax;
     // gate/up
-    {
+    if (phases & 1) {
         const int CPR = a.H / 32;
         const int cps = pick_cps(CPR);
         const int S = CPR / cps;
@@ -356,7 +356,7 @@ hipError_t launch_mode(const FwdArgs& a, uint16_t* hbuf, hipStream_t s) {
         if (err != hipSuccess) return err;
     }
     // down + combine
-    {
+    if (phases & 2) {
         const int CPR = a.I / 32;
         const int cps = pick_cps(CPR);
         const int S = CPR / cps;
@@ -373,6 +373,7 @@ hipError_t launch_mode(const FwdArgs& a, uint16_t* hbuf, hipStream_t s) {
         }
         return hipGetLastError();
     }
+    return hipSuccess;
 }
 
 }  // namespace
@@ -383,9 +384,9 @@ size_t decode_workspace_bytes(const FwdArgs& a) {
     return (size_t)PT * Imax * 2;
 }
 
-hipError_t launch_decode(const FwdArgs& a, uint16_t* hbuf, hipStream_t s) {
-    return a.quant_mode == BRX_QUANT_AFFINE ? launch_mode<BRX_QUANT_AFFINE>(a, hbuf, s)
-                                            : launch_mode<BRX_QUANT_MXFP4>(a, hbuf, s);
+hipError_t launch_decode(const FwdArgs& a, uint16_t* hbuf, int phases, hipStream_t s) {
+    return a.quant_mode == BRX_QUANT_AFFINE ? launch_mode<BRX_QUANT_AFFINE>(a, hbuf, phases, s)
+                                            : launch_mode<BRX_QUANT_MXFP4>(a, hbuf, phases, s);
 }
 
 }  // namespace brx

@@ -420,7 +420,7 @@ hipError_t launch_combine(const uint16_t* y_routed, const uint16_t* y_shared, co
     return hipGetLastError();
 }
 
-hipError_t launch_prefill(const FwdArgs& a, void* ws, size_t ws_bytes, hipStream_t s) {
+hipError_t launch_prefill(const FwdArgs& a, void* ws, size_t ws_bytes, int phases, hipStream_t s) {
     PfWs w = carve(a, ws);
     if (w.bytes > ws_bytes) return hipErrorInvalidValue;
     const int P = a.P;
@@ -428,26 +428,34 @@ hipError_t launch_prefill(const FwdArgs& a, void* ws, size_t ws_bytes, hipStream
     const int P_ext = P + T_sh;
     const int E_ext = a.E + (a.shared ? 1 : 0);
     const int Imax = a.I > a.I_sh ? a.I : a.I_sh;
-    hipError_t err = launch_sort_pairs(a.pexp, P, a.E, E_ext, T_sh, kBM, w.order, w.offsets, w.tile_start, s);
-    if (err != hipSuccess) return err;
     const int mt_max = (P_ext + kBM - 1) / kBM + E_ext;
     uint16_t* y_routed = a.yun ? a.yun : w.y_routed;
-    if (a.quant_mode == BRX_QUANT_AFFINE) {
-        hipLaunchKernelGGL(k_pf_gateup<BRX_QUANT_AFFINE>, dim3(mt_max, Imax / 64), dim3(kThreads), 0, s,
-                           a, w.order, w.offsets, w.tile_start, w.hbuf, Imax);
-        hipLaunchKernelGGL(k_pf_down<BRX_QUANT_AFFINE>, dim3(mt_max, (a.H + 127) / 128), dim3(kThreads), 0, s,
-                           a, w.order, w.offsets, w.tile_start, w.hbuf, Imax, y_routed, w.y_shared);
-    } else {
-        hipLaunchKernelGGL(k_pf_gateup<BRX_QUANT_MXFP4>, dim3(mt_max, Imax / 64), dim3(kThreads), 0, s,
-                           a, w.order, w.offsets, w.tile_start, w.hbuf, Imax);
-        hipLaunchKernelGGL(k_pf_down<BRX_QUANT_MXFP4>, dim3(mt_max, (a.H + 127) / 128), dim3(kThreads), 0, s,
-                           a, w.order, w.offsets, w.tile_start, w.hbuf, Imax, y_routed, w.y_shared);
+    hipError_t err = hipSuccess;
+    if (phases & 1) {
+        err = launch_sort_pairs(a.pexp, P, a.E, E_ext, T_sh, kBM, w.order, w.offsets, w.tile_start, s);
+        if (err != hipSuccess) return err;
+        if (a.quant_mode == BRX_QUANT_AFFINE)
+            hipLaunchKernelGGL(k_pf_gateup<BRX_QUANT_AFFINE>, dim3(mt_max, Imax / 64), dim3(kThreads), 0, s,
+                               a, w.order, w.offsets, w.tile_start, w.hbuf, Imax);
+        else
+            hipLaunchKernelGGL(k_pf_gateup<BRX_QUANT_MXFP4>, dim3(mt_max, Imax / 64), dim3(kThreads), 0, s,
+                               a, w.order, w.offsets, w.tile_start, w.hbuf, Imax);
+        err = hipGetLastError();
+        if (err != hipSuccess) return err;
     }
-    err = hipGetLastError();
-    if (err != hipSuccess) return err;
-    if (a.out)
-        err = launch_combine(y_routed, a.auto_shared ? w.y_shared : nullptr, a.w, a.sgate, a.T, a.k,
-                             a.H, a.out, s);
+    if (phases & 2) {
+        if (a.quant_mode == BRX_QUANT_AFFINE)
+            hipLaunchKernelGGL(k_pf_down<BRX_QUANT_AFFINE>, dim3(mt_max, (a.H + 127) / 128), dim3(kThreads), 0, s,
+                               a, w.order, w.offsets, w.tile_start, w.hbuf, Imax, y_routed, w.y_shared);
+        else
+            hipLaunchKernelGGL(k_pf_down<BRX_QUANT_MXFP4>, dim3(mt_max, (a.H + 127) / 128), dim3(kThreads), 0, s,
+                               a, w.order, w.offsets, w.tile_start, w.hbuf, Imax, y_routed, w.y_shared);
+        err = hipGetLastError();
+        if (err != hipSuccess) return err;
+        if (a.out)
+            err = launch_combine(y_routed, a.auto_shared ? w.y_shared : nullptr, a.w, a.sgate, a.T, a.k,
+                                 a.H, a.out, s);
+    }
     return err;
 }
 

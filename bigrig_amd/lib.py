@@ -18,7 +18,7 @@ SCALE_BF16, SCALE_F16 = 0, 1
 ACT_SWIGLU, ACT_SWIGLU_CLAMPED = 0, 1
 ROUTE_SOFTMAX_TOPK, ROUTE_SOFTMAX_TOPK_RENORM, ROUTE_TOPK_SOFTMAX = 0, 1, 2
 DT_F32, DT_BF16 = 0, 1
-FWD_FORCE_DECODE, FWD_FORCE_PREFILL = 1, 2
+FWD_FORCE_DECODE, FWD_FORCE_PREFILL, FWD_PHASE_A, FWD_PHASE_B = 1, 2, 4, 8
 
 EXPORTS = (
     "brx_abi_version", "brx_last_error", "brx_init", "brx_expert_layout_get",

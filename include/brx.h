@@ -151,6 +151,12 @@ int brx_router_topk(const brx_layer_desc* d, const void* x, const void* w_router
 /* flags for brx_moe_forward */
 #define BRX_FWD_FORCE_DECODE  1u  /* take the gather-GEMV path (at most 8 token rows, 64 pairs) */
 #define BRX_FWD_FORCE_PREFILL 2u  /* take the grouped-GEMM path whatever T is              */
+/* Split launch: run only the first half (gate/up + act; for the grouped GEMM also the
+ * bucketing) or only the second half (down + combine) of a forward. The halves share the
+ * library workspace, so a PHASE_B call must follow the PHASE_A call of the same forward with
+ * nothing else using the library in between. Both bits or neither = the whole forward. */
+#define BRX_FWD_PHASE_A       4u
+#define BRX_FWD_PHASE_B       8u
 
 /* The routed experts of one MoE layer for T tokens, reading expert bytes from the pool's
  * slots through its device table (slot = g2s[expert]):
