@@ -15,6 +15,11 @@ namespace {
 
 thread_local std::string g_err;
 int g_device = -1;
+// Device-scope counters some kernels use to let their last block finish the launch's work
+// (zeroed once here; every kernel that takes one leaves it at zero when it ends).
+unsigned* g_counters = nullptr;
+constexpr int kCounters = 16;
+enum { kCounterRouter = 0 };
 
 struct Workspace {
     void* ptr = nullptr;
@@ -133,6 +138,11 @@ int brx_init(int device) {
     HIP_TRY(hipGetDeviceProperties(&prop, device));
     if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
         return fail(BRX_EINVAL, "device %d is %s; libbrx is built for gfx950 only", device, prop.gcnArchName);
+    if (!g_counters) {
+        HIP_TRY(hipMalloc(&g_counters, sizeof(unsigned) * kCounters));
+        HIP_TRY(hipMemset(g_counters, 0, sizeof(unsigned) * kCounters));
+        HIP_TRY(hipDeviceSynchronize());
+    }
     g_device = device;
     return BRX_OK;
 }
@@ -273,8 +283,11 @@ int brx_router_topk(const brx_layer_desc* d, const void* x, const void* w_router
     if (((uintptr_t)x | (uintptr_t)w_router) & 15) return fail(BRX_EINVAL, "x and w_router must be 16-byte aligned");
     if (shared_gate_w && ((uintptr_t)shared_gate_w & 15)) return fail(BRX_EINVAL, "shared_gate_w must be 16-byte aligned");
     if (shared_gate_w && !out_shared_gate) return fail(BRX_EINVAL, "shared_gate_w given without out_shared_gate");
+    void* ws = nullptr;
+    size_t need = router_workspace_bytes(*d, T);
+    if (need && (rc = ws_reserve(need, (hipStream_t)stream, &ws))) return rc;
     hipError_t e = launch_router(*d, x, w_router, bias, shared_gate_w, T, out_idx, out_w, out_shared_gate,
-                                 (hipStream_t)stream);
+                                 (float*)ws, g_counters + kCounterRouter, (hipStream_t)stream);
     if (e != hipSuccess) return hip_fail(e, "router launch");
     return BRX_OK;
 }
@@ -326,7 +339,7 @@ static int forward_impl(const brx_layer_desc* d, brx_pool* p, const void* x, int
     }
     int phases = (flags & (BRX_FWD_PHASE_A | BRX_FWD_PHASE_B)) >> 2;
     if (phases == 0) phases = 3;
-    hipError_t e = decode ? launch_decode(a, (uint16_t*)ws, phases, s)
+    hipError_t e = decode ? launch_decode(a, ws, phases, s)
                           : launch_prefill(a, ws, g_ws.bytes, phases, s);
     if (e != hipSuccess) return hip_fail(e, decode ? "decode launch" : "prefill launch");
     HIP_TRY(hipEventRecord(p->last_read, s));

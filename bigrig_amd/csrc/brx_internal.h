@@ -156,9 +156,11 @@ __device__ __forceinline__ void perm8(const uint32_t in[4], uint32_t out[4]) {
 // ------------------------------------------------------------------ launchers
 hipError_t launch_router(const brx_layer_desc& d, const void* x, const void* w_router,
                          const float* bias, const void* sgw, int T, int32_t* out_idx,
-                         float* out_w, float* out_sg, hipStream_t s);
+                         float* out_w, float* out_sg, float* ws_logits, unsigned* counter,
+                         hipStream_t s);
+size_t router_workspace_bytes(const brx_layer_desc& d, int T);
 // phases: bit 0 = first half (gate/up), bit 1 = second half (down + combine)
-hipError_t launch_decode(const FwdArgs& a, uint16_t* hbuf, int phases, hipStream_t s);
+hipError_t launch_decode(const FwdArgs& a, void* ws, int phases, hipStream_t s);
 hipError_t launch_prefill(const FwdArgs& a, void* ws, size_t ws_bytes, int phases, hipStream_t s);
 size_t prefill_workspace_bytes(const FwdArgs& a);
 size_t decode_workspace_bytes(const FwdArgs& a);

@@ -6,17 +6,27 @@
 // router-weighted combine (stream.py:1523-1525).
 //
 // Two kernels per layer:
-//   k_dec_gateup  grid (row block, unique expert): gate and up rows of one expert for every
-//                 token routed to it, act() in the epilogue, h -> bf16 workspace.
-//   k_dec_down    grid (row block of H): down rows of every routed expert, the row's bf16
-//                 result, and the k-ordered combine out[t] = sum_j w[t,j] * y[t,j].
-// Weights stream from HBM once per step as 16-byte loads: each thread owns CPS consecutive
-// 16-byte chunks (32 nibbles each) of one row, so a wave covers whole rows contiguously.
-// Dequant is folded into the dot product: for a 32-element chunk with scale s and bias b,
+//   k_dec_gateup  grid (row block, expert entry): gate and up rows of one expert for every
+//                 token routed to it, act() in the epilogue, h -> bf16 workspace; its blocks of
+//                 row block 0 also record the entry table the down kernel reads.
+//   k_dec_down    grid (row block of H): down rows of every entry, each pair's bf16 row result,
+//                 and the k-ordered combine out[t] = sum_j w[t,j] * y[t,j].
+// An entry is a run of at most 8 pairs routed to one expert (so an expert is read once for all
+// the step's tokens that chose it), in order of first appearance; the shared expert, when the
+// layer has one, is the last entry and takes every token.
+//
+// A row of K inputs is CPR = K/32 chunks of 16 bytes (32 nibbles); SP consecutive lanes own one
+// row, lane `seg` the 4 consecutive chunks [4 seg, 4 seg + 4). Each wave derives its entry
+// itself (ballots and lane reads, no LDS and no barrier), then issues every weight, scale and
+// activation load before it waits on any of them, and the SP lane partials of a row are summed
+// by an in-wave xor butterfly: a launch costs the routing read, one slot-table read and one
+// round trip for the weights. Dequant is folded into the dot product: for a chunk with scale s
+// and bias b,
 //   sum_i (s q_i + b) x_i = s * sum_i (128 + q_i) x_i + (b - 128 s) * sum_i x_i,
-// where (128 + q_i) is formed as an exact bf16 by bit operations and the products are
-// accumulated in fp32 by v_dot2_f32_bf16. Row partials are combined in a fixed order, so a
-// row's result does not depend on which other rows or tokens share the launch.
+// where (128 + q_i) is formed as an exact bf16 by bit operations and the products accumulate
+// in fp32 through v_dot2_f32_bf16. For MXFP4 the hardware converts two e2m1 codes to a bf16
+// pair and the e8m0 scale multiplies the chunk sum. A row's value does not depend on which
+// other rows or tokens share the launch.
 #include "brx_internal.h"
 
 namespace brx {
@@ -25,284 +35,395 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kMaxTok = 8;
 constexpr int kMaxU = 65;     // 64 routed pairs + the shared expert
+constexpr int kCPS = 4;       // chunks per lane segment
 
-struct Plan {
-    int n;                    // number of unique experts (shared last)
-    int e[kMaxU];
-    int ntok[kMaxU];
-    int pair[kMaxU][kMaxTok]; // pair index: t*k + j, or P + t for the shared expert
-    int tok[kMaxU][kMaxTok];
+struct DecEntry {
+    int32_t slot;             // pool slot, or -1 for the shared expert
+    int32_t nt;
+    int32_t pair[kMaxTok];    // pair index: p, or P + t for the shared expert
 };
 
-// Experts of the step in order of first appearance over the pairs, then the shared expert.
-// Run by wave 0.
-__device__ void build_plan(const FwdArgs& a, Plan& pl) {
+struct DecTable {
+    int32_t n;
+    int32_t pad[3];
+    DecEntry ent[kMaxU];
+};
+
+// One entry as a wave sees it: its expert, slot, token count and the pairs it covers (a lane
+// mask over the pairs; the shared entry covers pairs P + t for every token t instead).
+struct Entry {
+    int e, slot, nt;
+    bool shared;
+    uint64_t mm;
+};
+
+__device__ __forceinline__ int rl(int v, int lane) { return __builtin_amdgcn_readlane(v, lane); }
+
+// Entry u of the step, computed by the calling wave (all results wave-uniform).
+// Returns false when u is past the last entry.
+__device__ __forceinline__ bool plan_entry(const FwdArgs& a, int u, Entry& en, int& n_out) {
     const int lane = threadIdx.x & 63;
     const int P = a.P;
     const int emax = a.shared ? a.E : a.E - 1;   // id E names the shared expert
-    int e = -1;
-    if (lane < P) e = min(max(a.pexp[lane], 0), emax);
-    // An entry is a run of up to kMaxTok pairs of one expert: a pair leads an entry when the
-    // number of earlier pairs routed to the same expert is a multiple of kMaxTok.
+    // the slot table rides along with the routing read: lane l holds g2s[l + 64 j]
+    constexpr int kG = 8;                        // E <= 512
+    int gt[kG];
+#pragma unroll
+    for (int j = 0; j < kG; ++j) {
+        const int ge = lane + kWave * j;
+        gt[j] = ge < a.E ? a.g2s[ge] : 0;
+    }
+    const int e = lane < P ? min(max(a.pexp[lane], 0), emax) : -1;
     int occ = 0;
-    for (int q = 0; q < P; ++q) {
-        int eq = __shfl(e, q, kWave);
-        if (q < lane && eq == e) ++occ;
-    }
+    for (int q = 0; q < P; ++q) occ += (q < lane && rl(e, q) == e) ? 1 : 0;
     const bool lead = lane < P && (occ % kMaxTok) == 0;
-    uint64_t mask = __ballot(lead);
-    int rank = __popcll(mask & ((1ull << lane) - 1ull));
-    int cnt = 0;
-    for (int q = 0; q < P; ++q) {        // uniform loop: every lane takes part in the shuffle
-        int eq = __shfl(e, q, kWave);
-        if (lead && q >= lane && eq == e && cnt < kMaxTok) {
-            pl.pair[rank][cnt] = q;
-            pl.tok[rank][cnt] = pair_tok(a, q);
-            ++cnt;
+    const uint64_t mask = __ballot(lead);
+    const int nr = __popcll(mask);
+    const int n = nr + (a.auto_shared ? 1 : 0);
+    n_out = n;
+    if (u >= n) return false;
+    if (u < nr) {
+        uint64_t m = mask;
+        for (int i = 0; i < u; ++i) m &= m - 1;
+        const int pu = __builtin_ctzll(m);
+        const int eu = rl(e, pu), occ0 = rl(occ, pu);
+        const bool member = lane < P && e == eu && occ >= occ0 && occ < occ0 + kMaxTok;
+        en.mm = __ballot(member);
+        en.e = eu;
+        en.nt = __popcll(en.mm);
+        en.shared = false;
+        int s = -1;
+        if (eu < a.E) {
+            const int gj = eu >> 6;
+            int gv = gt[0];
+#pragma unroll
+            for (int j = 1; j < kG; ++j) if (j == gj) gv = gt[j];
+            s = min(max(rl(gv, eu & 63), 0), a.capacity - 1);
         }
+        en.slot = s;
+    } else {
+        en.e = a.E;
+        en.nt = a.T;
+        en.slot = -1;
+        en.shared = true;
+        en.mm = 0;
     }
-    if (lead) {
-        pl.e[rank] = e;
-        pl.ntok[rank] = cnt;
-    }
-    int nr = __popcll(mask);
-    if (lane == 0) {
-        if (a.auto_shared) {
-            pl.e[nr] = a.E;
-            pl.ntok[nr] = a.T;
-            for (int t = 0; t < a.T; ++t) { pl.pair[nr][t] = P + t; pl.tok[nr][t] = t; }
-            pl.n = nr + 1;
+    return true;
+}
+
+// Walks an entry's pairs in order: next() returns the pair index, tok the token it reads.
+struct PairIter {
+    uint64_t rem;
+    int i;
+    __device__ __forceinline__ int next(const FwdArgs& a, const Entry& en, int& tok) {
+        int q;
+        if (en.shared) {
+            q = a.P + i;
+            tok = i;
         } else {
-            pl.n = nr;
+            q = __builtin_ctzll(rem);
+            rem &= rem - 1;
+            tok = pair_tok(a, q);
+        }
+        ++i;
+        return q;
+    }
+};
+
+__device__ __forceinline__ const uint8_t* slot_base(const FwdArgs& a, int slot) {
+    return slot >= 0 ? a.slots + (int64_t)slot * a.slot_stride : a.shared;
+}
+
+struct Seg {
+    uint4 w[kCPS];
+    float s[kCPS];   // scale per chunk
+    float b[kCPS];   // affine: bias - 128 * scale per chunk; mxfp4: unused
+};
+
+// Issue the loads of one row segment (no waiting). Chunks past the row are clamped to its last
+// chunk (loaded and then ignored), so no load sits behind a branch.
+template <int MODE>
+__device__ __forceinline__ void seg_load(const uint8_t* base, const Proj& P, int row, int c0,
+                                         int scale_f16, Seg& sg) {
+    const int n_in = P.n_in;
+    const int cpr = n_in / 32;
+    const uint4* wrow = reinterpret_cast<const uint4*>(base + P.w + (int64_t)row * (n_in / 2));
+#pragma unroll
+    for (int j = 0; j < kCPS; ++j) sg.w[j] = wrow[min(c0 + j, cpr - 1)];
+    if constexpr (MODE == BRX_QUANT_AFFINE) {
+        const int G = n_in / 64;
+        const uint16_t* sp = reinterpret_cast<const uint16_t*>(base + P.s) + (int64_t)row * G;
+        const uint16_t* bp = reinterpret_cast<const uint16_t*>(base + P.b) + (int64_t)row * G;
+        uint32_t sv[kCPS / 2], bv[kCPS / 2];
+#pragma unroll
+        for (int j = 0; j < kCPS / 2; ++j) {
+            const int g = min((c0 >> 1) + j, G - 1);
+            sv[j] = sp[g];
+            bv[j] = bp[g];
+        }
+#pragma unroll
+        for (int j = 0; j < kCPS; ++j) {
+            float s = scale_f16 ? h2f(sv[j >> 1]) : bf2f(sv[j >> 1]);
+            float b = scale_f16 ? h2f(bv[j >> 1]) : bf2f(bv[j >> 1]);
+            sg.s[j] = s;
+            sg.b[j] = b - 128.0f * s;
+        }
+    } else {
+        const int G = n_in / 32;
+        const uint8_t* sp = base + P.s + (int64_t)row * G;
+#pragma unroll
+        for (int j = 0; j < kCPS; ++j) {
+            sg.s[j] = e8m0_f32(sp[min(c0 + j, G - 1)]);
+            sg.b[j] = 0.0f;
         }
     }
 }
 
-__device__ __forceinline__ const uint8_t* expert_base(const FwdArgs& a, int e) {
-    if (e >= a.E) return a.shared;
-    int s = a.g2s[e];
-    s = min(max(s, 0), a.capacity - 1);
-    return a.slots + (int64_t)s * a.slot_stride;
-}
+// One chunk of activations as the dot needs it.
+struct XChunk {
+    uint32_t w[16];   // affine: pair-permuted (x_i, x_{i+4}) per 8; mxfp4: natural (x_2i, x_2i+1)
+    float sum;        // affine: sum of the 32 values
+};
 
-// Partial of one row segment: CPS chunks of 32 elements against `nt` activation vectors.
-// xp(i, c) -> pointer to 16 words (pair-permuted) of vector i at chunk c; xs(i, c) -> chunk sum.
-template <int MODE, int CPS, typename XP, typename XS>
-__device__ __forceinline__ void seg_partials(const uint8_t* wrow, const uint8_t* srow,
-                                             const uint8_t* brow, int c0, int gs, int scale_f16,
-                                             int nt, XP xp, XS xs, float* out) {
-    uint4 wv[CPS];
+// From natural-order memory (x): permute for the affine dot, sum the chunk.
+template <int MODE>
+__device__ __forceinline__ void x_prepare(const uint4 raw[4], XChunk& xc) {
+    if constexpr (MODE == BRX_QUANT_AFFINE) {
+        float s = 0.f;
 #pragma unroll
-    for (int j = 0; j < CPS; ++j) wv[j] = reinterpret_cast<const uint4*>(wrow)[c0 + j];
-    float sc[CPS], bi[CPS];
+        for (int q = 0; q < 4; ++q) {
+            uint32_t in[4] = {raw[q].x, raw[q].y, raw[q].z, raw[q].w}, o[4];
+            perm8(in, o);
 #pragma unroll
-    for (int j = 0; j < CPS; ++j) {
-        int g = ((c0 + j) * 32) / gs;
-        if constexpr (MODE == BRX_QUANT_AFFINE) {
-            sc[j] = load_scale(srow, g, scale_f16);
-            bi[j] = load_scale(brow, g, scale_f16) - 128.0f * sc[j];
-        } else {
-            sc[j] = e8m0_f32(srow[g]);
-            bi[j] = 0.0f;
-        }
-    }
-    for (int i = 0; i < nt; ++i) {
-        float p = 0.0f;
-#pragma unroll
-        for (int j = 0; j < CPS; ++j) {
-            const uint32_t* x16 = xp(i, c0 + j);
-            uint32_t wd[4] = {wv[j].x, wv[j].y, wv[j].z, wv[j].w};
-            float acc = 0.0f;
-            if constexpr (MODE == BRX_QUANT_AFFINE) {
-#pragma unroll
-                for (int q = 0; q < 4; ++q) acc = dot8_q4(wd[q], x16 + 4 * q, acc);
-                p = fmaf(sc[j], acc, fmaf(bi[j], xs(i, c0 + j), p));
-            } else {
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-#pragma unroll
-                    for (int b = 0; b < 4; ++b) {
-                        uint32_t xw = x16[4 * q + b];
-                        acc = fmaf(e2m1_f32((wd[q] >> (4 * b)) & 0xFu), bf2f(xw & 0xFFFFu), acc);
-                        acc = fmaf(e2m1_f32((wd[q] >> (4 * b + 16)) & 0xFu), bf2f(xw >> 16), acc);
-                    }
-                }
-                p = fmaf(sc[j], acc, p);
+            for (int z = 0; z < 4; ++z) {
+                xc.w[4 * q + z] = o[z];
+                s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, in[z]),
+                                                    __builtin_bit_cast(bf16x2_t, 0x3F803F80u), s,
+                                                    false);
             }
         }
-        out[i] = p;
+        xc.sum = s;
+    } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            xc.w[4 * q + 0] = raw[q].x;
+            xc.w[4 * q + 1] = raw[q].y;
+            xc.w[4 * q + 2] = raw[q].z;
+            xc.w[4 * q + 3] = raw[q].w;
+        }
+        xc.sum = 0.f;
+    }
+}
+
+// From the h buffer, which is stored in the order the dot needs (see h_pos).
+template <int MODE>
+__device__ __forceinline__ void h_prepare(const uint4 raw[4], XChunk& xc) {
+    float s = 0.f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        uint32_t in[4] = {raw[q].x, raw[q].y, raw[q].z, raw[q].w};
+#pragma unroll
+        for (int z = 0; z < 4; ++z) {
+            xc.w[4 * q + z] = in[z];
+            if constexpr (MODE == BRX_QUANT_AFFINE)
+                s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, in[z]),
+                                                    __builtin_bit_cast(bf16x2_t, 0x3F803F80u), s,
+                                                    false);
+        }
+    }
+    xc.sum = s;
+}
+
+// Dot of chunk j of a loaded segment with a prepared activation chunk.
+template <int MODE>
+__device__ __forceinline__ float chunk_dot(const Seg& sg, int j, const XChunk& xc) {
+    uint32_t wd[4] = {sg.w[j].x, sg.w[j].y, sg.w[j].z, sg.w[j].w};
+    float acc = 0.0f;
+    if constexpr (MODE == BRX_QUANT_AFFINE) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) acc = dot8_q4(wd[q], xc.w + 4 * q, acc);
+        return fmaf(sg.s[j], acc, sg.b[j] * xc.sum);
+    } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint32_t v = wd[q];
+            acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(v, 1.0f, 0),
+                                                  __builtin_bit_cast(bf16x2_t, xc.w[4 * q + 0]), acc, false);
+            acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(v, 1.0f, 1),
+                                                  __builtin_bit_cast(bf16x2_t, xc.w[4 * q + 1]), acc, false);
+            acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(v, 1.0f, 2),
+                                                  __builtin_bit_cast(bf16x2_t, xc.w[4 * q + 2]), acc, false);
+            acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(v, 1.0f, 3),
+                                                  __builtin_bit_cast(bf16x2_t, xc.w[4 * q + 3]), acc, false);
+        }
+        return sg.s[j] * acc;
+    }
+}
+
+template <int SP>
+__device__ __forceinline__ float seg_reduce(float v) {
+#pragma unroll
+    for (int off = SP / 2; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+}
+
+// Position of element r of a row in the stored h layout: pair-permuted within 8 for the
+// affine down projection, natural for MXFP4.
+template <int MODE>
+__device__ __forceinline__ int h_pos(int r) {
+    if constexpr (MODE == BRX_QUANT_AFFINE) {
+        const int m = r & ~7, i = r & 7;
+        return m + (i < 4 ? 2 * i : 2 * (i - 4) + 1);
+    } else {
+        return r;
     }
 }
 
 // ------------------------------------------------------------------ gate/up
-template <int MODE, int CPS>
+// Thread t owns row (t / SP) of the block's RB = 256 / SP rows and segment (t % SP), for both
+// the gate and the up projection.
+template <int MODE, int SP>
 __global__ __launch_bounds__(kThreads) void k_dec_gateup(FwdArgs a, uint16_t* __restrict__ hbuf,
-                                                         int RB, int hstride) {
-    __shared__ Plan pl;
-    extern __shared__ uint32_t dsm[];
+                                                         int hstride, DecTable* __restrict__ table) {
+    constexpr int RB = kThreads / SP;
+    Entry en;
+    int n;
+    if (!plan_entry(a, blockIdx.y, en, n)) return;
     const int tid = threadIdx.x;
-    if (tid < kWave) build_plan(a, pl);
-    __syncthreads();
-    const int u = blockIdx.y;
-    if (u >= pl.n) return;
-    const int e = pl.e[u];
-    const bool sh = e >= a.E;
+    if (blockIdx.x == 0 && tid == 0) {        // the entry table for the down kernel
+        DecEntry& d = table->ent[blockIdx.y];
+        d.slot = en.slot;
+        d.nt = en.nt;
+        PairIter it{en.mm, 0};
+        for (int i = 0; i < en.nt; ++i) {
+            int tok;
+            d.pair[i] = it.next(a, en, tok);
+        }
+        if (blockIdx.y == 0) table->n = n;
+    }
+    const bool sh = en.e >= a.E;
     const int inter = sh ? a.I_sh : a.I;
     const int r0 = blockIdx.x * RB;
     if (r0 >= inter) return;
     const Layout& L = sh ? a.lay_sh : a.lay;
-    const uint8_t* base = expert_base(a, e);
-    const int nt = pl.ntok[u];
-    const int H = a.H, CPR = H / 32, S = CPR / CPS;
+    const uint8_t* base = slot_base(a, en.slot);
+    const int H = a.H, CPR = H / 32;
+    const int rr = tid / SP, seg = tid % SP;
+    const int row = min(r0 + rr, inter - 1);
+    const int c0 = seg * kCPS;
+    const int nvalid = min(kCPS, CPR - c0);     // <= 0 for padding lanes
 
-    uint32_t* xperm = dsm;                                   // [nt][H/2] words
-    float* xsum = reinterpret_cast<float*>(xperm + nt * (H / 2));  // [nt][CPR]
-    float* part = xsum + nt * CPR;                           // [nt][2][RB][S]
-
-    // stage the tokens' activations, pair-permuted, with chunk sums
-    for (int it = tid; it < nt * CPR; it += kThreads) {
-        int i = it / CPR, c = it - i * CPR;
-        const uint4* src = reinterpret_cast<const uint4*>(a.x + (int64_t)pl.tok[u][i] * H + c * 32);
-        uint32_t* dst = xperm + i * (H / 2) + c * 16;
-        float s = 0.0f;
+    Seg g, v;
+    seg_load<MODE>(base, L.p[0], row, min(c0, CPR - 1), a.scale_f16, g);
+    seg_load<MODE>(base, L.p[1], row, min(c0, CPR - 1), a.scale_f16, v);
+    float bg = 0.f, bu = 0.f;
+    if (L.p[0].bias >= 0) {
+        bg = bf2f(reinterpret_cast<const uint16_t*>(base + L.p[0].bias)[row]);
+        bu = bf2f(reinterpret_cast<const uint16_t*>(base + L.p[1].bias)[row]);
+    }
+    PairIter pit{en.mm, 0};
+    for (int i = 0; i < en.nt; ++i) {
+        int tok;
+        const int pair = pit.next(a, en, tok);
+        const uint4* xp = reinterpret_cast<const uint4*>(a.x + (int64_t)tok * H);
+        uint4 xr[kCPS][4];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            uint4 v = src[q];
-            uint32_t in[4] = {v.x, v.y, v.z, v.w}, o[4];
-            perm8(in, o);
+        for (int j = 0; j < kCPS; ++j)
 #pragma unroll
-            for (int z = 0; z < 4; ++z) {
-                dst[4 * q + z] = o[z];
-                s += bf2f(in[z] & 0xFFFFu) + bf2f(in[z] >> 16);
+            for (int q = 0; q < 4; ++q) xr[j][q] = xp[min(c0 + j, CPR - 1) * 4 + q];
+        float pg = 0.f, pu = 0.f;
+#pragma unroll
+        for (int j = 0; j < kCPS; ++j) {
+            if (j < nvalid) {
+                XChunk xc;
+                x_prepare<MODE>(xr[j], xc);
+                pg += chunk_dot<MODE>(g, j, xc);
+                pu += chunk_dot<MODE>(v, j, xc);
             }
         }
-        xsum[i * CPR + c] = s;
-    }
-    __syncthreads();
-
-    auto xp = [&](int i, int c) { return xperm + i * (H / 2) + c * 16; };
-    auto xs = [&](int i, int c) { return xsum[i * CPR + c]; };
-    const int W = 2 * RB * S;
-    for (int wi = tid; wi < W; wi += kThreads) {
-        int mat = wi / (RB * S);
-        int rem = wi - mat * RB * S;
-        int rr = rem / S, seg = rem - rr * S;
-        int row = r0 + rr;
-        const Proj& P = L.p[mat];
-        const uint8_t* wrow = base + P.w + (int64_t)row * (H / 2);
-        int gcount = (MODE == BRX_QUANT_AFFINE) ? H / 64 : H / 32;
-        int gs = (MODE == BRX_QUANT_AFFINE) ? 64 : 32;
-        const uint8_t* srow = base + P.s + (int64_t)row * gcount * (MODE == BRX_QUANT_AFFINE ? 2 : 1);
-        const uint8_t* brow = (MODE == BRX_QUANT_AFFINE) ? base + P.b + (int64_t)row * gcount * 2 : nullptr;
-        float pr[kMaxTok];
-        seg_partials<MODE, CPS>(wrow, srow, brow, seg * CPS, gs, a.scale_f16, nt, xp, xs, pr);
-        for (int i = 0; i < nt; ++i) part[((i * 2 + mat) * RB + rr) * S + seg] = pr[i];
-    }
-    __syncthreads();
-
-    // reduce segments in order, activation, h -> bf16 (pair-permuted in blocks of 8)
-    uint16_t* hs = reinterpret_cast<uint16_t*>(part + nt * 2 * RB * S);  // [nt][RB]
-    for (int it = tid; it < nt * RB; it += kThreads) {
-        int i = it / RB, rr = it - i * RB;
-        const float* pg = part + ((i * 2 + 0) * RB + rr) * S;
-        const float* pu = part + ((i * 2 + 1) * RB + rr) * S;
-        float g = 0.0f, v = 0.0f;
-        for (int s2 = 0; s2 < S; ++s2) { g += pg[s2]; v += pu[s2]; }
-        int row = r0 + rr;
-        if (L.p[0].bias >= 0) {
-            g += bf2f(reinterpret_cast<const uint16_t*>(base + L.p[0].bias)[row]);
-            v += bf2f(reinterpret_cast<const uint16_t*>(base + L.p[1].bias)[row]);
+        pg = seg_reduce<SP>(pg);
+        pu = seg_reduce<SP>(pu);
+        if (seg == 0 && r0 + rr < inter) {
+            float h = act_apply(a.act, pg + bg, pu + bu, a.alpha, a.limit);
+            hbuf[(int64_t)pair * hstride + h_pos<MODE>(r0 + rr)] = (uint16_t)f2bf(h);
         }
-        hs[i * RB + rr] = (uint16_t)f2bf(act_apply(a.act, g, v, a.alpha, a.limit));
-    }
-    __syncthreads();
-    for (int it = tid; it < nt * (RB / 8); it += kThreads) {
-        int i = it / (RB / 8), m = it - i * (RB / 8);
-        const uint16_t* hr = hs + i * RB + 8 * m;
-        uint32_t in[4], o[4];
-#pragma unroll
-        for (int z = 0; z < 4; ++z) in[z] = (uint32_t)hr[2 * z] | ((uint32_t)hr[2 * z + 1] << 16);
-        perm8(in, o);
-        uint4* dst = reinterpret_cast<uint4*>(hbuf + (int64_t)pl.pair[u][i] * hstride + r0 + 8 * m);
-        *dst = make_uint4(o[0], o[1], o[2], o[3]);
     }
 }
 
 // ------------------------------------------------------------------ down + combine
-template <int MODE, int CPS>
+// Items (entry u, row rr, seg) in that order; SP consecutive lanes own one (entry, row).
+template <int MODE, int SP>
 __global__ __launch_bounds__(kThreads) void k_dec_down(FwdArgs a, const uint16_t* __restrict__ hbuf,
-                                                       int RBD, int hstride) {
-    __shared__ Plan pl;
-    extern __shared__ float fsm[];
+                                                       int RBD, int hstride,
+                                                       const DecTable* __restrict__ table) {
+    extern __shared__ float ys[];         // [PT][RBD]
     const int tid = threadIdx.x;
-    if (tid < kWave) build_plan(a, pl);
-    __syncthreads();
     const int P = a.P;
     const int PT = P + (a.auto_shared ? a.T : 0);
-    const int I = a.I, CPR = I / 32, S = CPR / CPS;
+    const int I = a.I, CPR = I / 32;
     const int n0 = blockIdx.x * RBD;
     const int H = a.H;
-
-    float* hsum = fsm;                          // [PT][CPR]
-    float* part = hsum + PT * CPR;              // [PT][RBD][S]
-    float* ys = part + PT * RBD * S;            // [PT][RBD]
-
-    // chunk sums of every pair's h (pair-permuted order does not change a chunk's sum)
-    for (int it = tid; it < PT * CPR; it += kThreads) {
-        int p = it / CPR, c = it - p * CPR;
-        const uint4* src = reinterpret_cast<const uint4*>(hbuf + (int64_t)p * hstride + c * 32);
-        float s = 0.0f;
+    const int n = table->n;
+    const int W = n * RBD * SP;
+    for (int b0 = 0; b0 < W; b0 += kThreads) {
+        const int it = b0 + tid;
+        const bool valid = it < W;
+        const int u = valid ? it / (RBD * SP) : 0;
+        const int rem = it - u * RBD * SP;
+        const int rr = valid ? rem / SP : 0;
+        const int seg = valid ? rem - rr * SP : SP;
+        const DecEntry& d = table->ent[u];
+        const int slot = d.slot;
+        const int nt = valid ? d.nt : 0;
+        const uint8_t* base = slot_base(a, slot);
+        const Layout& L = slot < 0 ? a.lay_sh : a.lay;
+        const int c0 = min(seg * kCPS, CPR - 1);
+        const int nvalid = valid ? min(kCPS, CPR - seg * kCPS) : 0;
+        Seg sg;
+        seg_load<MODE>(base, L.p[2], n0 + rr, c0, a.scale_f16, sg);
+        // the SP lanes of one (entry, row) share nt; lanes past W have nt = 0 and only take
+        // part in the shuffles
+        int ntg = nt;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            uint4 v = src[q];
-            uint32_t in[4] = {v.x, v.y, v.z, v.w};
+        for (int off = SP / 2; off >= 1; off >>= 1) ntg = max(ntg, __shfl_xor(ntg, off, kWave));
+        for (int i = 0; i < ntg; ++i) {
+            const int pi = d.pair[i < kMaxTok ? i : 0];
+            const uint4* hp = reinterpret_cast<const uint4*>(hbuf + (int64_t)pi * hstride);
+            uint4 hr[kCPS][4];
 #pragma unroll
-            for (int z = 0; z < 4; ++z) s += bf2f(in[z] & 0xFFFFu) + bf2f(in[z] >> 16);
+            for (int j = 0; j < kCPS; ++j)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) hr[j][q] = hp[min(c0 + j, CPR - 1) * 4 + q];
+            float p = 0.0f;
+#pragma unroll
+            for (int j = 0; j < kCPS; ++j) {
+                if (j < nvalid && i < nt) {
+                    XChunk xc;
+                    h_prepare<MODE>(hr[j], xc);
+                    p += chunk_dot<MODE>(sg, j, xc);
+                }
+            }
+            p = seg_reduce<SP>(p);
+            if (valid && seg == 0 && i < nt) ys[pi * RBD + rr] = p;
         }
-        hsum[it] = s;
-    }
-    __syncthreads();
-
-    const int gs = (MODE == BRX_QUANT_AFFINE) ? 64 : 32;
-    const int gcount = I / gs;
-    const int W = pl.n * RBD * S;
-    for (int wi = tid; wi < W; wi += kThreads) {
-        int u = wi / (RBD * S);
-        int rem = wi - u * RBD * S;
-        int rr = rem / S, seg = rem - rr * S;
-        int n = n0 + rr;
-        int e = pl.e[u];
-        const Layout& L = e >= a.E ? a.lay_sh : a.lay;
-        const uint8_t* base = expert_base(a, e);
-        const Proj& Pd = L.p[2];
-        const uint8_t* wrow = base + Pd.w + (int64_t)n * (I / 2);
-        const uint8_t* srow = base + Pd.s + (int64_t)n * gcount * (MODE == BRX_QUANT_AFFINE ? 2 : 1);
-        const uint8_t* brow = (MODE == BRX_QUANT_AFFINE) ? base + Pd.b + (int64_t)n * gcount * 2 : nullptr;
-        const int nt = pl.ntok[u];
-        auto xp = [&](int i, int c) {
-            return reinterpret_cast<const uint32_t*>(hbuf + (int64_t)pl.pair[u][i] * hstride + c * 32);
-        };
-        auto xs = [&](int i, int c) { return hsum[pl.pair[u][i] * CPR + c]; };
-        float pr[kMaxTok];
-        seg_partials<MODE, CPS>(wrow, srow, brow, seg * CPS, gs, a.scale_f16, nt, xp, xs, pr);
-        for (int i = 0; i < nt; ++i) part[(pl.pair[u][i] * RBD + rr) * S + seg] = pr[i];
     }
     __syncthreads();
 
     // each pair's row result, rounded to bf16 as the projection's output
     for (int it = tid; it < PT * RBD; it += kThreads) {
         int p = it / RBD, rr = it - p * RBD;
-        const float* pp = part + (p * RBD + rr) * S;
-        float y = 0.0f;
-        for (int s2 = 0; s2 < S; ++s2) y += pp[s2];
-        int n = n0 + rr;
-        int e = p < P ? min(max(a.pexp[p], 0), a.shared ? a.E : a.E - 1) : a.E;
-        const Layout& L = e >= a.E ? a.lay_sh : a.lay;
-        if (L.p[2].bias >= 0)
-            y += bf2f(reinterpret_cast<const uint16_t*>(expert_base(a, e) + L.p[2].bias)[n]);
+        float y = ys[it];
+        int nn = n0 + rr;
+        if (a.has_bias) {
+            int e = p < P ? min(max(a.pexp[p], 0), a.shared ? a.E : a.E - 1) : a.E;
+            int s = -1;
+            if (e < a.E) s = min(max(a.g2s[e], 0), a.capacity - 1);
+            const Layout& L = s < 0 ? a.lay_sh : a.lay;
+            y += bf2f(reinterpret_cast<const uint16_t*>(slot_base(a, s) + L.p[2].bias)[nn]);
+        }
         uint32_t yb = f2bf(y);
         ys[it] = bf2f(yb);
-        if (a.yun && p < P) a.yun[(int64_t)pair_row(a, p) * H + n] = (uint16_t)yb;
+        if (a.yun && p < P) a.yun[(int64_t)pair_row(a, p) * H + nn] = (uint16_t)yb;
     }
     __syncthreads();
 
@@ -318,75 +439,89 @@ __global__ __launch_bounds__(kThreads) void k_dec_down(FwdArgs a, const uint16_t
     }
 }
 
-int pick_cps(int cpr) {
-    for (int c : {4, 3, 2}) if (cpr % c == 0) return c;
-    return 1;
+int pow2ceil(int v) {
+    int p = 1;
+    while (p < v) p <<= 1;
+    return p;
+}
+
+template <int MODE, int SP>
+hipError_t launch_gateup(const FwdArgs& a, uint16_t* hbuf, DecTable* table, int nu, int Imax,
+                         hipStream_t s) {
+    constexpr int RB = kThreads / SP;
+    dim3 grid((Imax + RB - 1) / RB, nu);
+    hipLaunchKernelGGL((k_dec_gateup<MODE, SP>), grid, dim3(kThreads), 0, s, a, hbuf, Imax, table);
+    return hipGetLastError();
+}
+
+template <int MODE, int SP>
+hipError_t launch_down(const FwdArgs& a, uint16_t* hbuf, DecTable* table, int nu, int PT, int Imax,
+                       hipStream_t s) {
+    int RBD = 1;
+    while (RBD < 16 && nu * (RBD * 2) * SP <= kThreads && a.H % (RBD * 2) == 0) RBD *= 2;
+    size_t lds = (size_t)PT * RBD * 4;
+    hipLaunchKernelGGL((k_dec_down<MODE, SP>), dim3(a.H / RBD), dim3(kThreads), lds, s, a, hbuf, RBD,
+                       Imax, table);
+    return hipGetLastError();
+}
+
+#define BRX_SEG_CASES(FN, ...)                                                   \
+    do {                                                                         \
+        if (sp_ == 1) return FN<MODE, 1>(__VA_ARGS__);                           \
+        if (sp_ == 2) return FN<MODE, 2>(__VA_ARGS__);                           \
+        if (sp_ == 4) return FN<MODE, 4>(__VA_ARGS__);                           \
+        if (sp_ == 8) return FN<MODE, 8>(__VA_ARGS__);                           \
+        if (sp_ == 16) return FN<MODE, 16>(__VA_ARGS__);                         \
+        if (sp_ == 32) return FN<MODE, 32>(__VA_ARGS__);                         \
+        return hipErrorInvalidValue;                                             \
+    } while (0)
+
+template <int MODE>
+hipError_t dispatch_gateup(const FwdArgs& a, uint16_t* hbuf, DecTable* table, int nu, int Imax,
+                           hipStream_t s) {
+    const int sp_ = pow2ceil((a.H / 32 + kCPS - 1) / kCPS);
+    BRX_SEG_CASES(launch_gateup, a, hbuf, table, nu, Imax, s);
 }
 
 template <int MODE>
-hipError_t launch_mode(const FwdArgs& a, uint16_t* hbuf, int phases, hipStream_t s) {
+hipError_t dispatch_down(const FwdArgs& a, uint16_t* hbuf, DecTable* table, int nu, int PT, int Imax,
+                         hipStream_t s) {
+    const int sp_ = pow2ceil((a.I / 32 + kCPS - 1) / kCPS);
+    BRX_SEG_CASES(launch_down, a, hbuf, table, nu, PT, Imax, s);
+}
+
+template <int MODE>
+hipError_t launch_mode(const FwdArgs& a, uint16_t* hbuf, DecTable* table, int phases, hipStream_t s) {
     const int P = a.P;
     const int PT = P + (a.auto_shared ? a.T : 0);
     const int nu = P + (a.auto_shared ? 1 : 0);
     const int Imax = a.I > a.I_sh ? a.I : a.I_sh;
-    const int hstride = Imax;
-    // gate/up
     if (phases & 1) {
-        const int CPR = a.H / 32;
-        const int cps = pick_cps(CPR);
-        const int S = CPR / cps;
-        const int nt = a.auto_shared ? a.T : (a.T < P ? a.T : P);  // worst case tokens per expert
-        int RB = 16;
-        auto lds = [&](int rb) {
-            return (size_t)nt * (a.H / 2) * 4 + (size_t)nt * CPR * 4 + (size_t)nt * 2 * rb * S * 4 +
-                   (size_t)nt * rb * 2;
-        };
-        while (RB > 8 && (lds(RB) > 56 * 1024 || Imax % RB)) RB /= 2;
-        if (lds(RB) > 56 * 1024 || Imax % RB || a.I % RB || (a.shared && a.I_sh % RB))
-            return hipErrorInvalidValue;
-        dim3 grid((Imax + RB - 1) / RB, nu);
-        size_t L = lds(RB);
-        switch (cps) {
-            case 4: hipLaunchKernelGGL((k_dec_gateup<MODE, 4>), grid, dim3(kThreads), L, s, a, hbuf, RB, hstride); break;
-            case 3: hipLaunchKernelGGL((k_dec_gateup<MODE, 3>), grid, dim3(kThreads), L, s, a, hbuf, RB, hstride); break;
-            case 2: hipLaunchKernelGGL((k_dec_gateup<MODE, 2>), grid, dim3(kThreads), L, s, a, hbuf, RB, hstride); break;
-            default: hipLaunchKernelGGL((k_dec_gateup<MODE, 1>), grid, dim3(kThreads), L, s, a, hbuf, RB, hstride); break;
-        }
-        hipError_t err = hipGetLastError();
+        hipError_t err = dispatch_gateup<MODE>(a, hbuf, table, nu, Imax, s);
         if (err != hipSuccess) return err;
     }
-    // down + combine
     if (phases & 2) {
-        const int CPR = a.I / 32;
-        const int cps = pick_cps(CPR);
-        const int S = CPR / cps;
-        int RBD = 8;
-        while (RBD > 1 && nu * RBD * S > kThreads) RBD /= 2;
-        if (a.H % RBD) return hipErrorInvalidValue;
-        size_t L = (size_t)PT * CPR * 4 + (size_t)PT * RBD * S * 4 + (size_t)PT * RBD * 4;
-        dim3 grid(a.H / RBD);
-        switch (cps) {
-            case 4: hipLaunchKernelGGL((k_dec_down<MODE, 4>), grid, dim3(kThreads), L, s, a, hbuf, RBD, hstride); break;
-            case 3: hipLaunchKernelGGL((k_dec_down<MODE, 3>), grid, dim3(kThreads), L, s, a, hbuf, RBD, hstride); break;
-            case 2: hipLaunchKernelGGL((k_dec_down<MODE, 2>), grid, dim3(kThreads), L, s, a, hbuf, RBD, hstride); break;
-            default: hipLaunchKernelGGL((k_dec_down<MODE, 1>), grid, dim3(kThreads), L, s, a, hbuf, RBD, hstride); break;
-        }
-        return hipGetLastError();
+        hipError_t err = dispatch_down<MODE>(a, hbuf, table, nu, PT, Imax, s);
+        if (err != hipSuccess) return err;
     }
     return hipSuccess;
 }
+
+inline size_t table_bytes() { return (sizeof(DecTable) + 255) & ~(size_t)255; }
 
 }  // namespace
 
 size_t decode_workspace_bytes(const FwdArgs& a) {
     const int PT = a.P + (a.auto_shared ? a.T : 0);
     const int Imax = a.I > a.I_sh ? a.I : a.I_sh;
-    return (size_t)PT * Imax * 2;
+    return table_bytes() + (size_t)PT * Imax * 2;
 }
 
-hipError_t launch_decode(const FwdArgs& a, uint16_t* hbuf, int phases, hipStream_t s) {
-    return a.quant_mode == BRX_QUANT_AFFINE ? launch_mode<BRX_QUANT_AFFINE>(a, hbuf, phases, s)
-                                            : launch_mode<BRX_QUANT_MXFP4>(a, hbuf, phases, s);
+hipError_t launch_decode(const FwdArgs& a, void* ws, int phases, hipStream_t s) {
+    DecTable* table = reinterpret_cast<DecTable*>(ws);
+    uint16_t* hbuf = reinterpret_cast<uint16_t*>(reinterpret_cast<char*>(ws) + table_bytes());
+    return a.quant_mode == BRX_QUANT_AFFINE ? launch_mode<BRX_QUANT_AFFINE>(a, hbuf, table, phases, s)
+                                            : launch_mode<BRX_QUANT_MXFP4>(a, hbuf, table, phases, s);
 }
 
 }  // namespace brx

@@ -17,6 +17,7 @@ namespace {
 constexpr int kRouterThreads = 256;
 constexpr int kMaxE = 512;
 constexpr int kMaxK = 64;  // top-k is held one rank per lane
+constexpr int kSmallT = 64;  // up to this many tokens: logits kernel + top-k kernel
 
 __device__ __forceinline__ float wave_sum_xor(float v) {
 #pragma unroll
@@ -147,6 +148,194 @@ __global__ __launch_bounds__(kRouterThreads) void k_router(
     }
 }
 
+// ---------------------------------------------------------------- small T
+template <int kPer>
+__device__ __forceinline__ void topk_row(const float* __restrict__ l, float* lv, int t, int E, int k,
+                                         int mode, int has_sg, int32_t* __restrict__ out_idx,
+                                         float* __restrict__ out_w, float* __restrict__ out_sg);
+
+// k_router_logits: one wave per (expert row, tile of TT tokens); every load of the wave is
+// issued before the first FMA. Same per-lane chain and butterfly as above. With `counter`
+// set, the last block to finish (device-scope count after a release fence) also ranks the
+// top-k of every token, so a decode step routes in one launch; that block resets the count.
+template <bool WF32, int TT, int kPer>
+__global__ __launch_bounds__(kRouterThreads) void k_router_logits(
+    const uint16_t* __restrict__ x, const void* __restrict__ w, const float* __restrict__ bias,
+    const uint16_t* __restrict__ sgw, int T, int H, int E, float* __restrict__ logits,
+    unsigned* __restrict__ counter, int k, int mode, int32_t* __restrict__ out_idx,
+    float* __restrict__ out_w, float* __restrict__ out_sg) {
+    constexpr int kNJ = 6;                      // chunks per lane: H <= 64 * 8 * 6 = 3072
+    const int lane = threadIdx.x & 63;
+    const int r = blockIdx.x * (kRouterThreads / kWave) + (threadIdx.x >> 6);
+    const int rows = E + (sgw ? 1 : 0);
+    const int t0 = blockIdx.y * TT;
+    const int nt = min(TT, T - t0);
+    const int nch = H / 8;
+    if (r < rows) {
+        const bool wf32 = WF32 && r < E;
+        uint4 wv[kNJ][2];
+        uint4 xv[TT][kNJ];
+#pragma unroll
+        for (int j = 0; j < kNJ; ++j) {
+            const int c = lane + kWave * j;
+            if (c < nch) {
+                if (wf32) {
+                    const uint4* p = reinterpret_cast<const uint4*>(
+                        reinterpret_cast<const float*>(w) + (int64_t)r * H + 8 * c);
+                    wv[j][0] = p[0];
+                    wv[j][1] = p[1];
+                } else {
+                    const uint16_t* src = r < E ? reinterpret_cast<const uint16_t*>(w) + (int64_t)r * H : sgw;
+                    wv[j][0] = *reinterpret_cast<const uint4*>(src + 8 * c);
+                }
+#pragma unroll
+                for (int t = 0; t < TT; ++t)
+                    if (t < nt) xv[t][j] = *reinterpret_cast<const uint4*>(x + (int64_t)(t0 + t) * H + 8 * c);
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < TT; ++t) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int j = 0; j < kNJ; ++j) {
+                const int c = lane + kWave * j;
+                if (c < nch && t < nt) {
+                    uint32_t xw[4] = {xv[t][j].x, xv[t][j].y, xv[t][j].z, xv[t][j].w};
+                    float wf[8];
+                    if (wf32) {
+                        wf[0] = __uint_as_float(wv[j][0].x); wf[1] = __uint_as_float(wv[j][0].y);
+                        wf[2] = __uint_as_float(wv[j][0].z); wf[3] = __uint_as_float(wv[j][0].w);
+                        wf[4] = __uint_as_float(wv[j][1].x); wf[5] = __uint_as_float(wv[j][1].y);
+                        wf[6] = __uint_as_float(wv[j][1].z); wf[7] = __uint_as_float(wv[j][1].w);
+                    } else {
+                        uint32_t ww[4] = {wv[j][0].x, wv[j][0].y, wv[j][0].z, wv[j][0].w};
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            wf[2 * i] = bf2f(ww[i] & 0xFFFFu);
+                            wf[2 * i + 1] = bf2f(ww[i] >> 16);
+                        }
+                    }
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        acc = fmaf(bf2f(xw[i] & 0xFFFFu), wf[2 * i], acc);
+                        acc = fmaf(bf2f(xw[i] >> 16), wf[2 * i + 1], acc);
+                    }
+                }
+            }
+            float s = wave_sum_xor(acc);
+            if (lane == 0 && t < nt) logits[(int64_t)(t0 + t) * (E + 1) + r] = (r < E && bias) ? s + bias[r] : s;
+        }
+    }
+    if (counter == nullptr) return;
+    __shared__ unsigned s_last;
+    __threadfence();                            // release this block's logits
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const unsigned nblk = gridDim.x * gridDim.y;
+        s_last = atomicAdd(counter, 1u) == nblk - 1 ? 1u : 0u;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    __threadfence();                            // acquire every block's logits
+    if (threadIdx.x == 0) *counter = 0u;
+    __shared__ __attribute__((aligned(16))) float lv[kRouterThreads / kWave][kWave * kPer];
+    const int wv = threadIdx.x >> 6;
+    for (int t = wv; t < T; t += kRouterThreads / kWave)
+        topk_row<kPer>(logits + (int64_t)t * (E + 1), lv[wv], t, E, k, mode, sgw ? 1 : 0, out_idx,
+                       out_w, out_sg);
+}
+
+// Top-k of one token's logits row `l` ([E + 1], the last entry the shared-gate logit) by the
+// calling wave, with `lv` a wave-private LDS row of 64 * kPer floats. Each candidate's rank is
+// counted directly (how many logits beat it: greater, or equal with a lower id), so there is
+// no serial chain of k arg-max reductions; the candidates of rank < k are the top-k in order.
+template <int kPer>
+__device__ __forceinline__ void topk_row(const float* __restrict__ l, float* lv, int t, int E, int k,
+                                         int mode, int has_sg, int32_t* __restrict__ out_idx,
+                                         float* __restrict__ out_w, float* __restrict__ out_sg) {
+    const int lane = threadIdx.x & 63;
+    float v[kPer];
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+        const int e = lane + kWave * i;
+        v[i] = e < E ? l[e] : 0.0f;
+        if (e < E) lv[e] = v[i];
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    int rank[kPer];
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) rank[i] = 0;
+    float m = lv[0];
+    const int E4 = E & ~3;
+    for (int e2 = 0; e2 < E4; e2 += 4) {
+        const float4 q = *reinterpret_cast<const float4*>(&lv[e2]);
+        const float qq[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int z = 0; z < 4; ++z) {
+            m = fmaxf(m, qq[z]);
+#pragma unroll
+            for (int i = 0; i < kPer; ++i) {
+                const int e = lane + kWave * i;
+                rank[i] += (int)(qq[z] > v[i]) | ((int)(qq[z] == v[i]) & (int)(e2 + z < e));
+            }
+        }
+    }
+    for (int e2 = E4; e2 < E; ++e2) {
+        const float qv = lv[e2];
+        m = fmaxf(m, qv);
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const int e = lane + kWave * i;
+            rank[i] += (int)(qv > v[i]) | ((int)(qv == v[i]) & (int)(e2 < e));
+        }
+    }
+    float ex[kPer];
+    float part = 0.f, psel = 0.f;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+        const int e = lane + kWave * i;
+        const bool in = e < E;
+        const bool sel = in && rank[i] < k;
+        ex[i] = in ? expf(v[i] - m) : 0.f;
+        part += ex[i];
+        psel += sel ? ex[i] : 0.f;
+    }
+    // p = ex / sum(ex) over all experts; topk-softmax normalises over the selected ones only;
+    // the renormalised rule divides p by its sum over the selected ones
+    float scale;
+    if (mode == BRX_ROUTE_TOPK_SOFTMAX) {
+        scale = 1.0f / wave_sum_xor(psel);
+    } else {
+        const float wsum = wave_sum_xor(part);
+        scale = 1.0f / wsum;
+        if (mode == BRX_ROUTE_SOFTMAX_TOPK_RENORM) scale = scale / wave_sum_xor(psel / wsum);
+    }
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+        const int e = lane + kWave * i;
+        if (e < E && rank[i] < k) {
+            out_idx[(int64_t)t * k + rank[i]] = e;
+            out_w[(int64_t)t * k + rank[i]] = ex[i] * scale;
+        }
+    }
+    if (lane == 0 && has_sg && out_sg) out_sg[t] = 1.0f / (1.0f + expf(-l[E]));
+}
+
+// One wave per token over logits [T][E + 1].
+template <int kPer>
+__global__ __launch_bounds__(kRouterThreads) void k_router_topk(
+    const float* __restrict__ logits, int T, int E, int k, int mode, int has_sg,
+    int32_t* __restrict__ out_idx, float* __restrict__ out_w, float* __restrict__ out_sg) {
+    __shared__ __attribute__((aligned(16))) float lv[kRouterThreads / kWave][kWave * kPer];
+    const int wv = threadIdx.x >> 6;
+    const int t = blockIdx.x * (kRouterThreads / kWave) + wv;
+    if (t >= T) return;
+    topk_row<kPer>(logits + (int64_t)t * (E + 1), lv[wv], t, E, k, mode, has_sg, out_idx, out_w,
+                   out_sg);
+}
+
 template <bool WF32, int TPB>
 hipError_t launch_tpb(const brx_layer_desc& d, const void* x, const void* w, const float* bias,
                       const void* sgw, int T, int32_t* out_idx, float* out_w, float* out_sg,
@@ -161,13 +350,53 @@ hipError_t launch_tpb(const brx_layer_desc& d, const void* x, const void* w, con
 
 }  // namespace
 
+size_t router_workspace_bytes(const brx_layer_desc& d, int T) {
+    return T <= kSmallT ? sizeof(float) * (size_t)T * (d.n_experts + 1) : 0;
+}
+
+template <bool WF32, int KP>
+hipError_t launch_small(const brx_layer_desc& d, const void* x, const void* w_router, const float* bias,
+                        const void* sgw, int T, int32_t* out_idx, float* out_w, float* out_sg,
+                        float* ws_logits, unsigned* counter, hipStream_t s) {
+    constexpr int TT = 4;
+    const int rows = d.n_experts + (sgw ? 1 : 0);
+    dim3 grid((rows + 3) / 4, (T + TT - 1) / TT);
+    // The last-block top-k (counter given) measured slower than a second launch on MI355X:
+    // its device-scope release/acquire fences cost more than the launch they save. Kept off.
+    const bool fused = false && T <= 8 && counter != nullptr;
+    hipLaunchKernelGGL((k_router_logits<WF32, TT, KP>), grid, dim3(kRouterThreads), 0, s,
+                       (const uint16_t*)x, w_router, bias, (const uint16_t*)sgw, T, d.hidden,
+                       d.n_experts, ws_logits, fused ? counter : nullptr, d.top_k, d.route_mode,
+                       out_idx, out_w, out_sg);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || fused) return e;
+    hipLaunchKernelGGL(k_router_topk<KP>, dim3((T + 3) / 4), dim3(kRouterThreads), 0, s, ws_logits, T,
+                       d.n_experts, d.top_k, d.route_mode, sgw ? 1 : 0, out_idx, out_w, out_sg);
+    return hipGetLastError();
+}
+
+template <bool WF32>
+hipError_t launch_small_e(const brx_layer_desc& d, const void* x, const void* w_router, const float* bias,
+                          const void* sgw, int T, int32_t* out_idx, float* out_w, float* out_sg,
+                          float* ws_logits, unsigned* counter, hipStream_t s) {
+    const int E = d.n_experts;
+    if (E <= 64) return launch_small<WF32, 1>(d, x, w_router, bias, sgw, T, out_idx, out_w, out_sg, ws_logits, counter, s);
+    if (E <= 128) return launch_small<WF32, 2>(d, x, w_router, bias, sgw, T, out_idx, out_w, out_sg, ws_logits, counter, s);
+    if (E <= 256) return launch_small<WF32, 4>(d, x, w_router, bias, sgw, T, out_idx, out_w, out_sg, ws_logits, counter, s);
+    return launch_small<WF32, 8>(d, x, w_router, bias, sgw, T, out_idx, out_w, out_sg, ws_logits, counter, s);
+}
+
 hipError_t launch_router(const brx_layer_desc& d, const void* x, const void* w_router,
                          const float* bias, const void* sgw, int T, int32_t* out_idx,
-                         float* out_w, float* out_sg, hipStream_t s) {
+                         float* out_w, float* out_sg, float* ws_logits, unsigned* counter,
+                         hipStream_t s) {
     if (T <= 0) return hipSuccess;
+    const bool f32 = d.router_dtype == BRX_DT_F32;
+    if (T <= kSmallT)
+        return f32 ? launch_small_e<true>(d, x, w_router, bias, sgw, T, out_idx, out_w, out_sg, ws_logits, counter, s)
+                   : launch_small_e<false>(d, x, w_router, bias, sgw, T, out_idx, out_w, out_sg, ws_logits, counter, s);
     // x staged as fp32: keep TPB * H * 4 within 48 KB of LDS
-    bool f32 = d.router_dtype == BRX_DT_F32;
-    if (T >= 64 && d.hidden <= 2880) {
+    if (d.hidden <= 2880) {
         return f32 ? launch_tpb<true, 4>(d, x, w_router, bias, sgw, T, out_idx, out_w, out_sg, s)
                    : launch_tpb<false, 4>(d, x, w_router, bias, sgw, T, out_idx, out_w, out_sg, s);
     }
