@@ -1,0 +1,113 @@
+"""libbrx.so without a GPU: it loads, exports every entry point include/brx.h declares, and
+its host-side validation and layout arithmetic behave (no kernel is launched here)."""
+import ctypes as C
+import os
+import re
+
+import pytest
+
+from bigrig_amd import formats as F
+from bigrig_amd import lib as L
+from bigrig_amd.spec import E256_SHARED, GPT_OSS_120B, OLMOE_1B_7B, QWEN3_30B_A3B
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include",
+                      "brx.h")
+SPECS = [OLMOE_1B_7B, QWEN3_30B_A3B, E256_SHARED, GPT_OSS_120B]
+
+
+def _declared():
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\**\s+\**(brx_\w+)\s*\(", src, flags=re.M)))
+
+
+def test_header_declarations_match_binding():
+    names = _declared()
+    assert len(names) >= 19
+    assert sorted(L.EXPORTS) == names
+    assert set(L._SIGS) == set(names)
+
+
+def test_library_loads_and_exports_every_symbol():
+    lib = L.load()
+    raw = C.CDLL(L.LIB)
+    for name in _declared():
+        assert hasattr(raw, name), name
+    assert lib.brx_abi_version() == 1
+    src = open(HEADER).read()
+    assert int(re.search(r"#define BRX_ABI_VERSION (\d+)", src).group(1)) == 1
+
+
+def test_header_enums_match_binding():
+    src = open(HEADER).read()
+    for cname, val in (("BRX_EINVAL", L.BRX_EINVAL), ("BRX_ESTATE", L.BRX_ESTATE),
+                       ("BRX_ERANGE", L.BRX_ERANGE), ("BRX_QUANT_MXFP4", L.QUANT_MXFP4),
+                       ("BRX_ACT_SWIGLU_CLAMPED", L.ACT_SWIGLU_CLAMPED),
+                       ("BRX_ROUTE_TOPK_SOFTMAX", L.ROUTE_TOPK_SOFTMAX), ("BRX_DT_BF16", L.DT_BF16),
+                       ("BRX_FWD_FORCE_PREFILL", L.FWD_FORCE_PREFILL),
+                       ("BRX_FWD_PHASE_B", L.FWD_PHASE_B)):
+        m = re.search(rf"\b{cname}\s*=\s*(-?\d+)", src) or \
+            re.search(rf"#define {cname}\s+\(?(-?\d+)u?", src)
+        assert m, cname
+        assert int(m.group(1)) == val, cname
+    assert C.sizeof(L.LayerDesc) == 64 and C.sizeof(L.ExpertLayout) == 13 * 8
+
+
+@pytest.mark.parametrize("spec", SPECS, ids=lambda s: f"H{s.hidden}I{s.inter}{s.quant.mode}")
+def test_expert_layout_matches_formats(spec):
+    lib = L.load()
+    d = spec.desc()
+    out = L.ExpertLayout()
+    L.check(lib.brx_expert_layout_get(C.byref(d), 0, C.byref(out)))
+    es = spec.expert_spec()
+    offs = F.spec_offsets(es)
+    assert out.bytes_per_expert == F.spec_bytes(es) == spec.bytes_per_expert
+    for p, proj in enumerate(F.PROJECTIONS):
+        assert out.weight[p] == offs[(proj, "weight")]
+        assert out.scales[p] == offs[(proj, "scales")]
+        assert out.biases[p] == offs.get((proj, "biases"), -1)
+        assert out.bias[p] == offs.get((proj, "bias"), -1)
+    if spec.shared_inter:
+        L.check(lib.brx_expert_layout_get(C.byref(d), 1, C.byref(out)))
+        assert out.bytes_per_expert == F.spec_bytes(spec.expert_spec(True))
+    else:
+        assert lib.brx_expert_layout_get(C.byref(d), 1, C.byref(out)) == L.BRX_EINVAL
+
+
+BAD = [("hidden", 100, "hidden"), ("inter", 0, "inter"), ("n_experts", 513, "n_experts"),
+       ("top_k", 0, "top_k"), ("bits", 3, "affine"), ("group_size", 128, "affine"),
+       ("quant_mode", 7, "quant_mode"), ("act", 5, "act"), ("route_mode", 3, "route_mode"),
+       ("router_dtype", 9, "router_dtype"), ("shared_inter", 96, "shared_inter")]
+
+
+@pytest.mark.parametrize("field,value,msg", BAD, ids=[b[0] for b in BAD])
+def test_descriptor_validation(field, value, msg):
+    """Every entry point validates the descriptor before anything touches the device."""
+    lib = L.load()
+    d = QWEN3_30B_A3B.desc()
+    setattr(d, field, value)
+    out = L.ExpertLayout()
+    assert lib.brx_expert_layout_get(C.byref(d), 0, C.byref(out)) == L.BRX_EINVAL
+    assert msg in lib.brx_last_error().decode()
+    assert lib.brx_router_topk(C.byref(d), None, None, None, None, 1, None, None, None,
+                               None) == L.BRX_EINVAL
+    assert lib.brx_sort_pairs(C.byref(d), None, 1, None, None, None) == L.BRX_EINVAL
+    h = C.c_void_p()
+    assert lib.brx_pool_create(C.byref(d), 4, C.byref(h)) == L.BRX_EINVAL and not h.value
+
+
+def test_calls_before_init_fail_cleanly():
+    lib = L.load()
+    d = QWEN3_30B_A3B.desc()
+    assert lib.brx_router_topk(C.byref(d), None, None, None, None, 1, None, None, None,
+                               None) == L.BRX_ESTATE
+    assert "brx_init" in lib.brx_last_error().decode()
+    assert lib.brx_pool_destroy(None) == L.BRX_OK          # like free(NULL)
+    assert lib.brx_pool_capacity(None) < 0
+    with pytest.raises(L.BrxError):
+        L.check(lib.brx_pool_sync(None))
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        L.load(str(tmp_path / "nope.so"))
