@@ -52,7 +52,25 @@ def parse():
     ap.add_argument("--pool-tokens", type=int, default=64)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--skip", default="", help="comma list of: prefill,pool,cpu,graph")
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="only run a plain device copy of this many MiB (--steps times): the "
+                         "known-size reference for scaling HBM byte counters")
     return ap.parse_args()
+
+
+def copy_probe(args) -> None:
+    import torch
+    n = args.copy_mib << 20
+    src = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / args.steps
+    print(json.dumps({"copy_bytes": n, "read_bytes": n, "write_bytes": n, "steps": args.steps,
+                      "gbs": round(2 * n / dt / 1e9, 1)}), flush=True)
 
 
 class Stack:
@@ -309,11 +327,15 @@ def pool_bench(args, st: "Stack"):
         sw = StreamingSwitchGLU(pool, fetcher)
         sw.refresh()
         mods.append(MoELayer(spec, st.routers[l], sw, router_bias=st.biases[l]))
-    G = st.xbank[0].shape[0]
+    from bigrig_amd import synth
+    n = args.pool_tokens
+    # a fresh activation per (layer, token): repeating a small input bank would let the pool
+    # settle on that bank's experts and report no misses
+    xs = [synth.activations(8 + n, spec.hidden, seed=6000 + l) for l in layers]
 
     def token(i):
         for l, m in zip(layers, mods):
-            m(st.xbank[l][i % G:i % G + 1])
+            m(xs[l][i:i + 1])
 
     for i in range(8):            # fill the pools
         token(i)
@@ -322,7 +344,6 @@ def pool_bench(args, st: "Stack"):
         p = m.switch._pool
         p.hits = p.misses = 0
     t0 = time.perf_counter()
-    n = args.pool_tokens
     for i in range(n):
         token(8 + i)
     torch.cuda.synchronize()
@@ -390,6 +411,9 @@ def main():
         print("bench.py needs a GPU (no CPU fallback)", file=sys.stderr)
         sys.exit(1)
     L.init(0)
+    if args.copy_mib:
+        copy_probe(args)
+        return
     spec = QWEN3_30B_A3B
     skip = set(filter(None, args.skip.split(",")))
     keep = 0 if "pool" in skip else args.layers

@@ -60,6 +60,25 @@ def test_router_bit_exact(gpu, spec, T):
         np.testing.assert_allclose(sg.cpu().numpy(), osg, rtol=1e-5, atol=1e-7)
 
 
+@pytest.mark.parametrize("T", [1, 8, 65])
+def test_router_summation_order_kat(gpu, T):
+    """The kernels sum a logit in the oracle's lane-tree order: expert 0's row is built so that
+    this order gives exactly 0 (element order would give 1), expert 1's row gives 0.5 and every
+    other row -1, so the top-2 is [1, 0] only under the specified order."""
+    import torch
+    spec = small(OLMOE_1B_7B, hidden=1024, n_experts=64, top_k=2)
+    H = spec.hidden
+    w = np.full((64, H), -1.0 / H, np.float32)
+    w[0] = 0.0
+    w[0, 0], w[0, 8 * 32], w[0, 8] = 2.0 ** 24, 1.0, -(2.0 ** 24)
+    w[1] = 0.5 / H
+    x = np.full((T, H), 0x3F80, np.uint16)
+    lg, oidx, _, _ = oracle.router(x, w, True, None, 2, spec.route_mode)
+    assert (lg[:, 0] == 0.0).all() and (lg[:, 1] == 0.5).all() and (oidx == [1, 0]).all()
+    idx, _, _ = ops.router_topk(spec, to_dev_bits(x, gpu), torch.from_numpy(w).to(gpu))
+    assert (idx.cpu().numpy() == [1, 0]).all()
+
+
 def _layer_check(lay, moe, T, seed, check_f64=True):
     import torch
     spec = lay.spec
