@@ -7,9 +7,10 @@ Workload (synthetic, seeded; random-init weights of the named architecture):
   Expert weights N(0, 0.02) per (layer, expert, projection), quantized on the GPU; router
   weights N(0, 0.02) bf16 plus a per-layer Zipf(s=1.1) logit bias; layer inputs N(0, 1) bf16.
 
-One step = one decode token through all 48 layers (router top-k, gate/up + SwiGLU, down +
-router-weighted combine), every expert resident in HBM (the pool's sync-free path), the step
-replayed as a HIP graph. `value` = decode tokens/s of the stack.
+One step = one decode token through all 48 layers, each layer one brx_moe_block_forward call
+(router logits; gate/up + SwiGLU with the top-k ranked inside the kernel; down + router-weighted
+combine), every expert resident in HBM (the pool's sync-free path), the step replayed as a HIP
+graph. `value` = decode tokens/s of the stack.
 
 Also reported on the same line:
   roofline      the dominant kernel (decode gate/up) timed with HIP events on its stream:
@@ -34,6 +35,10 @@ sys.path.insert(0, ROOT)
 METRIC = "MoE-layer tokens/s at batch 1 and 2048-token prefill; % of HBM/MFMA roofline"
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
+
+
+def _r(v, n):
+    return None if v is None else round(v, n)
 
 
 def log(msg: str) -> None:
@@ -111,33 +116,31 @@ class Stack:
 
 
 def decode_bench(args, st: "Stack"):
+    """48-layer decode step of one token, each layer one brx_moe_block_forward call (router
+    logits, gate/up with the top-k ranked in-kernel, down + combine), replayed as a HIP graph.
+    Per-kernel times come from graphs of the block's split steps (PHASE_R, +PHASE_A, +PHASE_B)
+    timed with HIP events on the stream the kernels run on."""
+    import ctypes as C
+
     import torch
 
     from bigrig_amd import lib as L
-    from bigrig_amd.layer import moe_forward, router_topk
     spec, Ln = st.spec, st.layers
     G = st.xbank[0].shape[0]
     dev = st.xbank[0].device
     k, H = spec.top_k, spec.hidden
-    idx = [torch.empty((1, k), dtype=torch.int32, device=dev) for _ in range(Ln)]
-    wts = [torch.empty((1, k), dtype=torch.float32, device=dev) for _ in range(Ln)]
     outs = [torch.empty((1, H), dtype=torch.bfloat16, device=dev) for _ in range(Ln)]
     lib = L.load()
     d = spec.desc()
-    import ctypes as C
     dref = C.byref(d)
 
     def step(g: int, stream: int, phases: int = 0):
         for l in range(Ln):
             x = st.xbank[l][g:g + 1]
-            if phases == 0:
-                L.check(lib.brx_router_topk(dref, x.data_ptr(), st.routers[l].data_ptr(),
-                                            st.biases[l].data_ptr(), None, 1, idx[l].data_ptr(),
-                                            wts[l].data_ptr(), None, stream))
-            L.check(lib.brx_moe_forward(dref, st.pools[l].device.handle, x.data_ptr(),
-                                        idx[l].data_ptr(), wts[l].data_ptr(), None, None, 1,
-                                        outs[l].data_ptr(), None,
-                                        L.FWD_FORCE_DECODE | phases, stream))
+            L.check(lib.brx_moe_block_forward(dref, st.pools[l].device.handle, x.data_ptr(),
+                                              st.routers[l].data_ptr(), st.biases[l].data_ptr(),
+                                              None, None, 1, outs[l].data_ptr(), None, None,
+                                              L.FWD_FORCE_DECODE | phases, stream))
 
     s = torch.cuda.current_stream()
     sp = s.cuda_stream
@@ -145,17 +148,19 @@ def decode_bench(args, st: "Stack"):
         step(g, sp)
     torch.cuda.synchronize()
 
+    def capture(g, phases=0):
+        cg = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(cg):
+            step(g, torch.cuda.current_stream().cuda_stream, phases)
+        return cg
+
     use_graph = "graph" not in args.skip
     graphs = []
     if use_graph:
         try:
-            for g in range(G):
-                cg = torch.cuda.CUDAGraph()
-                with torch.cuda.graph(cg):
-                    step(g, torch.cuda.current_stream().cuda_stream)
-                graphs.append(cg)
+            graphs = [capture(g) for g in range(G)]
             torch.cuda.synchronize()
-        except Exception as ex:   # capture unsupported: fall back to eager launches
+        except Exception as ex:   # capture unsupported: time eager launches
             log(f"graph capture failed ({ex}); timing eager launches")
             graphs = []
             torch.cuda.synchronize()
@@ -175,8 +180,6 @@ def decode_bench(args, st: "Stack"):
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
     tok_s = args.steps / dt
-    # eager (no graph) rate for reference
-    torch.cuda.synchronize()
     t1 = time.perf_counter()
     ne = max(10, args.steps // 5)
     for i in range(ne):
@@ -184,43 +187,29 @@ def decode_bench(args, st: "Stack"):
     torch.cuda.synchronize()
     eager_tok_s = ne / (time.perf_counter() - t1)
 
-    # per-kernel timing with HIP events on the launch stream: gate/up (phase A) and down
-    # (phase B) of every layer, routing already computed by the steps above
-    ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
-    reps = 20
-    ta = tb = 0.0
-    for r in range(reps):
-        g = r % G
-        for l in range(Ln):       # routing of token g at every layer
-            x = st.xbank[l][g:g + 1]
-            L.check(lib.brx_router_topk(dref, x.data_ptr(), st.routers[l].data_ptr(),
-                                        st.biases[l].data_ptr(), None, 1, idx[l].data_ptr(),
-                                        wts[l].data_ptr(), None, sp))
-        e0, e1, e2 = ev(), ev(), ev()
-        e0.record(s)
-        for l in range(Ln):
-            x = st.xbank[l][g:g + 1]
-            L.check(lib.brx_moe_forward(dref, st.pools[l].device.handle, x.data_ptr(),
-                                        idx[l].data_ptr(), wts[l].data_ptr(), None, None, 1,
-                                        outs[l].data_ptr(), None,
-                                        L.FWD_FORCE_DECODE | L.FWD_PHASE_A, sp))
-        e1.record(s)
-        for l in range(Ln):
-            x = st.xbank[l][g:g + 1]
-            L.check(lib.brx_moe_forward(dref, st.pools[l].device.handle, x.data_ptr(),
-                                        idx[l].data_ptr(), wts[l].data_ptr(), None, None, 1,
-                                        outs[l].data_ptr(), None,
-                                        L.FWD_FORCE_DECODE | L.FWD_PHASE_A, sp))
-            L.check(lib.brx_moe_forward(dref, st.pools[l].device.handle, x.data_ptr(),
-                                        idx[l].data_ptr(), wts[l].data_ptr(), None, None, 1,
-                                        outs[l].data_ptr(), None,
-                                        L.FWD_FORCE_DECODE | L.FWD_PHASE_B, sp))
-        e2.record(s)
-        torch.cuda.synchronize()
-        ta += e0.elapsed_time(e1)
-        tb += e1.elapsed_time(e2)
-    gateup_ms = ta / reps / Ln
-    down_ms = tb / reps / Ln - gateup_ms
+    # per-kernel times: graphs of the split steps over all layers, events on the same stream
+    per = {}
+    if graphs:
+        ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
+        reps = 10
+        for name, ph in (("r", L.FWD_PHASE_R), ("ra", L.FWD_PHASE_R | L.FWD_PHASE_A),
+                         ("rab", L.FWD_PHASE_R | L.FWD_PHASE_A | L.FWD_PHASE_B)):
+            gs = [capture(g, ph) for g in range(G)]
+            for g in gs:
+                g.replay()
+            torch.cuda.synchronize()
+            e0, e1 = ev(), ev()
+            e0.record(s)
+            for r in range(reps):
+                for g in gs:
+                    g.replay()
+            e1.record(s)
+            torch.cuda.synchronize()
+            per[name] = e0.elapsed_time(e1) / (reps * G * Ln) * 1e3   # us per layer
+            del gs
+    router_us = per.get("r")
+    gateup_us = per["ra"] - per["r"] if per else None
+    down_us = per["rab"] - per["ra"] if per else None
     spec_e = spec.expert_spec()
     gu = sum(c["nbytes"] for p in ("gate_proj", "up_proj") for c in spec_e[p].values())
     dn = sum(c["nbytes"] for c in spec_e["down_proj"].values())
@@ -229,11 +218,11 @@ def decode_bench(args, st: "Stack"):
     layer_bytes = k * spec.bytes_per_expert + spec.router_bytes + 2 * H * 2
     return {
         "tok_s": tok_s, "ms_per_step": dt / args.steps * 1e3, "graph": bool(graphs),
-        "eager_tok_s": eager_tok_s,
-        "gateup_us": gateup_ms * 1e3, "down_us": down_ms * 1e3,
+        "eager_tok_s": eager_tok_s, "router_us": router_us,
+        "gateup_us": gateup_us, "down_us": down_us,
         "gateup_bytes": gu_bytes, "down_bytes": dn_bytes, "layer_bytes": layer_bytes,
-        "gateup_gbs": gu_bytes / (gateup_ms * 1e-3) / 1e9,
-        "down_gbs": dn_bytes / (down_ms * 1e-3) / 1e9 if down_ms > 0 else None,
+        "gateup_gbs": gu_bytes / (gateup_us * 1e-6) / 1e9 if gateup_us else None,
+        "down_gbs": dn_bytes / (down_us * 1e-6) / 1e9 if down_us else None,
         "step_gbs": layer_bytes * Ln * tok_s / 1e9,
     }
 
@@ -465,16 +454,19 @@ def main():
             "weights": "4-bit affine g64", "layer_gb_per_token": round(dec["layer_bytes"] / 1e9, 5),
         },
         "roofline": {
-            "bound": "hbm", "achieved": round(dec["gateup_gbs"], 1), "peak": HBM_PEAK_GBS,
-            "unit": "GB/s", "frac": round(dec["gateup_gbs"] / HBM_PEAK_GBS, 4),
+            "bound": "hbm", "achieved": _r(dec["gateup_gbs"], 1), "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": _r(dec["gateup_gbs"] / HBM_PEAK_GBS if dec["gateup_gbs"] else None, 4),
             "traffic": traffic,
-            "kernel": "k_dec_gateup (8 experts x gate+up, 14.16 MB/launch)",
-            "avg_us": round(dec["gateup_us"], 3),
+            "kernel": f"k_dec_gateup, routed in-kernel ({spec.top_k} experts x gate+up, "
+                      f"{dec['gateup_bytes'] / 1e6:.2f} MB per launch)",
+            "avg_us": _r(dec["gateup_us"], 3),
         },
         "decode_kernels": {
-            "gateup_us": round(dec["gateup_us"], 3), "down_us": round(dec["down_us"], 3),
-            "gateup_gbs": round(dec["gateup_gbs"], 1),
-            "down_gbs": None if dec["down_gbs"] is None else round(dec["down_gbs"], 1),
+            "router_us": _r(dec["router_us"], 3),
+            "gateup_us": _r(dec["gateup_us"], 3), "down_us": _r(dec["down_us"], 3),
+            "gateup_gbs": _r(dec["gateup_gbs"], 1),
+            "down_gbs": _r(dec["down_gbs"], 1),
             "stack_gbs": round(dec["step_gbs"], 1),
             "stack_frac": round(dec["step_gbs"] / HBM_PEAK_GBS, 4),
             "eager_tok_s": round(dec["eager_tok_s"], 1),

@@ -15,11 +15,6 @@ namespace {
 
 thread_local std::string g_err;
 int g_device = -1;
-// Device-scope counters some kernels use to let their last block finish the launch's work
-// (zeroed once here; every kernel that takes one leaves it at zero when it ends).
-unsigned* g_counters = nullptr;
-constexpr int kCounters = 16;
-enum { kCounterRouter = 0 };
 
 struct Workspace {
     void* ptr = nullptr;
@@ -138,11 +133,6 @@ int brx_init(int device) {
     HIP_TRY(hipGetDeviceProperties(&prop, device));
     if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
         return fail(BRX_EINVAL, "device %d is %s; libbrx is built for gfx950 only", device, prop.gcnArchName);
-    if (!g_counters) {
-        HIP_TRY(hipMalloc(&g_counters, sizeof(unsigned) * kCounters));
-        HIP_TRY(hipMemset(g_counters, 0, sizeof(unsigned) * kCounters));
-        HIP_TRY(hipDeviceSynchronize());
-    }
     g_device = device;
     return BRX_OK;
 }
@@ -287,22 +277,16 @@ int brx_router_topk(const brx_layer_desc* d, const void* x, const void* w_router
     size_t need = router_workspace_bytes(*d, T);
     if (need && (rc = ws_reserve(need, (hipStream_t)stream, &ws))) return rc;
     hipError_t e = launch_router(*d, x, w_router, bias, shared_gate_w, T, out_idx, out_w, out_shared_gate,
-                                 (float*)ws, g_counters + kCounterRouter, (hipStream_t)stream);
+                                 (float*)ws, (hipStream_t)stream);
     if (e != hipSuccess) return hip_fail(e, "router launch");
     return BRX_OK;
 }
 
-static int forward_impl(const brx_layer_desc* d, brx_pool* p, const void* x, int T, int P,
-                        const int32_t* pexp, const int32_t* ptok, const int32_t* prow, int yrows,
-                        const float* w, const void* shared_expert, const float* shared_gate,
-                        void* out, void* y_rows, unsigned flags, void* stream) {
-    const bool force_dec = flags & BRX_FWD_FORCE_DECODE, force_pf = flags & BRX_FWD_FORCE_PREFILL;
-    if (force_dec && force_pf) return fail(BRX_EINVAL, "FORCE_DECODE and FORCE_PREFILL are exclusive");
+static FwdArgs make_args(const brx_layer_desc* d, brx_pool* p, const void* x, int T, int P,
+                         const int32_t* pexp, const int32_t* ptok, const int32_t* prow, int yrows,
+                         const float* w, const void* shared_expert, const float* shared_gate,
+                         void* out, void* y_rows) {
     const bool token_mode = ptok == nullptr;
-    bool decode = force_dec || (!force_pf && (token_mode ? T <= 8 : P <= 8));
-    if (decode && (T > 8 || P > 64))
-        return fail(BRX_EINVAL, "the decode path takes at most 8 token rows and 64 pairs (T=%d, P=%d)", T, P);
-
     FwdArgs a{};
     a.x = (const uint16_t*)x;
     a.P = P;
@@ -326,25 +310,47 @@ static int forward_impl(const brx_layer_desc* d, brx_pool* p, const void* x, int
     a.out = (uint16_t*)out;
     a.yun = (uint16_t*)y_rows;
     a.yrows = yrows;
+    a.route_mode = d->route_mode;
+    return a;
+}
 
-    hipStream_t s = (hipStream_t)stream;
-    size_t need = decode ? decode_workspace_bytes(a) : prefill_workspace_bytes(a);
-    void* ws = nullptr;
-    int rc = ws_reserve(need, s, &ws);
-    if (rc) return rc;
+// Queue the expert kernels of one forward on `s` over workspace `ws` (decode or grouped GEMM),
+// ordered after the pool's pending refills, and mark the pool read.
+static int run_forward(brx_pool* p, const FwdArgs& a, bool decode, int phases, void* ws,
+                       size_t ws_bytes, hipStream_t s) {
     if (p->refill_pending) {
         // forwards of one pool are issued on one stream: once it has waited, later ones follow
         HIP_TRY(hipStreamWaitEvent(s, p->refill_done, 0));
         p->refill_pending = false;
     }
-    int phases = (flags & (BRX_FWD_PHASE_A | BRX_FWD_PHASE_B)) >> 2;
-    if (phases == 0) phases = 3;
-    hipError_t e = decode ? launch_decode(a, ws, phases, s)
-                          : launch_prefill(a, ws, g_ws.bytes, phases, s);
+    hipError_t e = decode ? launch_decode(a, ws, phases, s) : launch_prefill(a, ws, ws_bytes, phases, s);
     if (e != hipSuccess) return hip_fail(e, decode ? "decode launch" : "prefill launch");
     HIP_TRY(hipEventRecord(p->last_read, s));
     p->read_recorded = true;
     return BRX_OK;
+}
+
+static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+static int forward_impl(const brx_layer_desc* d, brx_pool* p, const void* x, int T, int P,
+                        const int32_t* pexp, const int32_t* ptok, const int32_t* prow, int yrows,
+                        const float* w, const void* shared_expert, const float* shared_gate,
+                        void* out, void* y_rows, unsigned flags, void* stream) {
+    const bool force_dec = flags & BRX_FWD_FORCE_DECODE, force_pf = flags & BRX_FWD_FORCE_PREFILL;
+    if (force_dec && force_pf) return fail(BRX_EINVAL, "FORCE_DECODE and FORCE_PREFILL are exclusive");
+    const bool token_mode = ptok == nullptr;
+    bool decode = force_dec || (!force_pf && (token_mode ? T <= 8 : P <= 8));
+    if (decode && (T > 8 || P > 64))
+        return fail(BRX_EINVAL, "the decode path takes at most 8 token rows and 64 pairs (T=%d, P=%d)", T, P);
+    FwdArgs a = make_args(d, p, x, T, P, pexp, ptok, prow, yrows, w, shared_expert, shared_gate, out, y_rows);
+    hipStream_t s = (hipStream_t)stream;
+    size_t need = decode ? decode_workspace_bytes(a) : prefill_workspace_bytes(a);
+    void* ws = nullptr;
+    int rc = ws_reserve(need, s, &ws);
+    if (rc) return rc;
+    int phases = (flags & (BRX_FWD_PHASE_A | BRX_FWD_PHASE_B)) >> 2;
+    if (phases == 0) phases = 3;
+    return run_forward(p, a, decode, phases, ws, g_ws.bytes, s);
 }
 
 static int check_forward_common(const brx_layer_desc* d, brx_pool* p, const void* x) {
@@ -395,6 +401,67 @@ int brx_moe_forward_pairs(const brx_layer_desc* d, brx_pool* p, const void* x, i
     if (shared_expert && ((uintptr_t)shared_expert & 15)) return fail(BRX_EINVAL, "shared expert must be 16-byte aligned");
     return forward_impl(d, p, x, T, n_pairs, pair_expert, pair_token, pair_row, n_rows, nullptr, shared_expert, nullptr,
                         nullptr, y_rows, flags, stream);
+}
+
+int brx_moe_block_forward(const brx_layer_desc* d, brx_pool* p, const void* x, const void* w_router,
+                          const float* router_bias, const void* shared_gate_w, const void* shared_expert,
+                          int T, void* out, int32_t* out_idx, float* out_w, unsigned flags, void* stream) {
+    int rc = check_forward_common(d, p, x);
+    if (rc) return rc;
+    if (T < 0) return fail(BRX_EINVAL, "T %d < 0", T);
+    if (T == 0) return BRX_OK;
+    if (!w_router || !out) return fail(BRX_EINVAL, "w_router and out are required");
+    if ((uintptr_t)w_router & 15) return fail(BRX_EINVAL, "w_router must be 16-byte aligned");
+    if ((uintptr_t)out & 3) return fail(BRX_EINVAL, "out must be 4-byte aligned");
+    if (!shared_gate_w != !shared_expert)
+        return fail(BRX_EINVAL, "shared_gate_w and shared_expert go together");
+    if (shared_expert && !d->shared_inter) return fail(BRX_EINVAL, "layer descriptor has no shared expert");
+    if (shared_expert && (((uintptr_t)shared_expert | (uintptr_t)shared_gate_w) & 15))
+        return fail(BRX_EINVAL, "shared expert and shared_gate_w must be 16-byte aligned");
+    const bool force_dec = flags & BRX_FWD_FORCE_DECODE, force_pf = flags & BRX_FWD_FORCE_PREFILL;
+    if (force_dec && force_pf) return fail(BRX_EINVAL, "FORCE_DECODE and FORCE_PREFILL are exclusive");
+    const unsigned phase_bits = flags & (BRX_FWD_PHASE_R | BRX_FWD_PHASE_A | BRX_FWD_PHASE_B);
+    const bool do_route = !phase_bits || (flags & BRX_FWD_PHASE_R);
+    int phases = phase_bits ? (int)((flags & (BRX_FWD_PHASE_A | BRX_FWD_PHASE_B)) >> 2) : 3;
+    const bool decode = force_dec || (!force_pf && T <= 8);
+    if (decode && T > 8) return fail(BRX_EINVAL, "the decode path takes at most 8 tokens (T=%d)", T);
+    const int k = d->top_k, P = T * k;
+    hipStream_t s = (hipStream_t)stream;
+
+    // one workspace for the whole block: routing first, then the expert kernels' scratch
+    const size_t logits_b = align256(sizeof(float) * (size_t)T * (d->n_experts + 1));
+    const size_t idx_b = out_idx ? 0 : align256(sizeof(int32_t) * P);
+    const size_t w_b = out_w ? 0 : align256(sizeof(float) * P);
+    const size_t sg_b = shared_expert ? align256(sizeof(float) * T) : 0;
+    const size_t route_b = logits_b + idx_b + w_b + sg_b;
+    FwdArgs a = make_args(d, p, x, T, P, nullptr, nullptr, nullptr, P, nullptr, shared_expert, nullptr, out,
+                          nullptr);
+    const size_t fwd_b = decode ? decode_workspace_bytes(a) : prefill_workspace_bytes(a);
+    void* ws = nullptr;
+    if ((rc = ws_reserve(route_b + fwd_b, s, &ws))) return rc;
+    char* base = (char*)ws;
+    float* logits = (float*)base;
+    int32_t* ridx = out_idx ? out_idx : (int32_t*)(base + logits_b);
+    float* rw = out_w ? out_w : (float*)(base + logits_b + idx_b);
+    float* rsg = shared_expert ? (float*)(base + logits_b + idx_b + w_b) : nullptr;
+    void* fws = base + route_b;
+    a.pexp = ridx;
+    a.w = rw;
+    a.sgate = rsg;
+    hipError_t e = hipSuccess;
+    if (decode) {
+        if (do_route) e = launch_router_logits(*d, x, w_router, router_bias, shared_gate_w, T, logits, s);
+        a.logits = logits;
+        a.route_idx = ridx;
+        a.route_w = rw;
+        a.route_sg = rsg;
+    } else if (do_route) {
+        e = launch_router(*d, x, w_router, router_bias, shared_gate_w, T, ridx, rw, rsg,
+                          T <= 64 ? logits : nullptr, s);
+    }
+    if (e != hipSuccess) return hip_fail(e, "router launch");
+    if (!phases) return BRX_OK;
+    return run_forward(p, a, decode, phases, fws, g_ws.bytes - route_b, s);
 }
 
 int brx_combine(const brx_layer_desc* d, const void* y_routed, const float* w, const void* y_shared,

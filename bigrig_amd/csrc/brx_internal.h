@@ -71,6 +71,14 @@ struct FwdArgs {
     uint16_t* out;              // [T, H] bf16 or null
     uint16_t* yun;              // [yrows, H] bf16 or null (token mode: [T, k, H])
     int32_t yrows;              // rows of yun
+    // routed in-kernel (decode of a whole MoE block): the gate/up kernel ranks `logits`
+    // [T, E + 1] itself and its first block publishes the routing through these, which then
+    // alias pexp / w / sgate for the down kernel
+    const float* logits;        // or null: routing comes in through pexp / w
+    int32_t route_mode;
+    int32_t* route_idx;         // [T, k]
+    float* route_w;             // [T, k]
+    float* route_sg;            // [T] or null
 };
 
 // Token row of pair p, and the row its result is written to; explicit lists are clamped so a
@@ -126,6 +134,95 @@ __device__ __forceinline__ float act_apply(int act, float g, float u, float alph
     return g / (1.0f + expf(-alpha * g)) * (u + 1.0f);
 }
 
+// ------------------------------------------------------------------ wave reductions (DPP)
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                                                 0xF, 0xF, false));
+}
+__device__ __forceinline__ float readlane_f(float v, int lane) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+// Max over the 64 lanes of a wave, returned to every lane: quad_perm [1,0,3,2] and [2,3,0,1],
+// row_half_mirror and row_mirror leave each row of 16 lanes holding its maximum; the four row
+// results are then combined through lane reads.
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v));
+    v = fmaxf(v, dpp_f<0x4E>(v));
+    v = fmaxf(v, dpp_f<0x141>(v));
+    v = fmaxf(v, dpp_f<0x140>(v));
+    return fmaxf(fmaxf(readlane_f(v, 0), readlane_f(v, 16)), fmaxf(readlane_f(v, 32), readlane_f(v, 48)));
+}
+
+// Sum over the 64 lanes of a wave by the same pattern, returned to every lane.
+__device__ __forceinline__ float wave_sum(float v) {
+    v += dpp_f<0xB1>(v);
+    v += dpp_f<0x4E>(v);
+    v += dpp_f<0x141>(v);
+    v += dpp_f<0x140>(v);
+    return (readlane_f(v, 0) + readlane_f(v, 16)) + (readlane_f(v, 32) + readlane_f(v, 48));
+}
+
+// Top-k of E <= 64 * kPer logits held by one wave (lane l holds expert l + 64 i in v[i]):
+// descending by value, ties to the lower expert id -- the order the oracle's selection loop
+// defines. k rounds of (wave max, lowest id holding it); after the call lane r < k holds rank
+// r's expert and logit.
+template <int kPer>
+__device__ __forceinline__ void wave_topk(const float v[kPer], int E, int k, int& sel_e, float& sel_v) {
+    const int lane = threadIdx.x & (kWave - 1);
+    bool live[kPer];
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) live[i] = lane + kWave * i < E;
+    sel_e = -1;
+    sel_v = 0.0f;
+    for (int r = 0; r < k; ++r) {
+        float lm = -__builtin_inff();
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) lm = live[i] ? fmaxf(lm, v[i]) : lm;
+        const float mx = wave_max(lm);
+        int pick = -1;
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const uint64_t b = __ballot(live[i] && v[i] == mx);
+            if (pick < 0 && b) pick = kWave * i + __builtin_ctzll(b);
+        }
+        if (pick < 0) {   // only NaN left: the lowest live id, as a strict > comparison would
+#pragma unroll
+            for (int i = 0; i < kPer; ++i) {
+                const uint64_t b = __ballot(live[i]);
+                if (pick < 0 && b) pick = kWave * i + __builtin_ctzll(b);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < kPer; ++i)
+            if (lane + kWave * i == pick) live[i] = false;
+        if (lane == r) {
+            sel_e = pick;
+            sel_v = pick >= 0 ? mx : 0.0f;
+        }
+    }
+}
+
+// Routing weight of the rank this lane holds (lanes >= k return 0): softmax over all E logits
+// then the selected entries (renormalised to sum 1 for BRX_ROUTE_SOFTMAX_TOPK_RENORM), or a
+// softmax over the k selected logits (BRX_ROUTE_TOPK_SOFTMAX).
+template <int kPer>
+__device__ __forceinline__ float wave_route_weight(const float v[kPer], int E, int k, int mode,
+                                                   float sel_v) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const float m = readlane_f(sel_v, 0);
+    const float ex = lane < k ? expf(sel_v - m) : 0.0f;
+    if (mode == BRX_ROUTE_TOPK_SOFTMAX) return ex / wave_sum(ex);
+    float part = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i)
+        if (lane + kWave * i < E) part += expf(v[i] - m);
+    float w = ex / wave_sum(part);
+    if (mode == BRX_ROUTE_SOFTMAX_TOPK_RENORM) w = w / wave_sum(w);
+    return w;
+}
+
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
@@ -156,9 +253,12 @@ __device__ __forceinline__ void perm8(const uint32_t in[4], uint32_t out[4]) {
 // ------------------------------------------------------------------ launchers
 hipError_t launch_router(const brx_layer_desc& d, const void* x, const void* w_router,
                          const float* bias, const void* sgw, int T, int32_t* out_idx,
-                         float* out_w, float* out_sg, float* ws_logits, unsigned* counter,
-                         hipStream_t s);
+                         float* out_w, float* out_sg, float* ws_logits, hipStream_t s);
 size_t router_workspace_bytes(const brx_layer_desc& d, int T);
+// logits [T, E + 1] only (the shared-gate logit in column E), for T <= 64
+hipError_t launch_router_logits(const brx_layer_desc& d, const void* x, const void* w_router,
+                                const float* bias, const void* sgw, int T, float* logits,
+                                hipStream_t s);
 // phases: bit 0 = first half (gate/up), bit 1 = second half (down + combine)
 hipError_t launch_decode(const FwdArgs& a, void* ws, int phases, hipStream_t s);
 hipError_t launch_prefill(const FwdArgs& a, void* ws, size_t ws_bytes, int phases, hipStream_t s);

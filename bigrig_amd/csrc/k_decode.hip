@@ -16,7 +16,8 @@
 // layer has one, is the last entry and takes every token.
 //
 // A row of K inputs is CPR = K/32 chunks of 16 bytes (32 nibbles); SP consecutive lanes own one
-// row, lane `seg` the 4 consecutive chunks [4 seg, 4 seg + 4). Each wave derives its entry
+// row, lane `seg` the 4 chunks seg + SP j (so each load instruction reads SP adjacent chunks of
+// the row). Each wave derives its entry
 // itself (ballots and lane reads, no LDS and no barrier), then issues every weight, scale and
 // activation load before it waits on any of them, and the SP lane partials of a row are summed
 // by an in-wave xor butterfly: a launch costs the routing read, one slot-table read and one
@@ -59,21 +60,32 @@ struct Entry {
 
 __device__ __forceinline__ int rl(int v, int lane) { return __builtin_amdgcn_readlane(v, lane); }
 
-// Entry u of the step, computed by the calling wave (all results wave-uniform).
-// Returns false when u is past the last entry.
-__device__ __forceinline__ bool plan_entry(const FwdArgs& a, int u, Entry& en, int& n_out) {
+// The slot table as the calling wave holds it: lane l has g2s[l + 64 j] in v[j]. Passed by
+// value and only indexed with constants, so it stays in registers.
+constexpr int kG = 8;                            // E <= 512
+struct G2S {
+    int v[kG];
+};
+__device__ __forceinline__ G2S load_g2s(const FwdArgs& a) {
     const int lane = threadIdx.x & 63;
-    const int P = a.P;
-    const int emax = a.shared ? a.E : a.E - 1;   // id E names the shared expert
-    // the slot table rides along with the routing read: lane l holds g2s[l + 64 j]
-    constexpr int kG = 8;                        // E <= 512
-    int gt[kG];
+    G2S g;
 #pragma unroll
     for (int j = 0; j < kG; ++j) {
         const int ge = lane + kWave * j;
-        gt[j] = ge < a.E ? a.g2s[ge] : 0;
+        g.v[j] = ge < a.E ? a.g2s[ge] : 0;
     }
-    const int e = lane < P ? min(max(a.pexp[lane], 0), emax) : -1;
+    return g;
+}
+
+// Entry u of the step, computed by the calling wave (all results wave-uniform) from the
+// lane's pair expert `e_raw` (lanes < P) and the slot table. Returns false when u is past the
+// last entry.
+__device__ __forceinline__ bool plan_entry(const FwdArgs& a, int u, int e_raw, const G2S gt,
+                                           Entry& en, int& n_out) {
+    const int lane = threadIdx.x & 63;
+    const int P = a.P;
+    const int emax = a.shared ? a.E : a.E - 1;   // id E names the shared expert
+    const int e = lane < P ? min(max(e_raw, 0), emax) : -1;
     int occ = 0;
     for (int q = 0; q < P; ++q) occ += (q < lane && rl(e, q) == e) ? 1 : 0;
     const bool lead = lane < P && (occ % kMaxTok) == 0;
@@ -95,9 +107,9 @@ __device__ __forceinline__ bool plan_entry(const FwdArgs& a, int u, Entry& en, i
         int s = -1;
         if (eu < a.E) {
             const int gj = eu >> 6;
-            int gv = gt[0];
+            int gv = gt.v[0];
 #pragma unroll
-            for (int j = 1; j < kG; ++j) if (j == gj) gv = gt[j];
+            for (int j = 1; j < kG; ++j) gv = j == gj ? gt.v[j] : gv;
             s = min(max(rl(gv, eu & 63), 0), a.capacity - 1);
         }
         en.slot = s;
@@ -109,6 +121,37 @@ __device__ __forceinline__ bool plan_entry(const FwdArgs& a, int u, Entry& en, i
         en.mm = 0;
     }
     return true;
+}
+
+// Routing inside the launch (a whole MoE block in decode): every block ranks the logits of
+// every token itself (wave w takes tokens w, w + 4, ...) into s_e[t * k + r]; the block that
+// `publish`es also writes idx, the routing weights and the shared-expert gate for the down
+// kernel and the caller.
+template <int kPer>
+__device__ __forceinline__ void route_tokens(const FwdArgs& a, int32_t* s_e, bool publish) {
+    const int lane = threadIdx.x & 63;
+    const int E = a.E, k = a.k;
+    for (int t = threadIdx.x >> 6; t < a.T; t += kThreads / kWave) {
+        const float* l = a.logits + (int64_t)t * (E + 1);
+        float v[kPer];
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const int e = lane + kWave * i;
+            v[i] = e < E ? l[e] : 0.0f;
+        }
+        int sel_e;
+        float sel_v;
+        wave_topk<kPer>(v, E, k, sel_e, sel_v);
+        if (lane < k) s_e[t * k + lane] = sel_e;
+        if (publish) {
+            const float w = wave_route_weight<kPer>(v, E, k, a.route_mode, sel_v);
+            if (lane < k) {
+                a.route_idx[t * k + lane] = sel_e;
+                a.route_w[t * k + lane] = w;
+            }
+            if (lane == 0 && a.route_sg) a.route_sg[t] = 1.0f / (1.0f + expf(-l[E]));
+        }
+    }
 }
 
 // Walks an entry's pairs in order: next() returns the pair index, tok the token it reads.
@@ -140,40 +183,40 @@ struct Seg {
     float b[kCPS];   // affine: bias - 128 * scale per chunk; mxfp4: unused
 };
 
-// Issue the loads of one row segment (no waiting). Chunks past the row are clamped to its last
-// chunk (loaded and then ignored), so no load sits behind a branch.
-template <int MODE>
-__device__ __forceinline__ void seg_load(const uint8_t* base, const Proj& P, int row, int c0,
+// Issue the loads of one row segment (no waiting): chunks seg + SP * j, j < kCPS, so that the
+// SP lanes of a row read SP consecutive 16-byte chunks per load instruction. Chunks past the
+// row are clamped to its last chunk (loaded and then ignored), so no load sits behind a branch.
+template <int MODE, int SP>
+__device__ __forceinline__ void seg_load(const uint8_t* base, const Proj& P, int row, int seg,
                                          int scale_f16, Seg& sg) {
     const int n_in = P.n_in;
     const int cpr = n_in / 32;
     const uint4* wrow = reinterpret_cast<const uint4*>(base + P.w + (int64_t)row * (n_in / 2));
 #pragma unroll
-    for (int j = 0; j < kCPS; ++j) sg.w[j] = wrow[min(c0 + j, cpr - 1)];
+    for (int j = 0; j < kCPS; ++j) sg.w[j] = wrow[min(seg + SP * j, cpr - 1)];
     if constexpr (MODE == BRX_QUANT_AFFINE) {
         const int G = n_in / 64;
         const uint16_t* sp = reinterpret_cast<const uint16_t*>(base + P.s) + (int64_t)row * G;
         const uint16_t* bp = reinterpret_cast<const uint16_t*>(base + P.b) + (int64_t)row * G;
-        uint32_t sv[kCPS / 2], bv[kCPS / 2];
+        uint32_t sv[kCPS], bv[kCPS];
 #pragma unroll
-        for (int j = 0; j < kCPS / 2; ++j) {
-            const int g = min((c0 >> 1) + j, G - 1);
+        for (int j = 0; j < kCPS; ++j) {
+            const int g = min(seg + SP * j, cpr - 1) >> 1;
             sv[j] = sp[g];
             bv[j] = bp[g];
         }
 #pragma unroll
         for (int j = 0; j < kCPS; ++j) {
-            float s = scale_f16 ? h2f(sv[j >> 1]) : bf2f(sv[j >> 1]);
-            float b = scale_f16 ? h2f(bv[j >> 1]) : bf2f(bv[j >> 1]);
+            float s = scale_f16 ? h2f(sv[j]) : bf2f(sv[j]);
+            float b = scale_f16 ? h2f(bv[j]) : bf2f(bv[j]);
             sg.s[j] = s;
             sg.b[j] = b - 128.0f * s;
         }
     } else {
-        const int G = n_in / 32;
-        const uint8_t* sp = base + P.s + (int64_t)row * G;
+        const uint8_t* sp = base + P.s + (int64_t)row * cpr;
 #pragma unroll
         for (int j = 0; j < kCPS; ++j) {
-            sg.s[j] = e8m0_f32(sp[min(c0 + j, G - 1)]);
+            sg.s[j] = e8m0_f32(sp[min(seg + SP * j, cpr - 1)]);
             sg.b[j] = 0.0f;
         }
     }
@@ -282,13 +325,24 @@ __device__ __forceinline__ int h_pos(int r) {
 // ------------------------------------------------------------------ gate/up
 // Thread t owns row (t / SP) of the block's RB = 256 / SP rows and segment (t % SP), for both
 // the gate and the up projection.
-template <int MODE, int SP>
+template <int MODE, int SP, int KP>
 __global__ __launch_bounds__(kThreads) void k_dec_gateup(FwdArgs a, uint16_t* __restrict__ hbuf,
                                                          int hstride, DecTable* __restrict__ table) {
     constexpr int RB = kThreads / SP;
+    const int lane = threadIdx.x & 63;
+    const G2S gt = load_g2s(a);
+    int e_raw;
+    if constexpr (KP > 0) {   // routed here: KP logits per lane (E <= 64 KP)
+        __shared__ int32_t s_e[kWave];   // P <= 64 pairs
+        route_tokens<KP>(a, s_e, blockIdx.x == 0 && blockIdx.y == 0);
+        __syncthreads();
+        e_raw = lane < a.P ? s_e[lane] : 0;
+    } else {
+        e_raw = lane < a.P ? a.pexp[lane] : 0;
+    }
     Entry en;
     int n;
-    if (!plan_entry(a, blockIdx.y, en, n)) return;
+    if (!plan_entry(a, blockIdx.y, e_raw, gt, en, n)) return;
     const int tid = threadIdx.x;
     if (blockIdx.x == 0 && tid == 0) {        // the entry table for the down kernel
         DecEntry& d = table->ent[blockIdx.y];
@@ -310,12 +364,10 @@ __global__ __launch_bounds__(kThreads) void k_dec_gateup(FwdArgs a, uint16_t* __
     const int H = a.H, CPR = H / 32;
     const int rr = tid / SP, seg = tid % SP;
     const int row = min(r0 + rr, inter - 1);
-    const int c0 = seg * kCPS;
-    const int nvalid = min(kCPS, CPR - c0);     // <= 0 for padding lanes
 
     Seg g, v;
-    seg_load<MODE>(base, L.p[0], row, min(c0, CPR - 1), a.scale_f16, g);
-    seg_load<MODE>(base, L.p[1], row, min(c0, CPR - 1), a.scale_f16, v);
+    seg_load<MODE, SP>(base, L.p[0], row, seg, a.scale_f16, g);
+    seg_load<MODE, SP>(base, L.p[1], row, seg, a.scale_f16, v);
     float bg = 0.f, bu = 0.f;
     if (L.p[0].bias >= 0) {
         bg = bf2f(reinterpret_cast<const uint16_t*>(base + L.p[0].bias)[row]);
@@ -330,11 +382,11 @@ __global__ __launch_bounds__(kThreads) void k_dec_gateup(FwdArgs a, uint16_t* __
 #pragma unroll
         for (int j = 0; j < kCPS; ++j)
 #pragma unroll
-            for (int q = 0; q < 4; ++q) xr[j][q] = xp[min(c0 + j, CPR - 1) * 4 + q];
+            for (int q = 0; q < 4; ++q) xr[j][q] = xp[min(seg + SP * j, CPR - 1) * 4 + q];
         float pg = 0.f, pu = 0.f;
 #pragma unroll
         for (int j = 0; j < kCPS; ++j) {
-            if (j < nvalid) {
+            if (seg + SP * j < CPR) {
                 XChunk xc;
                 x_prepare<MODE>(xr[j], xc);
                 pg += chunk_dot<MODE>(g, j, xc);
@@ -377,10 +429,9 @@ __global__ __launch_bounds__(kThreads) void k_dec_down(FwdArgs a, const uint16_t
         const int nt = valid ? d.nt : 0;
         const uint8_t* base = slot_base(a, slot);
         const Layout& L = slot < 0 ? a.lay_sh : a.lay;
-        const int c0 = min(seg * kCPS, CPR - 1);
-        const int nvalid = valid ? min(kCPS, CPR - seg * kCPS) : 0;
+        const int sg0 = min(seg, SP - 1);
         Seg sg;
-        seg_load<MODE>(base, L.p[2], n0 + rr, c0, a.scale_f16, sg);
+        seg_load<MODE, SP>(base, L.p[2], n0 + rr, sg0, a.scale_f16, sg);
         // the SP lanes of one (entry, row) share nt; lanes past W have nt = 0 and only take
         // part in the shuffles
         int ntg = nt;
@@ -393,11 +444,11 @@ __global__ __launch_bounds__(kThreads) void k_dec_down(FwdArgs a, const uint16_t
 #pragma unroll
             for (int j = 0; j < kCPS; ++j)
 #pragma unroll
-                for (int q = 0; q < 4; ++q) hr[j][q] = hp[min(c0 + j, CPR - 1) * 4 + q];
+                for (int q = 0; q < 4; ++q) hr[j][q] = hp[min(sg0 + SP * j, CPR - 1) * 4 + q];
             float p = 0.0f;
 #pragma unroll
             for (int j = 0; j < kCPS; ++j) {
-                if (j < nvalid && i < nt) {
+                if (valid && sg0 + SP * j < CPR && i < nt) {
                     XChunk xc;
                     h_prepare<MODE>(hr[j], xc);
                     p += chunk_dot<MODE>(sg, j, xc);
@@ -449,8 +500,14 @@ template <int MODE, int SP>
 hipError_t launch_gateup(const FwdArgs& a, uint16_t* hbuf, DecTable* table, int nu, int Imax,
                          hipStream_t s) {
     constexpr int RB = kThreads / SP;
-    dim3 grid((Imax + RB - 1) / RB, nu);
-    hipLaunchKernelGGL((k_dec_gateup<MODE, SP>), grid, dim3(kThreads), 0, s, a, hbuf, Imax, table);
+    dim3 grid((Imax + RB - 1) / RB, nu), block(kThreads);
+#define BRX_GU(KP) hipLaunchKernelGGL((k_dec_gateup<MODE, SP, KP>), grid, block, 0, s, a, hbuf, Imax, table)
+    if (!a.logits) BRX_GU(0);
+    else if (a.E <= 64) BRX_GU(1);
+    else if (a.E <= 128) BRX_GU(2);
+    else if (a.E <= 256) BRX_GU(4);
+    else BRX_GU(8);
+#undef BRX_GU
     return hipGetLastError();
 }
 

@@ -94,51 +94,15 @@ __global__ __launch_bounds__(kRouterThreads) void k_router(
     for (int t = wv; t < nt; t += kRouterThreads / kWave) {
         const float* l = lg + t * (E + 1);
         float v[kPer];
-        bool taken[kPer];
 #pragma unroll
         for (int i = 0; i < kPer; ++i) {
             int e = lane + kWave * i;
             v[i] = e < E ? l[e] : 0.0f;
-            taken[i] = e >= E;
         }
-        // rank r's (id, logit) ends up in lane r
-        int my_id = -1;
-        float my_v = 0.0f;
-        for (int r = 0; r < k; ++r) {
-            float bv = 0.0f;
-            int bid = 0x7fffffff;
-#pragma unroll
-            for (int i = 0; i < kPer; ++i) {
-                int e = lane + kWave * i;
-                if (!taken[i] && (bid == 0x7fffffff || v[i] > bv)) { bv = v[i]; bid = e; }
-            }
-#pragma unroll
-            for (int off = 32; off >= 1; off >>= 1) {
-                float ov = __shfl_xor(bv, off, kWave);
-                int oid = __shfl_xor(bid, off, kWave);
-                bool better = (oid != 0x7fffffff) &&
-                              (bid == 0x7fffffff || ov > bv || (ov == bv && oid < bid));
-                if (better) { bv = ov; bid = oid; }
-            }
-            if (lane == r) { my_id = bid; my_v = bv; }
-#pragma unroll
-            for (int i = 0; i < kPer; ++i)
-                if (lane + kWave * i == bid) taken[i] = true;
-        }
-        const float m = __shfl(my_v, 0, kWave);
-        float wt;
-        if (mode == BRX_ROUTE_TOPK_SOFTMAX) {
-            float ex = lane < k ? expf(my_v - m) : 0.0f;
-            wt = ex / wave_sum_xor(ex);
-        } else {
-            float part = 0.0f;
-#pragma unroll
-            for (int i = 0; i < kPer; ++i)
-                if (lane + kWave * i < E) part += expf(v[i] - m);
-            float s = wave_sum_xor(part);
-            wt = lane < k ? expf(my_v - m) / s : 0.0f;
-            if (mode == BRX_ROUTE_SOFTMAX_TOPK_RENORM) wt = wt / wave_sum_xor(wt);
-        }
+        int my_id;
+        float my_v;
+        wave_topk<kPer>(v, E, k, my_id, my_v);
+        const float wt = wave_route_weight<kPer>(v, E, k, mode, my_v);
         const int64_t tt = t0 + t;
         if (lane < k) {
             out_idx[tt * k + lane] = my_id;
@@ -149,109 +113,81 @@ __global__ __launch_bounds__(kRouterThreads) void k_router(
 }
 
 // ---------------------------------------------------------------- small T
-template <int kPer>
-__device__ __forceinline__ void topk_row(const float* __restrict__ l, float* lv, int t, int E, int k,
-                                         int mode, int has_sg, int32_t* __restrict__ out_idx,
-                                         float* __restrict__ out_w, float* __restrict__ out_sg);
-
-// k_router_logits: one wave per (expert row, tile of TT tokens); every load of the wave is
-// issued before the first FMA. Same per-lane chain and butterfly as above. With `counter`
-// set, the last block to finish (device-scope count after a release fence) also ranks the
-// top-k of every token, so a decode step routes in one launch; that block resets the count.
-template <bool WF32, int TT, int kPer>
-__global__ __launch_bounds__(kRouterThreads) void k_router_logits(
+// k_router_logits: one wave per (expert row, tile of TT tokens), WPB waves per block; every
+// load of the wave is issued before the first FMA. Same per-lane chain and butterfly as
+// k_router, so the logits are the same bits.
+template <bool WF32, int TT, int WPB>
+__global__ __launch_bounds__(WPB * kWave) void k_router_logits(
     const uint16_t* __restrict__ x, const void* __restrict__ w, const float* __restrict__ bias,
-    const uint16_t* __restrict__ sgw, int T, int H, int E, float* __restrict__ logits,
-    unsigned* __restrict__ counter, int k, int mode, int32_t* __restrict__ out_idx,
-    float* __restrict__ out_w, float* __restrict__ out_sg) {
+    const uint16_t* __restrict__ sgw, int T, int H, int E, float* __restrict__ logits) {
     constexpr int kNJ = 6;                      // chunks per lane: H <= 64 * 8 * 6 = 3072
     const int lane = threadIdx.x & 63;
-    const int r = blockIdx.x * (kRouterThreads / kWave) + (threadIdx.x >> 6);
+    const int r = blockIdx.x * WPB + (threadIdx.x >> 6);
     const int rows = E + (sgw ? 1 : 0);
     const int t0 = blockIdx.y * TT;
     const int nt = min(TT, T - t0);
     const int nch = H / 8;
-    if (r < rows) {
-        const bool wf32 = WF32 && r < E;
-        uint4 wv[kNJ][2];
-        uint4 xv[TT][kNJ];
+    if (r >= rows) return;
+    const bool wf32 = WF32 && r < E;
+    uint4 wv[kNJ][2];
+    uint4 xv[TT][kNJ];
+#pragma unroll
+    for (int j = 0; j < kNJ; ++j) {
+        const int c = lane + kWave * j;
+        if (c < nch) {
+            if (wf32) {
+                const uint4* p = reinterpret_cast<const uint4*>(
+                    reinterpret_cast<const float*>(w) + (int64_t)r * H + 8 * c);
+                wv[j][0] = p[0];
+                wv[j][1] = p[1];
+            } else {
+                const uint16_t* src = r < E ? reinterpret_cast<const uint16_t*>(w) + (int64_t)r * H : sgw;
+                wv[j][0] = *reinterpret_cast<const uint4*>(src + 8 * c);
+            }
+#pragma unroll
+            for (int t = 0; t < TT; ++t)
+                if (t < nt) xv[t][j] = *reinterpret_cast<const uint4*>(x + (int64_t)(t0 + t) * H + 8 * c);
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < TT; ++t) {
+        float acc = 0.0f;
 #pragma unroll
         for (int j = 0; j < kNJ; ++j) {
             const int c = lane + kWave * j;
-            if (c < nch) {
+            if (c < nch && t < nt) {
+                uint32_t xw[4] = {xv[t][j].x, xv[t][j].y, xv[t][j].z, xv[t][j].w};
+                float wf[8];
                 if (wf32) {
-                    const uint4* p = reinterpret_cast<const uint4*>(
-                        reinterpret_cast<const float*>(w) + (int64_t)r * H + 8 * c);
-                    wv[j][0] = p[0];
-                    wv[j][1] = p[1];
+                    wf[0] = __uint_as_float(wv[j][0].x); wf[1] = __uint_as_float(wv[j][0].y);
+                    wf[2] = __uint_as_float(wv[j][0].z); wf[3] = __uint_as_float(wv[j][0].w);
+                    wf[4] = __uint_as_float(wv[j][1].x); wf[5] = __uint_as_float(wv[j][1].y);
+                    wf[6] = __uint_as_float(wv[j][1].z); wf[7] = __uint_as_float(wv[j][1].w);
                 } else {
-                    const uint16_t* src = r < E ? reinterpret_cast<const uint16_t*>(w) + (int64_t)r * H : sgw;
-                    wv[j][0] = *reinterpret_cast<const uint4*>(src + 8 * c);
-                }
-#pragma unroll
-                for (int t = 0; t < TT; ++t)
-                    if (t < nt) xv[t][j] = *reinterpret_cast<const uint4*>(x + (int64_t)(t0 + t) * H + 8 * c);
-            }
-        }
-#pragma unroll
-        for (int t = 0; t < TT; ++t) {
-            float acc = 0.0f;
-#pragma unroll
-            for (int j = 0; j < kNJ; ++j) {
-                const int c = lane + kWave * j;
-                if (c < nch && t < nt) {
-                    uint32_t xw[4] = {xv[t][j].x, xv[t][j].y, xv[t][j].z, xv[t][j].w};
-                    float wf[8];
-                    if (wf32) {
-                        wf[0] = __uint_as_float(wv[j][0].x); wf[1] = __uint_as_float(wv[j][0].y);
-                        wf[2] = __uint_as_float(wv[j][0].z); wf[3] = __uint_as_float(wv[j][0].w);
-                        wf[4] = __uint_as_float(wv[j][1].x); wf[5] = __uint_as_float(wv[j][1].y);
-                        wf[6] = __uint_as_float(wv[j][1].z); wf[7] = __uint_as_float(wv[j][1].w);
-                    } else {
-                        uint32_t ww[4] = {wv[j][0].x, wv[j][0].y, wv[j][0].z, wv[j][0].w};
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) {
-                            wf[2 * i] = bf2f(ww[i] & 0xFFFFu);
-                            wf[2 * i + 1] = bf2f(ww[i] >> 16);
-                        }
-                    }
+                    uint32_t ww[4] = {wv[j][0].x, wv[j][0].y, wv[j][0].z, wv[j][0].w};
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
-                        acc = fmaf(bf2f(xw[i] & 0xFFFFu), wf[2 * i], acc);
-                        acc = fmaf(bf2f(xw[i] >> 16), wf[2 * i + 1], acc);
+                        wf[2 * i] = bf2f(ww[i] & 0xFFFFu);
+                        wf[2 * i + 1] = bf2f(ww[i] >> 16);
                     }
                 }
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    acc = fmaf(bf2f(xw[i] & 0xFFFFu), wf[2 * i], acc);
+                    acc = fmaf(bf2f(xw[i] >> 16), wf[2 * i + 1], acc);
+                }
             }
-            float s = wave_sum_xor(acc);
-            if (lane == 0 && t < nt) logits[(int64_t)(t0 + t) * (E + 1) + r] = (r < E && bias) ? s + bias[r] : s;
         }
+        float s = wave_sum_xor(acc);
+        if (lane == 0 && t < nt) logits[(int64_t)(t0 + t) * (E + 1) + r] = (r < E && bias) ? s + bias[r] : s;
     }
-    if (counter == nullptr) return;
-    __shared__ unsigned s_last;
-    __threadfence();                            // release this block's logits
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const unsigned nblk = gridDim.x * gridDim.y;
-        s_last = atomicAdd(counter, 1u) == nblk - 1 ? 1u : 0u;
-    }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();                            // acquire every block's logits
-    if (threadIdx.x == 0) *counter = 0u;
-    __shared__ __attribute__((aligned(16))) float lv[kRouterThreads / kWave][kWave * kPer];
-    const int wv = threadIdx.x >> 6;
-    for (int t = wv; t < T; t += kRouterThreads / kWave)
-        topk_row<kPer>(logits + (int64_t)t * (E + 1), lv[wv], t, E, k, mode, sgw ? 1 : 0, out_idx,
-                       out_w, out_sg);
 }
 
-// Top-k of one token's logits row `l` ([E + 1], the last entry the shared-gate logit) by the
-// calling wave, with `lv` a wave-private LDS row of 64 * kPer floats. Each candidate's rank is
-// counted directly (how many logits beat it: greater, or equal with a lower id), so there is
-// no serial chain of k arg-max reductions; the candidates of rank < k are the top-k in order.
+// Top-k of one token's logits row `l` ([E + 1], the last entry the shared-gate logit) and its
+// routing weights, by the calling wave.
 template <int kPer>
-__device__ __forceinline__ void topk_row(const float* __restrict__ l, float* lv, int t, int E, int k,
-                                         int mode, int has_sg, int32_t* __restrict__ out_idx,
+__device__ __forceinline__ void topk_row(const float* __restrict__ l, int t, int E, int k, int mode,
+                                         int has_sg, int32_t* __restrict__ out_idx,
                                          float* __restrict__ out_w, float* __restrict__ out_sg) {
     const int lane = threadIdx.x & 63;
     float v[kPer];
@@ -259,66 +195,14 @@ __device__ __forceinline__ void topk_row(const float* __restrict__ l, float* lv,
     for (int i = 0; i < kPer; ++i) {
         const int e = lane + kWave * i;
         v[i] = e < E ? l[e] : 0.0f;
-        if (e < E) lv[e] = v[i];
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    int rank[kPer];
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) rank[i] = 0;
-    float m = lv[0];
-    const int E4 = E & ~3;
-    for (int e2 = 0; e2 < E4; e2 += 4) {
-        const float4 q = *reinterpret_cast<const float4*>(&lv[e2]);
-        const float qq[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-        for (int z = 0; z < 4; ++z) {
-            m = fmaxf(m, qq[z]);
-#pragma unroll
-            for (int i = 0; i < kPer; ++i) {
-                const int e = lane + kWave * i;
-                rank[i] += (int)(qq[z] > v[i]) | ((int)(qq[z] == v[i]) & (int)(e2 + z < e));
-            }
-        }
-    }
-    for (int e2 = E4; e2 < E; ++e2) {
-        const float qv = lv[e2];
-        m = fmaxf(m, qv);
-#pragma unroll
-        for (int i = 0; i < kPer; ++i) {
-            const int e = lane + kWave * i;
-            rank[i] += (int)(qv > v[i]) | ((int)(qv == v[i]) & (int)(e2 < e));
-        }
-    }
-    float ex[kPer];
-    float part = 0.f, psel = 0.f;
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-        const int e = lane + kWave * i;
-        const bool in = e < E;
-        const bool sel = in && rank[i] < k;
-        ex[i] = in ? expf(v[i] - m) : 0.f;
-        part += ex[i];
-        psel += sel ? ex[i] : 0.f;
-    }
-    // p = ex / sum(ex) over all experts; topk-softmax normalises over the selected ones only;
-    // the renormalised rule divides p by its sum over the selected ones
-    float scale;
-    if (mode == BRX_ROUTE_TOPK_SOFTMAX) {
-        scale = 1.0f / wave_sum_xor(psel);
-    } else {
-        const float wsum = wave_sum_xor(part);
-        scale = 1.0f / wsum;
-        if (mode == BRX_ROUTE_SOFTMAX_TOPK_RENORM) scale = scale / wave_sum_xor(psel / wsum);
-    }
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-        const int e = lane + kWave * i;
-        if (e < E && rank[i] < k) {
-            out_idx[(int64_t)t * k + rank[i]] = e;
-            out_w[(int64_t)t * k + rank[i]] = ex[i] * scale;
-        }
+    int my_id;
+    float my_v;
+    wave_topk<kPer>(v, E, k, my_id, my_v);
+    const float wt = wave_route_weight<kPer>(v, E, k, mode, my_v);
+    if (lane < k) {
+        out_idx[(int64_t)t * k + lane] = my_id;
+        out_w[(int64_t)t * k + lane] = wt;
     }
     if (lane == 0 && has_sg && out_sg) out_sg[t] = 1.0f / (1.0f + expf(-l[E]));
 }
@@ -328,12 +212,9 @@ template <int kPer>
 __global__ __launch_bounds__(kRouterThreads) void k_router_topk(
     const float* __restrict__ logits, int T, int E, int k, int mode, int has_sg,
     int32_t* __restrict__ out_idx, float* __restrict__ out_w, float* __restrict__ out_sg) {
-    __shared__ __attribute__((aligned(16))) float lv[kRouterThreads / kWave][kWave * kPer];
-    const int wv = threadIdx.x >> 6;
-    const int t = blockIdx.x * (kRouterThreads / kWave) + wv;
+    const int t = blockIdx.x * (kRouterThreads / kWave) + (threadIdx.x >> 6);
     if (t >= T) return;
-    topk_row<kPer>(logits + (int64_t)t * (E + 1), lv[wv], t, E, k, mode, has_sg, out_idx, out_w,
-                   out_sg);
+    topk_row<kPer>(logits + (int64_t)t * (E + 1), t, E, k, mode, has_sg, out_idx, out_w, out_sg);
 }
 
 template <bool WF32, int TPB>
@@ -348,53 +229,55 @@ hipError_t launch_tpb(const brx_layer_desc& d, const void* x, const void* w, con
     return hipGetLastError();
 }
 
+template <bool WF32>
+hipError_t logits_launch(const brx_layer_desc& d, const void* x, const void* w_router, const float* bias,
+                         const void* sgw, int T, float* logits, hipStream_t s) {
+    constexpr int TT = 4, WPB = 1;
+    const int rows = d.n_experts + (sgw ? 1 : 0);
+    dim3 grid((rows + WPB - 1) / WPB, (T + TT - 1) / TT);
+    hipLaunchKernelGGL((k_router_logits<WF32, TT, WPB>), grid, dim3(WPB * kWave), 0, s,
+                       (const uint16_t*)x, w_router, bias, (const uint16_t*)sgw, T, d.hidden,
+                       d.n_experts, logits);
+    return hipGetLastError();
+}
+
+hipError_t topk_launch(const brx_layer_desc& d, int T, int has_sg, const float* logits,
+                       int32_t* out_idx, float* out_w, float* out_sg, hipStream_t s) {
+    const int E = d.n_experts;
+    dim3 grid((T + 3) / 4), block(kRouterThreads);
+#define BRX_TOPK(KP) hipLaunchKernelGGL(k_router_topk<KP>, grid, block, 0, s, logits, T, E, d.top_k, \
+                                        d.route_mode, has_sg, out_idx, out_w, out_sg)
+    if (E <= 64) BRX_TOPK(1);
+    else if (E <= 128) BRX_TOPK(2);
+    else if (E <= 256) BRX_TOPK(4);
+    else BRX_TOPK(8);
+#undef BRX_TOPK
+    return hipGetLastError();
+}
+
 }  // namespace
 
 size_t router_workspace_bytes(const brx_layer_desc& d, int T) {
     return T <= kSmallT ? sizeof(float) * (size_t)T * (d.n_experts + 1) : 0;
 }
 
-template <bool WF32, int KP>
-hipError_t launch_small(const brx_layer_desc& d, const void* x, const void* w_router, const float* bias,
-                        const void* sgw, int T, int32_t* out_idx, float* out_w, float* out_sg,
-                        float* ws_logits, unsigned* counter, hipStream_t s) {
-    constexpr int TT = 4;
-    const int rows = d.n_experts + (sgw ? 1 : 0);
-    dim3 grid((rows + 3) / 4, (T + TT - 1) / TT);
-    // The last-block top-k (counter given) measured slower than a second launch on MI355X:
-    // its device-scope release/acquire fences cost more than the launch they save. Kept off.
-    const bool fused = false && T <= 8 && counter != nullptr;
-    hipLaunchKernelGGL((k_router_logits<WF32, TT, KP>), grid, dim3(kRouterThreads), 0, s,
-                       (const uint16_t*)x, w_router, bias, (const uint16_t*)sgw, T, d.hidden,
-                       d.n_experts, ws_logits, fused ? counter : nullptr, d.top_k, d.route_mode,
-                       out_idx, out_w, out_sg);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess || fused) return e;
-    hipLaunchKernelGGL(k_router_topk<KP>, dim3((T + 3) / 4), dim3(kRouterThreads), 0, s, ws_logits, T,
-                       d.n_experts, d.top_k, d.route_mode, sgw ? 1 : 0, out_idx, out_w, out_sg);
-    return hipGetLastError();
-}
-
-template <bool WF32>
-hipError_t launch_small_e(const brx_layer_desc& d, const void* x, const void* w_router, const float* bias,
-                          const void* sgw, int T, int32_t* out_idx, float* out_w, float* out_sg,
-                          float* ws_logits, unsigned* counter, hipStream_t s) {
-    const int E = d.n_experts;
-    if (E <= 64) return launch_small<WF32, 1>(d, x, w_router, bias, sgw, T, out_idx, out_w, out_sg, ws_logits, counter, s);
-    if (E <= 128) return launch_small<WF32, 2>(d, x, w_router, bias, sgw, T, out_idx, out_w, out_sg, ws_logits, counter, s);
-    if (E <= 256) return launch_small<WF32, 4>(d, x, w_router, bias, sgw, T, out_idx, out_w, out_sg, ws_logits, counter, s);
-    return launch_small<WF32, 8>(d, x, w_router, bias, sgw, T, out_idx, out_w, out_sg, ws_logits, counter, s);
+hipError_t launch_router_logits(const brx_layer_desc& d, const void* x, const void* w_router,
+                                const float* bias, const void* sgw, int T, float* logits,
+                                hipStream_t s) {
+    return d.router_dtype == BRX_DT_F32 ? logits_launch<true>(d, x, w_router, bias, sgw, T, logits, s)
+                                        : logits_launch<false>(d, x, w_router, bias, sgw, T, logits, s);
 }
 
 hipError_t launch_router(const brx_layer_desc& d, const void* x, const void* w_router,
                          const float* bias, const void* sgw, int T, int32_t* out_idx,
-                         float* out_w, float* out_sg, float* ws_logits, unsigned* counter,
-                         hipStream_t s) {
+                         float* out_w, float* out_sg, float* ws_logits, hipStream_t s) {
     if (T <= 0) return hipSuccess;
     const bool f32 = d.router_dtype == BRX_DT_F32;
-    if (T <= kSmallT)
-        return f32 ? launch_small_e<true>(d, x, w_router, bias, sgw, T, out_idx, out_w, out_sg, ws_logits, counter, s)
-                   : launch_small_e<false>(d, x, w_router, bias, sgw, T, out_idx, out_w, out_sg, ws_logits, counter, s);
+    if (T <= kSmallT) {
+        hipError_t e = launch_router_logits(d, x, w_router, bias, sgw, T, ws_logits, s);
+        if (e != hipSuccess) return e;
+        return topk_launch(d, T, sgw ? 1 : 0, ws_logits, out_idx, out_w, out_sg, s);
+    }
     // x staged as fp32: keep TPB * H * 4 within 48 KB of LDS
     if (d.hidden <= 2880) {
         return f32 ? launch_tpb<true, 4>(d, x, w_router, bias, sgw, T, out_idx, out_w, out_sg, s)

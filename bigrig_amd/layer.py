@@ -76,6 +76,23 @@ def moe_forward(spec: LayerSpec, pool: ExpertPool, x2, idx, w=None, shared=None,
         path_flag(T) if flags is None else flags, _stream(stream)))
 
 
+def moe_block(spec: LayerSpec, pool: ExpertPool, x2, router_w, router_bias=None,
+              shared_gate_w=None, shared=None, out=None, out_idx=None, out_w=None, flags=0,
+              stream=None):
+    """The whole MoE block over a fully resident pool: routing, experts, combine (+ shared).
+    Returns out [T, H] bf16; out_idx / out_w, when given, receive the routing used."""
+    import torch
+    T = x2.shape[0]
+    if out is None:
+        out = torch.empty((T, spec.hidden), dtype=torch.bfloat16, device=x2.device)
+    d = spec.desc()
+    L.check(L.load().brx_moe_block_forward(
+        C.byref(d), pool.device.handle, _dptr(x2), _dptr(router_w), _dptr(router_bias),
+        _dptr(shared_gate_w), _dptr(shared), T, _dptr(out), _dptr(out_idx), _dptr(out_w), flags,
+        _stream(stream)))
+    return out
+
+
 def forward_pairs(spec: LayerSpec, pool: ExpertPool, x2, pair_tok, pair_exp, pair_row, y_rows,
                   flags: int, shared=None, stream=None):
     d = spec.desc()
@@ -288,6 +305,15 @@ class MoELayer:
 
     def __call__(self, x, stream=None):
         x2 = x.reshape(-1, self.spec.hidden).contiguous()
+        sw = self.switch
+        if sw._sync_free:
+            # every expert resident: routing, experts and combine in one library call, the
+            # routing never read by the host (stream.py:1377-1394)
+            sw._pool.g2s_device(_stream(stream))   # uploads only if residency changed
+            sgw = self.shared_gate_w if sw.shared is not None else None
+            out = moe_block(self.spec, sw._pool, x2, self.router_w, self.router_bias, sgw,
+                            sw.shared, flags=path_flag(x2.shape[0]), stream=stream)
+            return out.reshape(x.shape)
         idx, w, sg = self.route(x2, stream)
-        out = self.switch.forward_combined(x2, idx, w, sg, stream)
+        out = sw.forward_combined(x2, idx, w, sg, stream)
         return out.reshape(x.shape)

@@ -18,14 +18,14 @@ SCALE_BF16, SCALE_F16 = 0, 1
 ACT_SWIGLU, ACT_SWIGLU_CLAMPED = 0, 1
 ROUTE_SOFTMAX_TOPK, ROUTE_SOFTMAX_TOPK_RENORM, ROUTE_TOPK_SOFTMAX = 0, 1, 2
 DT_F32, DT_BF16 = 0, 1
-FWD_FORCE_DECODE, FWD_FORCE_PREFILL, FWD_PHASE_A, FWD_PHASE_B = 1, 2, 4, 8
+FWD_FORCE_DECODE, FWD_FORCE_PREFILL, FWD_PHASE_A, FWD_PHASE_B, FWD_PHASE_R = 1, 2, 4, 8, 16
 
 EXPORTS = (
     "brx_abi_version", "brx_last_error", "brx_init", "brx_expert_layout_get",
     "brx_pool_create", "brx_pool_destroy", "brx_pool_capacity", "brx_pool_slot_ptr",
     "brx_pool_g2s_ptr", "brx_pool_refill_async", "brx_pool_refill_from_device_async",
     "brx_pool_set_g2s", "brx_pool_sync", "brx_router_topk", "brx_moe_forward",
-    "brx_moe_forward_pairs", "brx_combine", "brx_dequant",
+    "brx_moe_forward_pairs", "brx_moe_block_forward", "brx_combine", "brx_dequant",
     "brx_sort_pairs",
 )
 
@@ -77,6 +77,8 @@ _SIGS = {
                          C.c_uint, _vp], C.c_int),
     "brx_moe_forward_pairs": ([C.POINTER(LayerDesc), _vp, _vp, C.c_int, _vp, _vp, _vp, C.c_int,
                                C.c_int, _vp, _vp, C.c_uint, _vp], C.c_int),
+    "brx_moe_block_forward": ([C.POINTER(LayerDesc), _vp, _vp, _vp, _vp, _vp, _vp, C.c_int, _vp,
+                               _vp, _vp, C.c_uint, _vp], C.c_int),
     "brx_combine": ([C.POINTER(LayerDesc), _vp, _vp, _vp, _vp, C.c_int, _vp, _vp], C.c_int),
     "brx_dequant": ([C.POINTER(LayerDesc), _vp, C.c_int, C.c_int, _vp, _vp], C.c_int),
     "brx_sort_pairs": ([C.POINTER(LayerDesc), _vp, C.c_int, _vp, _vp, _vp], C.c_int),

@@ -157,6 +157,10 @@ int brx_router_topk(const brx_layer_desc* d, const void* x, const void* w_router
  * nothing else using the library in between. Both bits or neither = the whole forward. */
 #define BRX_FWD_PHASE_A       4u
 #define BRX_FWD_PHASE_B       8u
+/* brx_moe_block_forward only: the routing step (router logits for T <= 8, the whole router
+ * otherwise). Any set of PHASE_R / PHASE_A / PHASE_B runs just those steps, in that order, on
+ * the library workspace, under the same rule as PHASE_A / PHASE_B above. */
+#define BRX_FWD_PHASE_R      16u
 
 /* The routed experts of one MoE layer for T tokens, reading expert bytes from the pool's
  * slots through its device table (slot = g2s[expert]):
@@ -189,6 +193,22 @@ int brx_moe_forward_pairs(const brx_layer_desc* d, brx_pool* p, const void* x, i
                           const int32_t* pair_token, const int32_t* pair_expert,
                           const int32_t* pair_row, int n_pairs, int n_rows,
                           const void* shared_expert, void* y_rows, unsigned flags, void* stream);
+
+/* A whole MoE block for T tokens with every expert resident (the reference's sync-free path,
+ * stream.py:1377-1394, where the routing never leaves the device): router top-k as
+ * brx_router_topk, the routed experts and the combine as brx_moe_forward, and an always-on
+ * shared expert gated by sigmoid(x . shared_gate_w) when shared_gate_w/shared_expert are given
+ * (mlx_lm's MoE block around SwitchGLU; stream.py:1523-1525, adapter.py:61-64).
+ *   out [T, H] bf16; out_idx [T, k] int32 and out_w [T, k] fp32 optional (device): the routing
+ *   the block used, the same values brx_router_topk returns.
+ * For T <= 8 (or FORCE_DECODE) the routing is ranked inside the expert kernel, so the block is
+ * three launches; larger T routes first and runs the grouped GEMM. Every expert of the layer
+ * must be resident: the pool's table is read for all E experts. PHASE_R / PHASE_A / PHASE_B
+ * split the block into its routing, first-half and second-half launches (timing). */
+int brx_moe_block_forward(const brx_layer_desc* d, brx_pool* p, const void* x, const void* w_router,
+                          const float* router_bias, const void* shared_gate_w,
+                          const void* shared_expert, int T, void* out, int32_t* out_idx,
+                          float* out_w, unsigned flags, void* stream);
 
 /* The caller's router-weighted combine of unreduced rows (stream.py:1523-1525):
  *   out[t] = bf16( sum_j w[t, j] * y_routed[t, j]  (+ shared_gate[t] * y_shared[t]) )

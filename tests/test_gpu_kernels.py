@@ -120,6 +120,42 @@ def test_prefill_layer(gpu, spec, T):
     pool.close()
 
 
+@pytest.mark.parametrize("spec", [SMALL_AFFINE, SMALL_F16, SMALL_MXFP4, SMALL_SHARED],
+                         ids=["bf16", "f16", "mxfp4", "shared"])
+@pytest.mark.parametrize("T", [1, 5, 8, 40])
+def test_block_forward(gpu, spec, T):
+    """brx_moe_block_forward (routing ranked inside the decode kernel for T <= 8): the routing
+    it reports is the oracle's bit for bit, and the block output matches the oracle layer."""
+    import torch
+    lay = make_layer(spec, seed=13, zipf=0.9)
+    _, sw, pool, _ = build_gpu_layer(lay, gpu)
+    x = make_x(T, spec.hidden, seed=300 + T)
+    xd = to_dev_bits(x, gpu)
+    router = to_dev_bits(lay.router, gpu)
+    bias = None if lay.bias is None else to_dev_bits(lay.bias, gpu)
+    sgw = None if lay.sgate_w is None else to_dev_bits(lay.sgate_w, gpu)
+    gi = torch.full((T, spec.top_k), -1, dtype=torch.int32, device=gpu)
+    gw = torch.zeros((T, spec.top_k), dtype=torch.float32, device=gpu)
+    pool.g2s_device(torch.cuda.current_stream().cuda_stream)
+    out = ops.moe_block(spec, pool, xd, router, bias, sgw, sw.shared, out_idx=gi, out_w=gw,
+                        flags=ops.path_flag(T))
+    torch.cuda.synchronize()
+    _, idx, w, sg = oracle.router(x, lay.router, spec.router_dtype == "float32", lay.bias,
+                                  spec.top_k, spec.route_mode, lay.sgate_w)
+    assert np.array_equal(gi.cpu().numpy(), idx)
+    np.testing.assert_allclose(gw.cpu().numpy(), w, rtol=1e-5, atol=1e-7)
+    ref, _ = oracle.moe_forward(spec, lay.experts, x, idx, w, lay.shared, sg)
+    r = oracle.rel_l2(F.bf16_bits_to_f32(bits(out)), F.bf16_bits_to_f32(ref))
+    assert r < TOL, f"rel L2 vs C oracle {r:.3e}"
+    # the same block through the separate router + expert entry points gives the same bits
+    moe = ops.MoELayer(spec, router, sw, router_bias=bias, shared_gate_w=sgw)
+    sw._sync_free = False
+    out2 = moe(xd)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(out2), bits(out))
+    pool.close()
+
+
 @pytest.mark.parametrize("T", [1, 16])
 def test_unreduced_rows(gpu, T):
     """The operator's unreduced [T, k, H] rows (the reference boundary) against the oracle."""

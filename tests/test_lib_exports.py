@@ -45,7 +45,7 @@ def test_header_enums_match_binding():
                        ("BRX_ACT_SWIGLU_CLAMPED", L.ACT_SWIGLU_CLAMPED),
                        ("BRX_ROUTE_TOPK_SOFTMAX", L.ROUTE_TOPK_SOFTMAX), ("BRX_DT_BF16", L.DT_BF16),
                        ("BRX_FWD_FORCE_PREFILL", L.FWD_FORCE_PREFILL),
-                       ("BRX_FWD_PHASE_B", L.FWD_PHASE_B)):
+                       ("BRX_FWD_PHASE_B", L.FWD_PHASE_B), ("BRX_FWD_PHASE_R", L.FWD_PHASE_R)):
         m = re.search(rf"\b{cname}\s*=\s*(-?\d+)", src) or \
             re.search(rf"#define {cname}\s+\(?(-?\d+)u?", src)
         assert m, cname
