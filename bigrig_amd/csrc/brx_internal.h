@@ -134,6 +134,18 @@ __device__ __forceinline__ float act_apply(int act, float g, float u, float alph
     return g / (1.0f + expf(-alpha * g)) * (u + 1.0f);
 }
 
+// The kernel arguments sit in memory the scalar cache fills on first touch, one 64-byte line
+// at a time. Touching every line of a by-value argument struct at kernel entry brings them all
+// in one round trip, instead of one round trip at each first use of a field deeper in the kernel.
+template <typename T>
+__device__ __forceinline__ void prefetch_args(const T& a) {
+    const uint32_t* p = reinterpret_cast<const uint32_t*>(&a);
+    uint32_t acc = 0;
+#pragma unroll
+    for (int i = 0; i < (int)(sizeof(T) / 4); i += 16) acc ^= p[i];
+    asm volatile("" ::"s"(acc));
+}
+
 // ------------------------------------------------------------------ wave reductions (DPP)
 template <int CTRL>
 __device__ __forceinline__ float dpp_f(float v) {

@@ -8,25 +8,25 @@
 // Two kernels per layer:
 //   k_dec_gateup  grid (row block, expert entry): gate and up rows of one expert for every
 //                 token routed to it, act() in the epilogue, h -> bf16 workspace; its blocks of
-//                 row block 0 also record the entry table the down kernel reads.
+//                 row block 0 also record the entry table the down kernel reads. With the
+//                 layer's router logits given, every block first ranks the top-k itself.
 //   k_dec_down    grid (row block of H): down rows of every entry, each pair's bf16 row result,
 //                 and the k-ordered combine out[t] = sum_j w[t,j] * y[t,j].
 // An entry is a run of at most 8 pairs routed to one expert (so an expert is read once for all
 // the step's tokens that chose it), in order of first appearance; the shared expert, when the
 // layer has one, is the last entry and takes every token.
 //
-// A row of K inputs is CPR = K/32 chunks of 16 bytes (32 nibbles); SP consecutive lanes own one
-// row, lane `seg` the 4 chunks seg + SP j (so each load instruction reads SP adjacent chunks of
-// the row). Each wave derives its entry
-// itself (ballots and lane reads, no LDS and no barrier), then issues every weight, scale and
-// activation load before it waits on any of them, and the SP lane partials of a row are summed
-// by an in-wave xor butterfly: a launch costs the routing read, one slot-table read and one
-// round trip for the weights. Dequant is folded into the dot product: for a chunk with scale s
-// and bias b,
+// A weight row of K inputs is U = K/64 units of 32 bytes (64 nibbles: one affine group with
+// one scale and one bias, or two MXFP4 groups whose two e8m0 scales are one 16-bit load). SP
+// consecutive lanes own a row, lane s the UPL units s + SP j, so each load instruction of a
+// row group reads SP adjacent 32-byte units. The activations a block multiplies (x for
+// gate/up, h for down) are staged once in LDS in the order the dot product wants them, with
+// each unit's sum beside it; the lanes then read them from LDS instead of re-fetching them per
+// row. Dequantization is folded into the dot product: for a unit with scale s and bias b,
 //   sum_i (s q_i + b) x_i = s * sum_i (128 + q_i) x_i + (b - 128 s) * sum_i x_i,
 // where (128 + q_i) is formed as an exact bf16 by bit operations and the products accumulate
-// in fp32 through v_dot2_f32_bf16. For MXFP4 the hardware converts two e2m1 codes to a bf16
-// pair and the e8m0 scale multiplies the chunk sum. A row's value does not depend on which
+// in fp32 through v_dot2_f32_bf16; for MXFP4 the hardware converts two e2m1 codes to a bf16
+// pair and each group's e8m0 scale multiplies its sum. A row's value does not depend on which
 // other rows or tokens share the launch.
 #include "brx_internal.h"
 
@@ -34,13 +34,16 @@ namespace brx {
 namespace {
 
 constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / kWave;
 constexpr int kMaxTok = 8;
 constexpr int kMaxU = 65;     // 64 routed pairs + the shared expert
-constexpr int kCPS = 4;       // chunks per lane segment
+constexpr int kXU = 144;      // LDS bytes per staged activation unit: 64 bf16 + 16 pad
+constexpr int kDownLds = 96 * 1024;   // staged h budget of the down kernel
 
 struct DecEntry {
     int32_t slot;             // pool slot, or -1 for the shared expert
-    int32_t nt;
+    int32_t nt;               // pairs of the entry; 0 marks a grid row past the last entry
+    int32_t pad[2];
     int32_t pair[kMaxTok];    // pair index: p, or P + t for the shared expert
 };
 
@@ -60,27 +63,10 @@ struct Entry {
 
 __device__ __forceinline__ int rl(int v, int lane) { return __builtin_amdgcn_readlane(v, lane); }
 
-// The slot table as the calling wave holds it: lane l has g2s[l + 64 j] in v[j]. Passed by
-// value and only indexed with constants, so it stays in registers.
-constexpr int kG = 8;                            // E <= 512
-struct G2S {
-    int v[kG];
-};
-__device__ __forceinline__ G2S load_g2s(const FwdArgs& a) {
-    const int lane = threadIdx.x & 63;
-    G2S g;
-#pragma unroll
-    for (int j = 0; j < kG; ++j) {
-        const int ge = lane + kWave * j;
-        g.v[j] = ge < a.E ? a.g2s[ge] : 0;
-    }
-    return g;
-}
-
 // Entry u of the step, computed by the calling wave (all results wave-uniform) from the
-// lane's pair expert `e_raw` (lanes < P) and the slot table. Returns false when u is past the
-// last entry.
-__device__ __forceinline__ bool plan_entry(const FwdArgs& a, int u, int e_raw, const G2S gt,
+// lane's pair expert `e_raw` (lanes < P) and the slot table (staged in LDS). Returns false when
+// u is past the last entry.
+__device__ __forceinline__ bool plan_entry(const FwdArgs& a, int u, int e_raw, const int32_t* s_g2s,
                                            Entry& en, int& n_out) {
     const int lane = threadIdx.x & 63;
     const int P = a.P;
@@ -105,13 +91,7 @@ __device__ __forceinline__ bool plan_entry(const FwdArgs& a, int u, int e_raw, c
         en.nt = __popcll(en.mm);
         en.shared = false;
         int s = -1;
-        if (eu < a.E) {
-            const int gj = eu >> 6;
-            int gv = gt.v[0];
-#pragma unroll
-            for (int j = 1; j < kG; ++j) gv = j == gj ? gt.v[j] : gv;
-            s = min(max(rl(gv, eu & 63), 0), a.capacity - 1);
-        }
+        if (eu < a.E) s = min(max(s_g2s[eu], 0), a.capacity - 1);
         en.slot = s;
     } else {
         en.e = a.E;
@@ -124,32 +104,52 @@ __device__ __forceinline__ bool plan_entry(const FwdArgs& a, int u, int e_raw, c
 }
 
 // Routing inside the launch (a whole MoE block in decode): every block ranks the logits of
-// every token itself (wave w takes tokens w, w + 4, ...) into s_e[t * k + r]; the block that
+// every token itself (wave w takes tokens w and w + 4) into s_e[t * k + r]; the block that
 // `publish`es also writes idx, the routing weights and the shared-expert gate for the down
-// kernel and the caller.
+// kernel and the caller. Split into the loads (issued early) and the ranking.
 template <int kPer>
-__device__ __forceinline__ void route_tokens(const FwdArgs& a, int32_t* s_e, bool publish) {
+struct RouteRegs {
+    float v[2][kPer];
+};
+
+template <int kPer>
+__device__ __forceinline__ void route_load(const FwdArgs& a, RouteRegs<kPer>& rg) {
     const int lane = threadIdx.x & 63;
-    const int E = a.E, k = a.k;
-    for (int t = threadIdx.x >> 6; t < a.T; t += kThreads / kWave) {
-        const float* l = a.logits + (int64_t)t * (E + 1);
-        float v[kPer];
+    const int E = a.E;
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+        const int t = (threadIdx.x >> 6) + kWaves * tt;
+        const float* l = a.logits + (int64_t)min(t, a.T - 1) * (E + 1);
 #pragma unroll
         for (int i = 0; i < kPer; ++i) {
             const int e = lane + kWave * i;
-            v[i] = e < E ? l[e] : 0.0f;
+            const float v = l[min(e, E - 1)];   // clamped, branch-free
+            rg.v[tt][i] = e < E ? v : 0.0f;
         }
+    }
+}
+
+template <int kPer>
+__device__ __forceinline__ void route_rank(const FwdArgs& a, const RouteRegs<kPer>& rg, int32_t* s_e,
+                                           bool publish) {
+    const int lane = threadIdx.x & 63;
+    const int E = a.E, k = a.k;
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+        const int t = (threadIdx.x >> 6) + kWaves * tt;
+        if (t >= a.T) break;   // wave-uniform
         int sel_e;
         float sel_v;
-        wave_topk<kPer>(v, E, k, sel_e, sel_v);
+        wave_topk<kPer>(rg.v[tt], E, k, sel_e, sel_v);
         if (lane < k) s_e[t * k + lane] = sel_e;
         if (publish) {
-            const float w = wave_route_weight<kPer>(v, E, k, a.route_mode, sel_v);
+            const float w = wave_route_weight<kPer>(rg.v[tt], E, k, a.route_mode, sel_v);
             if (lane < k) {
                 a.route_idx[t * k + lane] = sel_e;
                 a.route_w[t * k + lane] = w;
             }
-            if (lane == 0 && a.route_sg) a.route_sg[t] = 1.0f / (1.0f + expf(-l[E]));
+            if (lane == 0 && a.route_sg)
+                a.route_sg[t] = 1.0f / (1.0f + expf(-a.logits[(int64_t)t * (E + 1) + E]));
         }
     }
 }
@@ -177,173 +177,236 @@ __device__ __forceinline__ const uint8_t* slot_base(const FwdArgs& a, int slot) 
     return slot >= 0 ? a.slots + (int64_t)slot * a.slot_stride : a.shared;
 }
 
-struct Seg {
-    uint4 w[kCPS];
-    float s[kCPS];   // scale per chunk
-    float b[kCPS];   // affine: bias - 128 * scale per chunk; mxfp4: unused
+
+// ------------------------------------------------------------------ weight units
+template <int MODE, int UPL>
+struct Units {
+    uint4 w[UPL][2];
+    uint32_t s[UPL];   // affine: scale bits; mxfp4: the two e8m0 bytes
+    uint32_t b[UPL];   // affine: bias bits
 };
 
-// Issue the loads of one row segment (no waiting): chunks seg + SP * j, j < kCPS, so that the
-// SP lanes of a row read SP consecutive 16-byte chunks per load instruction. Chunks past the
-// row are clamped to its last chunk (loaded and then ignored), so no load sits behind a branch.
-template <int MODE, int SP>
-__device__ __forceinline__ void seg_load(const uint8_t* base, const Proj& P, int row, int seg,
-                                         int scale_f16, Seg& sg) {
-    const int n_in = P.n_in;
-    const int cpr = n_in / 32;
-    const uint4* wrow = reinterpret_cast<const uint4*>(base + P.w + (int64_t)row * (n_in / 2));
+// Issue the loads of one row's units (no waiting). Units past the row are clamped to its last
+// unit (loaded and then ignored), so no load sits behind a branch.
+template <int MODE, int UPL>
+__device__ __forceinline__ void units_load(const uint8_t* base, const Proj& P, int row, int s, int SP,
+                                           Units<MODE, UPL>& u) {
+    const int U = P.n_in / 64;
+    const uint4* wrow = reinterpret_cast<const uint4*>(base + P.w + (int64_t)row * (P.n_in / 2));
 #pragma unroll
-    for (int j = 0; j < kCPS; ++j) sg.w[j] = wrow[min(seg + SP * j, cpr - 1)];
+    for (int j = 0; j < UPL; ++j) {
+        const int un = min(s + SP * j, U - 1);
+        u.w[j][0] = wrow[2 * un];
+        u.w[j][1] = wrow[2 * un + 1];
+    }
     if constexpr (MODE == BRX_QUANT_AFFINE) {
-        const int G = n_in / 64;
-        const uint16_t* sp = reinterpret_cast<const uint16_t*>(base + P.s) + (int64_t)row * G;
-        const uint16_t* bp = reinterpret_cast<const uint16_t*>(base + P.b) + (int64_t)row * G;
-        uint32_t sv[kCPS], bv[kCPS];
+        const uint16_t* sp = reinterpret_cast<const uint16_t*>(base + P.s) + (int64_t)row * U;
+        const uint16_t* bp = reinterpret_cast<const uint16_t*>(base + P.b) + (int64_t)row * U;
 #pragma unroll
-        for (int j = 0; j < kCPS; ++j) {
-            const int g = min(seg + SP * j, cpr - 1) >> 1;
-            sv[j] = sp[g];
-            bv[j] = bp[g];
-        }
-#pragma unroll
-        for (int j = 0; j < kCPS; ++j) {
-            float s = scale_f16 ? h2f(sv[j]) : bf2f(sv[j]);
-            float b = scale_f16 ? h2f(bv[j]) : bf2f(bv[j]);
-            sg.s[j] = s;
-            sg.b[j] = b - 128.0f * s;
+        for (int j = 0; j < UPL; ++j) {
+            const int un = min(s + SP * j, U - 1);
+            u.s[j] = sp[un];
+            u.b[j] = bp[un];
         }
     } else {
-        const uint8_t* sp = base + P.s + (int64_t)row * cpr;
+        const uint16_t* sp = reinterpret_cast<const uint16_t*>(base + P.s + (int64_t)row * (2 * U));
 #pragma unroll
-        for (int j = 0; j < kCPS; ++j) {
-            sg.s[j] = e8m0_f32(sp[min(seg + SP * j, cpr - 1)]);
-            sg.b[j] = 0.0f;
+        for (int j = 0; j < UPL; ++j) {
+            u.s[j] = sp[min(s + SP * j, U - 1)];
+            u.b[j] = 0u;
         }
     }
 }
 
-// One chunk of activations as the dot needs it.
-struct XChunk {
-    uint32_t w[16];   // affine: pair-permuted (x_i, x_{i+4}) per 8; mxfp4: natural (x_2i, x_2i+1)
-    float sum;        // affine: sum of the 32 values
-};
-
-// From natural-order memory (x): permute for the affine dot, sum the chunk.
-template <int MODE>
-__device__ __forceinline__ void x_prepare(const uint4 raw[4], XChunk& xc) {
+// Dot of unit j with a staged activation unit `xu` (8 pieces of 16 bytes in LDS) whose sum is
+// `xsum` (affine only).
+template <int MODE, int UPL>
+__device__ __forceinline__ float unit_dot(const Units<MODE, UPL>& u, int j, const uint4* xu, float xsum,
+                                          int scale_f16) {
+    const uint32_t wd[8] = {u.w[j][0].x, u.w[j][0].y, u.w[j][0].z, u.w[j][0].w,
+                            u.w[j][1].x, u.w[j][1].y, u.w[j][1].z, u.w[j][1].w};
     if constexpr (MODE == BRX_QUANT_AFFINE) {
-        float s = 0.f;
+        float acc = 0.0f;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            uint32_t in[4] = {raw[q].x, raw[q].y, raw[q].z, raw[q].w}, o[4];
-            perm8(in, o);
-#pragma unroll
-            for (int z = 0; z < 4; ++z) {
-                xc.w[4 * q + z] = o[z];
-                s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, in[z]),
-                                                    __builtin_bit_cast(bf16x2_t, 0x3F803F80u), s,
-                                                    false);
-            }
+        for (int m = 0; m < 8; ++m) {
+            const uint4 xv = xu[m];
+            const uint32_t xp[4] = {xv.x, xv.y, xv.z, xv.w};
+            acc = dot8_q4(wd[m], xp, acc);
         }
-        xc.sum = s;
+        const float sc = scale_f16 ? h2f(u.s[j]) : bf2f(u.s[j]);
+        const float bi = scale_f16 ? h2f(u.b[j]) : bf2f(u.b[j]);
+        return fmaf(sc, acc, (bi - 128.0f * sc) * xsum);
     } else {
+        float a0 = 0.0f, a1 = 0.0f;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            xc.w[4 * q + 0] = raw[q].x;
-            xc.w[4 * q + 1] = raw[q].y;
-            xc.w[4 * q + 2] = raw[q].z;
-            xc.w[4 * q + 3] = raw[q].w;
-        }
-        xc.sum = 0.f;
-    }
-}
-
-// From the h buffer, which is stored in the order the dot needs (see h_pos).
-template <int MODE>
-__device__ __forceinline__ void h_prepare(const uint4 raw[4], XChunk& xc) {
-    float s = 0.f;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        uint32_t in[4] = {raw[q].x, raw[q].y, raw[q].z, raw[q].w};
-#pragma unroll
-        for (int z = 0; z < 4; ++z) {
-            xc.w[4 * q + z] = in[z];
-            if constexpr (MODE == BRX_QUANT_AFFINE)
-                s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, in[z]),
-                                                    __builtin_bit_cast(bf16x2_t, 0x3F803F80u), s,
-                                                    false);
-        }
-    }
-    xc.sum = s;
-}
-
-// Dot of chunk j of a loaded segment with a prepared activation chunk.
-template <int MODE>
-__device__ __forceinline__ float chunk_dot(const Seg& sg, int j, const XChunk& xc) {
-    uint32_t wd[4] = {sg.w[j].x, sg.w[j].y, sg.w[j].z, sg.w[j].w};
-    float acc = 0.0f;
-    if constexpr (MODE == BRX_QUANT_AFFINE) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) acc = dot8_q4(wd[q], xc.w + 4 * q, acc);
-        return fmaf(sg.s[j], acc, sg.b[j] * xc.sum);
-    } else {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const uint32_t v = wd[q];
+        for (int m = 0; m < 8; ++m) {
+            const uint4 xv = xu[m];
+            const uint32_t xp[4] = {xv.x, xv.y, xv.z, xv.w};
+            const uint32_t v = wd[m];
+            float acc = m < 4 ? a0 : a1;
             acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(v, 1.0f, 0),
-                                                  __builtin_bit_cast(bf16x2_t, xc.w[4 * q + 0]), acc, false);
+                                                  __builtin_bit_cast(bf16x2_t, xp[0]), acc, false);
             acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(v, 1.0f, 1),
-                                                  __builtin_bit_cast(bf16x2_t, xc.w[4 * q + 1]), acc, false);
+                                                  __builtin_bit_cast(bf16x2_t, xp[1]), acc, false);
             acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(v, 1.0f, 2),
-                                                  __builtin_bit_cast(bf16x2_t, xc.w[4 * q + 2]), acc, false);
+                                                  __builtin_bit_cast(bf16x2_t, xp[2]), acc, false);
             acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(v, 1.0f, 3),
-                                                  __builtin_bit_cast(bf16x2_t, xc.w[4 * q + 3]), acc, false);
+                                                  __builtin_bit_cast(bf16x2_t, xp[3]), acc, false);
+            if (m < 4) a0 = acc; else a1 = acc;
         }
-        return sg.s[j] * acc;
+        return e8m0_f32(u.s[j] & 0xFFu) * a0 + e8m0_f32(u.s[j] >> 8) * a1;
     }
 }
 
-template <int SP>
-__device__ __forceinline__ float seg_reduce(float v) {
-#pragma unroll
-    for (int off = SP / 2; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+// Sums over aligned groups of 2, 4, 8 and 16 lanes through DPP (quad_perm [1,0,3,2] and
+// [2,3,0,1], row_half_mirror, row_mirror); every lane of the group receives the sum.
+__device__ __forceinline__ float sum8_dpp(float v) {
+    v += dpp_f<0xB1>(v);
+    v += dpp_f<0x4E>(v);
+    v += dpp_f<0x141>(v);
     return v;
 }
 
-// Position of element r of a row in the stored h layout: pair-permuted within 8 for the
-// affine down projection, natural for MXFP4.
+// Sum over the SP consecutive lanes of a row group (SP a power of two, <= 64).
+__device__ __forceinline__ float group_sum(float v, int SP) {
+    if (SP >= 2) v += dpp_f<0xB1>(v);
+    if (SP >= 4) v += dpp_f<0x4E>(v);
+    if (SP >= 8) v += dpp_f<0x141>(v);
+    if (SP >= 16) v += dpp_f<0x140>(v);
+    if (SP >= 32) v += __shfl_xor(v, 16, kWave);
+    if (SP >= 64) v += __shfl_xor(v, 32, kWave);
+    return v;
+}
+
+// ------------------------------------------------------------------ activation staging
+// Stage `nrows` activation rows of K bf16 (row i at src + row_of(i) * K) into LDS as units of
+// 8 pieces (kXU bytes a unit), each piece in the order the dot product wants (affine: pairs
+// (x_i, x_{i+4}); MXFP4: natural), and each unit's sum (affine) in `sums` [nrows][U]. A thread
+// fetches up to kStageB pieces before it waits on any of them. The 8 pieces of a unit are 8
+// consecutive threads, so the unit sum is a fixed 3-step butterfly.
+constexpr int kStageB = 4;
+struct StageRegs {
+    uint4 v[kStageB];
+};
+
+// Issue the loads of slots [base, base + kStageB): branch-free, every address clamped into the
+// rows, so they can be scheduled together with any other loads issued next to them.
+template <typename RowOf>
+__device__ __forceinline__ void stage_issue(const uint16_t* __restrict__ src, int K, int nrows, RowOf row_of,
+                                            int base, StageRegs& st) {
+    const int pcs = (K / 64) * 8;
+    const int per_row = (pcs + kThreads - 1) / kThreads;
+    const int nslots = nrows * per_row;
+#pragma unroll
+    for (int b = 0; b < kStageB; ++b) {
+        const int sl = min(base + b, nslots - 1);       // uniform
+        const int r = sl / per_row;
+        const int pi = min((sl - r * per_row) * kThreads + (int)threadIdx.x, pcs - 1);
+        st.v[b] = *reinterpret_cast<const uint4*>(src + (int64_t)row_of(r) * K + (pi >> 3) * 64 + (pi & 7) * 8);
+    }
+}
+
+// Write the slots [base, base + kStageB) loaded by stage_issue to LDS.
 template <int MODE>
-__device__ __forceinline__ int h_pos(int r) {
-    if constexpr (MODE == BRX_QUANT_AFFINE) {
-        const int m = r & ~7, i = r & 7;
-        return m + (i < 4 ? 2 * i : 2 * (i - 4) + 1);
-    } else {
-        return r;
+__device__ __forceinline__ void stage_store(int K, int nrows, int base, const StageRegs& st, uint8_t* xs,
+                                            float* sums) {
+    const int U = K / 64;
+    const int pcs = U * 8;
+    const int per_row = (pcs + kThreads - 1) / kThreads;
+    const int nslots = nrows * per_row;
+#pragma unroll
+    for (int b = 0; b < kStageB; ++b) {
+        const int sl = base + b;
+        if (sl >= nslots) break;                        // uniform
+        const int r = sl / per_row, pi = (sl - r * per_row) * kThreads + threadIdx.x;
+        const bool ok = pi < pcs;
+        const int un = pi >> 3, q = pi & 7;
+        uint32_t in[4] = {st.v[b].x, st.v[b].y, st.v[b].z, st.v[b].w}, o[4];
+        float part = 0.0f;
+        if constexpr (MODE == BRX_QUANT_AFFINE) {
+            perm8(in, o);
+#pragma unroll
+            for (int z = 0; z < 4; ++z)
+                part = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, in[z]),
+                                                       __builtin_bit_cast(bf16x2_t, 0x3F803F80u), part, false);
+        } else {
+#pragma unroll
+            for (int z = 0; z < 4; ++z) o[z] = in[z];
+        }
+        if (ok)
+            *reinterpret_cast<uint4*>(xs + ((int64_t)r * U + un) * kXU + q * 16) = make_uint4(o[0], o[1], o[2], o[3]);
+        if constexpr (MODE == BRX_QUANT_AFFINE) {
+            part = sum8_dpp(part);
+            if (ok && q == 0) sums[r * U + un] = part;
+        }
+    }
+}
+
+// Stage `nrows` activation rows of K bf16 (row i at src + row_of(i) * K) into LDS as units of
+// 8 pieces (kXU bytes a unit), each piece in the order the dot product wants (affine: pairs
+// (x_i, x_{i+4}); MXFP4: natural), and each unit's sum (affine) in `sums` [nrows][U]. A thread
+// fetches kStageB pieces before it waits on any of them; the 8 pieces of a unit are 8
+// consecutive lanes, so the unit sum is a fixed 3-step DPP butterfly. `first` > 0 skips the
+// slots a caller already staged.
+template <int MODE, typename RowOf>
+__device__ __forceinline__ void stage_rows(const uint16_t* __restrict__ src, int K, int nrows,
+                                           RowOf row_of, uint8_t* xs, float* sums, int first = 0) {
+    const int pcs = (K / 64) * 8;
+    const int nslots = nrows * ((pcs + kThreads - 1) / kThreads);
+    for (int base = first; base < nslots; base += kStageB) {
+        StageRegs st;
+        stage_issue(src, K, nrows, row_of, base, st);
+        stage_store<MODE>(K, nrows, base, st, xs, sums);
     }
 }
 
 // ------------------------------------------------------------------ gate/up
-// Thread t owns row (t / SP) of the block's RB = 256 / SP rows and segment (t % SP), for both
-// the gate and the up projection.
-template <int MODE, int SP, int KP>
+// Wave w of the block owns rows w * RW + g (g = lane / SP, RW = 64 / SP) of the block's
+// RB = 4 RW rows, for both the gate and the up projection.
+template <int MODE, int UPL, int KP>
 __global__ __launch_bounds__(kThreads) void k_dec_gateup(FwdArgs a, uint16_t* __restrict__ hbuf,
-                                                         int hstride, DecTable* __restrict__ table) {
-    constexpr int RB = kThreads / SP;
+                                                         int hstride, DecTable* __restrict__ table,
+                                                         int lsp) {
+    prefetch_args(a);
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    __shared__ int32_t s_e[kWave];   // P <= 64 pairs
+    const int SP = 1 << lsp;
     const int lane = threadIdx.x & 63;
-    const G2S gt = load_g2s(a);
-    int e_raw;
-    if constexpr (KP > 0) {   // routed here: KP logits per lane (E <= 64 KP)
-        __shared__ int32_t s_e[kWave];   // P <= 64 pairs
-        route_tokens<KP>(a, s_e, blockIdx.x == 0 && blockIdx.y == 0);
-        __syncthreads();
-        e_raw = lane < a.P ? s_e[lane] : 0;
-    } else {
-        e_raw = lane < a.P ? a.pexp[lane] : 0;
-    }
+    const int tid = threadIdx.x;
+    const int H = a.H, U = H / 64;
+    uint8_t* xs = lds;
+    float* xsum = reinterpret_cast<float*>(lds + (size_t)a.T * U * kXU);
+    // one round trip for the routing, the slot table and every token's activations: all their
+    // loads are issued branch-free before the first wait; x is staged while the routing is
+    // ranked
+    __shared__ int32_t s_g2s[512];   // E <= 512
+    const int gi0 = min(tid, a.E - 1), gi1 = min(tid + kThreads, a.E - 1);
+    const int g2s0 = a.g2s[gi0], g2s1 = a.g2s[gi1];
+    int pe = 0;
+    if constexpr (KP == 0) pe = a.pexp[min(lane, a.P - 1)];
+    RouteRegs<(KP > 0 ? KP : 1)> rg;
+    if constexpr (KP > 0) route_load<KP>(a, rg);
+    StageRegs st;
+    auto tok_row = [](int i) { return i; };
+    stage_issue(a.x, H, a.T, tok_row, 0, st);
+    if (tid < a.E) s_g2s[tid] = g2s0;
+    if (tid + kThreads < a.E) s_g2s[tid + kThreads] = g2s1;
+    if constexpr (KP == 0)
+        if (tid < a.P) s_e[tid] = pe;
+    stage_store<MODE>(H, a.T, 0, st, xs, xsum);
+    stage_rows<MODE>(a.x, H, a.T, tok_row, xs, xsum, kStageB);
+    if constexpr (KP > 0) route_rank<KP>(a, rg, s_e, blockIdx.x == 0 && blockIdx.y == 0);
+    __syncthreads();
+    const int e_raw = lane < a.P ? s_e[lane] : 0;
     Entry en;
     int n;
-    if (!plan_entry(a, blockIdx.y, e_raw, gt, en, n)) return;
-    const int tid = threadIdx.x;
+    if (!plan_entry(a, blockIdx.y, e_raw, s_g2s, en, n)) {
+        if (blockIdx.x == 0 && tid == 0) {    // no entry here: an empty table row
+            table->ent[blockIdx.y].slot = 0;
+            table->ent[blockIdx.y].nt = 0;
+        }
+        return;
+    }
     if (blockIdx.x == 0 && tid == 0) {        // the entry table for the down kernel
         DecEntry& d = table->ent[blockIdx.y];
         d.slot = en.slot;
@@ -357,17 +420,18 @@ __global__ __launch_bounds__(kThreads) void k_dec_gateup(FwdArgs a, uint16_t* __
     }
     const bool sh = en.e >= a.E;
     const int inter = sh ? a.I_sh : a.I;
-    const int r0 = blockIdx.x * RB;
+    const int RW = kWave >> lsp;
+    const int r0 = blockIdx.x * kWaves * RW;
     if (r0 >= inter) return;
     const Layout& L = sh ? a.lay_sh : a.lay;
     const uint8_t* base = slot_base(a, en.slot);
-    const int H = a.H, CPR = H / 32;
-    const int rr = tid / SP, seg = tid % SP;
+    const int g = lane >> lsp, sl = lane & (SP - 1);
+    const int rr = (tid >> 6) * RW + g;
     const int row = min(r0 + rr, inter - 1);
 
-    Seg g, v;
-    seg_load<MODE, SP>(base, L.p[0], row, seg, a.scale_f16, g);
-    seg_load<MODE, SP>(base, L.p[1], row, seg, a.scale_f16, v);
+    Units<MODE, UPL> ug, uu;
+    units_load<MODE, UPL>(base, L.p[0], row, sl, SP, ug);
+    units_load<MODE, UPL>(base, L.p[1], row, sl, SP, uu);
     float bg = 0.f, bu = 0.f;
     if (L.p[0].bias >= 0) {
         bg = bf2f(reinterpret_cast<const uint16_t*>(base + L.p[0].bias)[row]);
@@ -377,94 +441,40 @@ __global__ __launch_bounds__(kThreads) void k_dec_gateup(FwdArgs a, uint16_t* __
     for (int i = 0; i < en.nt; ++i) {
         int tok;
         const int pair = pit.next(a, en, tok);
-        const uint4* xp = reinterpret_cast<const uint4*>(a.x + (int64_t)tok * H);
-        uint4 xr[kCPS][4];
-#pragma unroll
-        for (int j = 0; j < kCPS; ++j)
-#pragma unroll
-            for (int q = 0; q < 4; ++q) xr[j][q] = xp[min(seg + SP * j, CPR - 1) * 4 + q];
         float pg = 0.f, pu = 0.f;
 #pragma unroll
-        for (int j = 0; j < kCPS; ++j) {
-            if (seg + SP * j < CPR) {
-                XChunk xc;
-                x_prepare<MODE>(xr[j], xc);
-                pg += chunk_dot<MODE>(g, j, xc);
-                pu += chunk_dot<MODE>(v, j, xc);
+        for (int j = 0; j < UPL; ++j) {
+            const int un = sl + SP * j;
+            if (un < U) {
+                const uint4* xu = reinterpret_cast<const uint4*>(xs + ((int64_t)tok * U + un) * kXU);
+                const float sx = MODE == BRX_QUANT_AFFINE ? xsum[tok * U + un] : 0.0f;
+                pg += unit_dot<MODE, UPL>(ug, j, xu, sx, a.scale_f16);
+                pu += unit_dot<MODE, UPL>(uu, j, xu, sx, a.scale_f16);
             }
         }
-        pg = seg_reduce<SP>(pg);
-        pu = seg_reduce<SP>(pu);
-        if (seg == 0 && r0 + rr < inter) {
-            float h = act_apply(a.act, pg + bg, pu + bu, a.alpha, a.limit);
-            hbuf[(int64_t)pair * hstride + h_pos<MODE>(r0 + rr)] = (uint16_t)f2bf(h);
+        pg = group_sum(pg, SP);
+        pu = group_sum(pu, SP);
+        if (sl == 0 && r0 + rr < inter) {
+            const float h = act_apply(a.act, pg + bg, pu + bu, a.alpha, a.limit);
+            hbuf[(int64_t)pair * hstride + r0 + rr] = (uint16_t)f2bf(h);
         }
     }
 }
 
 // ------------------------------------------------------------------ down + combine
-// Items (entry u, row rr, seg) in that order; SP consecutive lanes own one (entry, row).
-template <int MODE, int SP>
-__global__ __launch_bounds__(kThreads) void k_dec_down(FwdArgs a, const uint16_t* __restrict__ hbuf,
-                                                       int RBD, int hstride,
-                                                       const DecTable* __restrict__ table) {
-    extern __shared__ float ys[];         // [PT][RBD]
+// Each pair's row result rounded to bf16 (the projection's output, with its bias), the
+// unreduced rows when asked for, and the k-ordered combine out[t] = sum_j w[t,j] * y[t,j]
+// (+ the gated shared expert): the rows [n0, n0 + RBD) of every pair, ys [PT][RBD] in LDS.
+__device__ __forceinline__ void dec_down_epilogue(const FwdArgs& a, float* ys, int RBD, int lrbd, int n0) {
     const int tid = threadIdx.x;
     const int P = a.P;
     const int PT = P + (a.auto_shared ? a.T : 0);
-    const int I = a.I, CPR = I / 32;
-    const int n0 = blockIdx.x * RBD;
     const int H = a.H;
-    const int n = table->n;
-    const int W = n * RBD * SP;
-    for (int b0 = 0; b0 < W; b0 += kThreads) {
-        const int it = b0 + tid;
-        const bool valid = it < W;
-        const int u = valid ? it / (RBD * SP) : 0;
-        const int rem = it - u * RBD * SP;
-        const int rr = valid ? rem / SP : 0;
-        const int seg = valid ? rem - rr * SP : SP;
-        const DecEntry& d = table->ent[u];
-        const int slot = d.slot;
-        const int nt = valid ? d.nt : 0;
-        const uint8_t* base = slot_base(a, slot);
-        const Layout& L = slot < 0 ? a.lay_sh : a.lay;
-        const int sg0 = min(seg, SP - 1);
-        Seg sg;
-        seg_load<MODE, SP>(base, L.p[2], n0 + rr, sg0, a.scale_f16, sg);
-        // the SP lanes of one (entry, row) share nt; lanes past W have nt = 0 and only take
-        // part in the shuffles
-        int ntg = nt;
-#pragma unroll
-        for (int off = SP / 2; off >= 1; off >>= 1) ntg = max(ntg, __shfl_xor(ntg, off, kWave));
-        for (int i = 0; i < ntg; ++i) {
-            const int pi = d.pair[i < kMaxTok ? i : 0];
-            const uint4* hp = reinterpret_cast<const uint4*>(hbuf + (int64_t)pi * hstride);
-            uint4 hr[kCPS][4];
-#pragma unroll
-            for (int j = 0; j < kCPS; ++j)
-#pragma unroll
-                for (int q = 0; q < 4; ++q) hr[j][q] = hp[min(sg0 + SP * j, CPR - 1) * 4 + q];
-            float p = 0.0f;
-#pragma unroll
-            for (int j = 0; j < kCPS; ++j) {
-                if (valid && sg0 + SP * j < CPR && i < nt) {
-                    XChunk xc;
-                    h_prepare<MODE>(hr[j], xc);
-                    p += chunk_dot<MODE>(sg, j, xc);
-                }
-            }
-            p = seg_reduce<SP>(p);
-            if (valid && seg == 0 && i < nt) ys[pi * RBD + rr] = p;
-        }
-    }
-    __syncthreads();
-
-    // each pair's row result, rounded to bf16 as the projection's output
     for (int it = tid; it < PT * RBD; it += kThreads) {
-        int p = it / RBD, rr = it - p * RBD;
-        float y = ys[it];
+        int p = it >> lrbd, rr = it & (RBD - 1);
         int nn = n0 + rr;
+        if (nn >= H) continue;
+        float y = ys[it];
         if (a.has_bias) {
             int e = p < P ? min(max(a.pexp[p], 0), a.shared ? a.E : a.E - 1) : a.E;
             int s = -1;
@@ -480,7 +490,8 @@ __global__ __launch_bounds__(kThreads) void k_dec_down(FwdArgs a, const uint16_t
 
     if (a.out) {
         for (int it = tid; it < a.T * RBD; it += kThreads) {
-            int t = it / RBD, rr = it - t * RBD;
+            int t = it >> lrbd, rr = it & (RBD - 1);
+            if (n0 + rr >= H) continue;
             float acc = 0.0f;
             for (int j = 0; j < a.k; ++j)
                 acc = fmaf(a.w[t * a.k + j], ys[(t * a.k + j) * RBD + rr], acc);
@@ -490,18 +501,260 @@ __global__ __launch_bounds__(kThreads) void k_dec_down(FwdArgs a, const uint16_t
     }
 }
 
-int pow2ceil(int v) {
-    int p = 1;
-    while (p < v) p <<= 1;
-    return p;
+
+// Items (entry u, row r) of the block's RBD rows: wave w, row group g takes item
+// (pass * 4 + w) * RW + g. The h rows of a batch of entries are staged in LDS first.
+template <int MODE, int UPL>
+__global__ __launch_bounds__(kThreads) void k_dec_down(FwdArgs a, const uint16_t* __restrict__ hbuf,
+                                                       int RBD, int hstride,
+                                                       const DecTable* __restrict__ table, int lsp,
+                                                       int lrbd, int hs_bytes) {
+    prefetch_args(a);
+    const int SP = 1 << lsp;
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int P = a.P;
+    const int PT = P + (a.auto_shared ? a.T : 0);
+    const int Imax = a.I > a.I_sh ? a.I : a.I_sh;
+    const int n0 = blockIdx.x * RBD;
+    const int H = a.H;
+    const int n = table->n;
+    __shared__ int32_t s_pair[kMaxU + kMaxTok];
+    __shared__ int32_t s_first[kMaxU + 1], s_nt[kMaxU + 1], s_slot[kMaxU + 1];
+    float* ys = reinterpret_cast<float*>(lds);                         // [PT][RBD]
+    uint8_t* hs = lds + (((size_t)PT * RBD * 4 + 15) & ~(size_t)15);  // staged h
+    const int RW = kWave >> lsp;
+    const int g = lane >> lsp, sl = lane & (SP - 1);
+    const int Umax = Imax / 64;
+
+    // the table in one parallel read: wave 0 takes the entries' pair counts and slots and scans
+    // the counts (s_first[u] = staged row of entry u's first pair); every thread holds up to
+    // three (entry, i) pair ids until the scan is known, then files them as s_pair[row]
+    // Every read of the table is issued at once and masked by n afterwards (all indices are in
+    // bounds of the table whatever n is), together with this row group's first item's slot and,
+    // when every pair's h row fits in LDS, the h rows themselves (staged row = pair id): one
+    // round trip. The first item's weights are then requested before the scan and the barriers.
+    constexpr int kQ = (kMaxU * kMaxTok + kThreads - 1) / kThreads;
+    int qp[kQ];
+#pragma unroll
+    for (int z = 0; z < kQ; ++z) {
+        const int q = min(tid + kThreads * z, kMaxU * kMaxTok - 1);
+        qp[z] = table->ent[q / kMaxTok].pair[q % kMaxTok];
+    }
+    int nt0 = 0, sl0 = 0, nt64 = 0, sl64 = 0;
+    if (tid < kWave) {
+        nt0 = table->ent[tid].nt;
+        sl0 = table->ent[tid].slot;
+        nt64 = table->ent[kWave].nt;
+        sl64 = table->ent[kWave].slot;
+    }
+    const int it_first = (tid >> 6) * RW + g;
+    const int slot_first = table->ent[min(it_first >> lrbd, kMaxU - 1)].slot;
+    const bool all_fit = (size_t)PT * Umax * (kXU + 4) <= (size_t)hs_bytes;
+    float* hsum_all = reinterpret_cast<float*>(hs + (size_t)PT * Umax * kXU);
+    if (all_fit) stage_rows<MODE>(hbuf, hstride, PT, [](int i) { return i; }, hs, hsum_all);
+    Units<MODE, UPL> ud;
+    const bool have_first = all_fit;
+    if (have_first) {
+        // an item past the last entry reads a stale table slot: point it at slot 0 instead
+        int sf = (it_first >> lrbd) < n ? slot_first : 0;
+        sf = min(max(sf, a.shared ? -1 : 0), a.capacity - 1);
+        const Layout& L = sf < 0 ? a.lay_sh : a.lay;
+        units_load<MODE, UPL>(slot_base(a, sf), L.p[2], min(n0 + (it_first & (RBD - 1)), H - 1), sl, SP, ud);
+    }
+    if (tid < kWave) {
+        nt0 = tid < n ? nt0 : 0;
+        sl0 = tid < n ? sl0 : 0;
+        const bool has64 = n > kWave;
+        nt64 = has64 ? nt64 : 0;
+        sl64 = has64 ? sl64 : 0;
+        int inc = nt0;
+        for (int off = 1; off < kWave; off <<= 1) {
+            const int v = __shfl_up(inc, off, kWave);
+            if (lane >= off) inc += v;
+        }
+        const int tot0 = __shfl(inc, kWave - 1, kWave);
+        s_first[tid] = inc - nt0;
+        s_nt[tid] = nt0;
+        s_slot[tid] = sl0;
+        if (tid == 0) {   // entry 64 exists only with 64 routed pairs and the shared expert
+            s_first[kWave] = tot0;
+            s_nt[kWave] = nt64;
+            s_slot[kWave] = sl64;
+            s_first[kWave + 1] = tot0 + nt64;
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int z = 0; z < kQ; ++z) {
+        const int q = tid + kThreads * z;
+        const int u = q / kMaxTok, i = q - u * kMaxTok;
+        if (q < n * kMaxTok && i < s_nt[u]) s_pair[s_first[u] + i] = qp[z];
+    }
+    __syncthreads();
+
+    int u0 = 0;
+    while (u0 < n) {
+        // the entries [u0, u1) whose pairs fit the staging budget (at least one entry)
+        int u1 = all_fit ? n : u0 + 1;
+        while (u1 < n && (size_t)(s_first[u1 + 1] - s_first[u0]) * Umax * (kXU + 4) <= (size_t)hs_bytes) ++u1;
+        const int rows = s_first[u1] - s_first[u0];
+        const int row0 = s_first[u0];
+        const int items = (u1 - u0) * RBD;
+        // this row group's item of the first pass: its weights are requested before the h rows
+        // are staged, so the two fetches overlap (already in flight when every row fits)
+        int it = (tid >> 6) * RW + g;
+        bool valid = it < items;
+        int iu = valid ? it >> lrbd : 0;
+        int r = valid ? it & (RBD - 1) : 0;
+        if (!have_first) {
+            const int slot = s_slot[u0 + iu];
+            const Layout& L = slot < 0 ? a.lay_sh : a.lay;
+            units_load<MODE, UPL>(slot_base(a, slot), L.p[2], min(n0 + r, H - 1), sl, SP, ud);
+        }
+        float* hsum = all_fit ? hsum_all : reinterpret_cast<float*>(hs + (size_t)rows * Umax * kXU);
+        if (!all_fit) {
+            stage_rows<MODE>(hbuf, hstride, rows, [&](int i) { return s_pair[row0 + i]; }, hs, hsum);
+            __syncthreads();
+        }
+        for (int it0 = 0; it0 < items; it0 += kWaves * RW) {
+            if (it0 > 0) {
+                it = it0 + (tid >> 6) * RW + g;
+                valid = it < items;
+                iu = valid ? it >> lrbd : 0;
+                r = valid ? it & (RBD - 1) : 0;
+                const int slot = s_slot[u0 + iu];
+                const Layout& L = slot < 0 ? a.lay_sh : a.lay;
+                units_load<MODE, UPL>(slot_base(a, slot), L.p[2], min(n0 + r, H - 1), sl, SP, ud);
+            }
+            const int u = u0 + iu;
+            const int slot = s_slot[u];
+            const int nt = valid ? s_nt[u] : 0;
+            const int U = (slot < 0 ? a.lay_sh : a.lay).p[2].n_in / 64;
+            const int srow = s_first[u] - row0;   // staged row of the item's first pair (batched)
+            // the SP lanes of one item share nt; lanes past the items have nt = 0 and only take
+            // part in the shuffles
+            int ntg = nt;
+            for (int off = SP >> 1; off >= 1; off >>= 1) ntg = max(ntg, __shfl_xor(ntg, off, kWave));
+            for (int i = 0; i < ntg; ++i) {
+                float p = 0.0f;
+#pragma unroll
+                for (int j = 0; j < UPL; ++j) {
+                    const int un = sl + SP * j;
+                    if (i < nt && un < U) {
+                        const int hr = all_fit ? s_pair[s_first[u] + i] : srow + i;
+                        const uint4* hu = reinterpret_cast<const uint4*>(hs + ((int64_t)hr * Umax + un) * kXU);
+                        const float sx = MODE == BRX_QUANT_AFFINE ? hsum[hr * Umax + un] : 0.0f;
+                        p += unit_dot<MODE, UPL>(ud, j, hu, sx, a.scale_f16);
+                    }
+                }
+                p = group_sum(p, SP);
+                if (valid && sl == 0 && i < nt && n0 + r < H) ys[s_pair[s_first[u] + i] * RBD + r] = p;
+            }
+        }
+        __syncthreads();
+        u0 = u1;
+    }
+
+    dec_down_epilogue(a, ys, RBD, lrbd, n0);
 }
 
-template <int MODE, int SP>
-hipError_t launch_gateup(const FwdArgs& a, uint16_t* hbuf, DecTable* table, int nu, int Imax,
+// The down kernel when the h rows of every pair fit in LDS (every decode step of the shipped
+// shapes): each row group reads its item's table row itself, the h rows are staged by pair id,
+// and the item's weights are requested as soon as its slot is known -- two memory round trips
+// in all, no scan and one barrier before the dot products.
+template <int MODE, int UPL>
+__global__ __launch_bounds__(kThreads) void k_dec_down_fit(FwdArgs a, const uint16_t* __restrict__ hbuf,
+                                                           int RBD, int hstride,
+                                                           const DecTable* __restrict__ table, int lsp,
+                                                           int lrbd, int nu) {
+    prefetch_args(a);
+    const int SP = 1 << lsp;
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int P = a.P;
+    const int PT = P + (a.auto_shared ? a.T : 0);
+    const int Imax = a.I > a.I_sh ? a.I : a.I_sh;
+    const int Umax = Imax / 64;
+    const int n0 = blockIdx.x * RBD;
+    const int H = a.H;
+    float* ys = reinterpret_cast<float*>(lds);                         // [PT][RBD]
+    uint8_t* hs = lds + (((size_t)PT * RBD * 4 + 15) & ~(size_t)15);  // [PT][Umax] units
+    float* hsum = reinterpret_cast<float*>(hs + (size_t)PT * Umax * kXU);
+    const int RW = kWave >> lsp;
+    const int g = lane >> lsp, sl = lane & (SP - 1);
+    const int items = nu * RBD;
+
+    for (int it0 = 0; it0 < items; it0 += kWaves * RW) {
+        const int it = it0 + (tid >> 6) * RW + g;
+        const bool in_range = it < items;
+        const int u = min(it >> lrbd, nu - 1);
+        const int r = it & (RBD - 1);
+        // the item's table row: header and pair ids, three 16-byte loads
+        const uint4* ep = reinterpret_cast<const uint4*>(&table->ent[u]);
+        const uint4 hd = ep[0], p0 = ep[1], p1 = ep[2];
+        if (it0 == 0) {   // h rows of every pair, in the same round trip
+            stage_rows<MODE>(hbuf, hstride, PT, [](int i) { return i; }, hs, hsum);
+        }
+        const int nt = in_range ? (int)hd.y : 0;
+        int slot = nt > 0 ? (int)hd.x : 0;
+        slot = min(max(slot, a.shared ? -1 : 0), a.capacity - 1);
+        const Layout& L = slot < 0 ? a.lay_sh : a.lay;
+        const int U = L.p[2].n_in / 64;
+        Units<MODE, UPL> ud;
+        units_load<MODE, UPL>(slot_base(a, slot), L.p[2], min(n0 + r, H - 1), sl, SP, ud);
+        if (it0 == 0) __syncthreads();
+        const int pr[kMaxTok] = {(int)p0.x, (int)p0.y, (int)p0.z, (int)p0.w,
+                                 (int)p1.x, (int)p1.y, (int)p1.z, (int)p1.w};
+        // the SP lanes of one item share nt; lanes past the items have nt = 0 and only take
+        // part in the sums
+        int ntg = nt;
+        for (int off = SP >> 1; off >= 1; off >>= 1) ntg = max(ntg, __shfl_xor(ntg, off, kWave));
+#pragma unroll
+        for (int i = 0; i < kMaxTok; ++i) {
+            if (i >= ntg) break;
+            const int hr = min(max(pr[i], 0), PT - 1);
+            float p = 0.0f;
+#pragma unroll
+            for (int j = 0; j < UPL; ++j) {
+                const int un = sl + SP * j;
+                if (i < nt && un < U) {
+                    const uint4* hu = reinterpret_cast<const uint4*>(hs + ((int64_t)hr * Umax + un) * kXU);
+                    const float sx = MODE == BRX_QUANT_AFFINE ? hsum[hr * Umax + un] : 0.0f;
+                    p += unit_dot<MODE, UPL>(ud, j, hu, sx, a.scale_f16);
+                }
+            }
+            p = group_sum(p, SP);
+            if (sl == 0 && i < nt && n0 + r < H) ys[hr * RBD + r] = p;
+        }
+    }
+    __syncthreads();
+    dec_down_epilogue(a, ys, RBD, lrbd, n0);
+}
+
+// (SP, UPL) for a row of U units: the fewest lane slots SP * UPL >= U, then the units per lane
+// nearest `pref` (UPL <= 4, SP a power of two <= 64).
+void pick_split(int U, int pref, int& SP, int& UPL) {
+    int best = 1 << 30, bestd = 1 << 30;
+    SP = 64;
+    UPL = 1;
+    for (int sp = 1; sp <= 64; sp <<= 1)
+        for (int upl = 1; upl <= 4; ++upl) {
+            if (sp * upl < U) continue;
+            const int cost = sp * upl, dist = upl > pref ? upl - pref : pref - upl;
+            if (cost < best || (cost == best && dist < bestd)) { best = cost; bestd = dist; SP = sp; UPL = upl; }
+        }
+}
+
+template <int MODE, int UPL>
+hipError_t launch_gateup(const FwdArgs& a, uint16_t* hbuf, DecTable* table, int nu, int Imax, int SP,
                          hipStream_t s) {
-    constexpr int RB = kThreads / SP;
+    const int RB = kWaves * (kWave / SP);
     dim3 grid((Imax + RB - 1) / RB, nu), block(kThreads);
-#define BRX_GU(KP) hipLaunchKernelGGL((k_dec_gateup<MODE, SP, KP>), grid, block, 0, s, a, hbuf, Imax, table)
+    // staged x of up to T tokens
+    const size_t lds = (size_t)a.T * (a.H / 64) * (kXU + 4);
+    const int lsp = __builtin_ctz(SP);
+#define BRX_GU(KP) hipLaunchKernelGGL((k_dec_gateup<MODE, UPL, KP>), grid, block, lds, s, a, hbuf, Imax, table, lsp)
     if (!a.logits) BRX_GU(0);
     else if (a.E <= 64) BRX_GU(1);
     else if (a.E <= 128) BRX_GU(2);
@@ -511,41 +764,34 @@ hipError_t launch_gateup(const FwdArgs& a, uint16_t* hbuf, DecTable* table, int 
     return hipGetLastError();
 }
 
-template <int MODE, int SP>
-hipError_t launch_down(const FwdArgs& a, uint16_t* hbuf, DecTable* table, int nu, int PT, int Imax,
+template <int MODE, int UPL>
+hipError_t launch_down(const FwdArgs& a, uint16_t* hbuf, DecTable* table, int nu, int PT, int Imax, int SP,
                        hipStream_t s) {
+    // rows per block: enough (entry, row) items to give every row group of the 4 waves one
+    const int per_pass = kWaves * (kWave / SP);
     int RBD = 1;
-    while (RBD < 16 && nu * (RBD * 2) * SP <= kThreads && a.H % (RBD * 2) == 0) RBD *= 2;
-    size_t lds = (size_t)PT * RBD * 4;
-    hipLaunchKernelGGL((k_dec_down<MODE, SP>), dim3(a.H / RBD), dim3(kThreads), lds, s, a, hbuf, RBD,
-                       Imax, table);
+    while (RBD < 64 && nu * RBD * 2 <= per_pass && a.H % (RBD * 2) == 0) RBD *= 2;
+    const int Umax = Imax / 64;
+    const size_t need = (size_t)PT * Umax * (kXU + 4);
+    const int hs_bytes = (int)(need < (size_t)kDownLds ? need : (size_t)kDownLds);
+    const size_t ys_b = (((size_t)PT * RBD * 4) + 15) & ~(size_t)15;
+    const size_t lds = ys_b + (size_t)hs_bytes + 16;
+    if (need <= (size_t)kDownLds)
+        hipLaunchKernelGGL((k_dec_down_fit<MODE, UPL>), dim3((a.H + RBD - 1) / RBD), dim3(kThreads), lds, s, a,
+                           hbuf, RBD, Imax, table, __builtin_ctz(SP), __builtin_ctz(RBD), nu);
+    else
+        hipLaunchKernelGGL((k_dec_down<MODE, UPL>), dim3((a.H + RBD - 1) / RBD), dim3(kThreads), lds, s, a, hbuf,
+                           RBD, Imax, table, __builtin_ctz(SP), __builtin_ctz(RBD), hs_bytes);
     return hipGetLastError();
 }
 
-#define BRX_SEG_CASES(FN, ...)                                                   \
+#define BRX_UPL_CASES(FN, ...)                                                   \
     do {                                                                         \
-        if (sp_ == 1) return FN<MODE, 1>(__VA_ARGS__);                           \
-        if (sp_ == 2) return FN<MODE, 2>(__VA_ARGS__);                           \
-        if (sp_ == 4) return FN<MODE, 4>(__VA_ARGS__);                           \
-        if (sp_ == 8) return FN<MODE, 8>(__VA_ARGS__);                           \
-        if (sp_ == 16) return FN<MODE, 16>(__VA_ARGS__);                         \
-        if (sp_ == 32) return FN<MODE, 32>(__VA_ARGS__);                         \
-        return hipErrorInvalidValue;                                             \
+        if (upl_ == 1) return FN<MODE, 1>(__VA_ARGS__);                          \
+        if (upl_ == 2) return FN<MODE, 2>(__VA_ARGS__);                          \
+        if (upl_ == 3) return FN<MODE, 3>(__VA_ARGS__);                          \
+        return FN<MODE, 4>(__VA_ARGS__);                                         \
     } while (0)
-
-template <int MODE>
-hipError_t dispatch_gateup(const FwdArgs& a, uint16_t* hbuf, DecTable* table, int nu, int Imax,
-                           hipStream_t s) {
-    const int sp_ = pow2ceil((a.H / 32 + kCPS - 1) / kCPS);
-    BRX_SEG_CASES(launch_gateup, a, hbuf, table, nu, Imax, s);
-}
-
-template <int MODE>
-hipError_t dispatch_down(const FwdArgs& a, uint16_t* hbuf, DecTable* table, int nu, int PT, int Imax,
-                         hipStream_t s) {
-    const int sp_ = pow2ceil((a.I / 32 + kCPS - 1) / kCPS);
-    BRX_SEG_CASES(launch_down, a, hbuf, table, nu, PT, Imax, s);
-}
 
 template <int MODE>
 hipError_t launch_mode(const FwdArgs& a, uint16_t* hbuf, DecTable* table, int phases, hipStream_t s) {
@@ -554,11 +800,15 @@ hipError_t launch_mode(const FwdArgs& a, uint16_t* hbuf, DecTable* table, int ph
     const int nu = P + (a.auto_shared ? 1 : 0);
     const int Imax = a.I > a.I_sh ? a.I : a.I_sh;
     if (phases & 1) {
-        hipError_t err = dispatch_gateup<MODE>(a, hbuf, table, nu, Imax, s);
+        int SP, upl_;
+        pick_split(a.H / 64, 2, SP, upl_);
+        hipError_t err = [&]() -> hipError_t { BRX_UPL_CASES(launch_gateup, a, hbuf, table, nu, Imax, SP, s); }();
         if (err != hipSuccess) return err;
     }
     if (phases & 2) {
-        hipError_t err = dispatch_down<MODE>(a, hbuf, table, nu, PT, Imax, s);
+        int SP, upl_;
+        pick_split(Imax / 64, 3, SP, upl_);
+        hipError_t err = [&]() -> hipError_t { BRX_UPL_CASES(launch_down, a, hbuf, table, nu, PT, Imax, SP, s); }();
         if (err != hipSuccess) return err;
     }
     return hipSuccess;

@@ -110,6 +110,20 @@ def test_decode_layer(gpu, spec, T):
     pool.close()
 
 
+@pytest.mark.parametrize("spec", [small(QWEN3_30B_A3B, hidden=512, inter=768, n_experts=64, top_k=8),
+                                  small(GPT_OSS_120B, hidden=512, inter=1536, n_experts=32, top_k=4)],
+                         ids=["affine-I768", "mxfp4-I1536"])
+def test_decode_layer_staged_in_batches(gpu, spec):
+    """8 tokens whose h rows do not all fit in LDS: the down kernel stages them entry batch by
+    entry batch."""
+    lay = make_layer(spec, seed=17, bank=8)
+    moe, sw, pool, _ = build_gpu_layer(lay, gpu)
+    pairs = 8 * spec.top_k
+    assert pairs * (spec.inter // 64) * 148 > 96 * 1024
+    _layer_check(lay, moe, 8, seed=170, check_f64=False)
+    pool.close()
+
+
 @pytest.mark.parametrize("spec", [SMALL_AFFINE, SMALL_F16, SMALL_MXFP4, SMALL_SHARED],
                          ids=["bf16", "f16", "mxfp4", "shared"])
 @pytest.mark.parametrize("T", [9, 64, 257])
