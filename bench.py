@@ -213,8 +213,11 @@ def decode_bench(args, st: "Stack"):
     spec_e = spec.expert_spec()
     gu = sum(c["nbytes"] for p in ("gate_proj", "up_proj") for c in spec_e[p].values())
     dn = sum(c["nbytes"] for c in spec_e["down_proj"].values())
-    gu_bytes = k * gu + 2 * H
-    dn_bytes = k * dn + 2 * H + 2 * k * spec.inter
+    E = spec.n_experts
+    # per launch: the selected experts' packed bytes + x, logits, slot table and h written
+    # (gate/up); + h read, out written and the routing weights (down)
+    gu_bytes = k * gu + 2 * H + 4 * (E + 1) + 4 * E + 2 * k * spec.inter
+    dn_bytes = k * dn + 2 * k * spec.inter + 2 * H + 4 * k
     layer_bytes = k * spec.bytes_per_expert + spec.router_bytes + 2 * H * 2
     return {
         "tok_s": tok_s, "ms_per_step": dt / args.steps * 1e3, "graph": bool(graphs),
@@ -459,7 +462,7 @@ def main():
             "frac": _r(dec["gateup_gbs"] / HBM_PEAK_GBS if dec["gateup_gbs"] else None, 4),
             "traffic": traffic,
             "kernel": f"k_dec_gateup, routed in-kernel ({spec.top_k} experts x gate+up, "
-                      f"{dec['gateup_bytes'] / 1e6:.2f} MB per launch)",
+                      f"{dec['gateup_bytes']:,} B per launch)",
             "avg_us": _r(dec["gateup_us"], 3),
         },
         "decode_kernels": {
