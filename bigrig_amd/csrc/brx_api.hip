@@ -456,8 +456,7 @@ int brx_moe_block_forward(const brx_layer_desc* d, brx_pool* p, const void* x, c
         a.route_w = rw;
         a.route_sg = rsg;
     } else if (do_route) {
-        e = launch_router(*d, x, w_router, router_bias, shared_gate_w, T, ridx, rw, rsg,
-                          T <= 64 ? logits : nullptr, s);
+        e = launch_router(*d, x, w_router, router_bias, shared_gate_w, T, ridx, rw, rsg, logits, s);
     }
     if (e != hipSuccess) return hip_fail(e, "router launch");
     if (!phases) return BRX_OK;

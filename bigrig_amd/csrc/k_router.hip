@@ -15,9 +15,7 @@ namespace brx {
 namespace {
 
 constexpr int kRouterThreads = 256;
-constexpr int kMaxE = 512;
-constexpr int kMaxK = 64;  // top-k is held one rank per lane
-constexpr int kSmallT = 64;  // up to this many tokens: logits kernel + top-k kernel
+constexpr int kSmallT = 64;  // up to this many tokens: one wave per (row, 4 tokens); above: token tiles
 
 __device__ __forceinline__ float wave_sum_xor(float v) {
 #pragma unroll
@@ -25,90 +23,109 @@ __device__ __forceinline__ float wave_sum_xor(float v) {
     return v;
 }
 
-template <bool WF32>
-__device__ __forceinline__ void load_w8(const void* w, int64_t row, int H, int c, float out[8]) {
-    if constexpr (WF32) {
-        const float4* p = reinterpret_cast<const float4*>(
-            reinterpret_cast<const float*>(w) + row * H + 8 * c);
-        float4 a = p[0], b = p[1];
-        out[0] = a.x; out[1] = a.y; out[2] = a.z; out[3] = a.w;
-        out[4] = b.x; out[5] = b.y; out[6] = b.z; out[7] = b.w;
-    } else {
-        uint4 v = *reinterpret_cast<const uint4*>(
-            reinterpret_cast<const uint16_t*>(w) + row * H + 8 * c);
-        uint32_t u[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            out[2 * i] = bf2f(u[i] & 0xFFFFu);
-            out[2 * i + 1] = bf2f(u[i] >> 16);
-        }
-    }
-}
-
-// One block: TPB tokens, all E (+1 shared-gate) rows. x staged in LDS as fp32.
-template <bool WF32, int TPB>
-__global__ __launch_bounds__(kRouterThreads) void k_router(
+// ---------------------------------------------------------------- many tokens
+// k_router_tiled: a block takes a tile of TT tokens (staged in LDS as bf16) and a group of
+// rows; each row's weights are loaded once per block and used for all TT tokens. Per token the
+// lane partials follow the same fmaf chain as k_router_logits; the TT partials are reduced by a
+// transposed butterfly that forms exactly the sums of the xor butterfly (strides 32, 16, ...,
+// 1; fp32 addition is commutative, so a[i] + a[i^s] is the same value on both lanes): at
+// stride 32 a lane keeps half of the tokens and sends the other half, at 16 a quarter, and so
+// on, so 16 tokens take 17 exchanges instead of 96. Token tau ends on lanes 4 tau .. 4 tau + 3.
+template <bool WF32, int TT>
+__global__ __launch_bounds__(kRouterThreads) void k_router_tiled(
     const uint16_t* __restrict__ x, const void* __restrict__ w, const float* __restrict__ bias,
-    const uint16_t* __restrict__ sgw, int T, int H, int E, int k, int mode,
-    int32_t* __restrict__ out_idx, float* __restrict__ out_w, float* __restrict__ out_sg) {
-    extern __shared__ float smem[];
-    float* xs = smem;                              // [TPB][H]
-    float* lg = smem + (size_t)TPB * H;            // [TPB][E + 1]
+    const uint16_t* __restrict__ sgw, int T, int H, int E, int rows_per_block, float* __restrict__ logits) {
+    static_assert(TT == 16, "the exchange pattern below is written for 16 tokens");
+    constexpr int kNJ = 6;                      // chunks per lane: H <= 64 * 8 * 6 = 3072
+    extern __shared__ uint4 xs4[];              // [TT][H / 8] chunks of 8 bf16
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int t0 = blockIdx.x * TPB;
-    const int nt = min(TPB, T - t0);
+    const int t0 = blockIdx.x * TT;
+    const int nt = min(TT, T - t0);
     const int nch = H / 8;
-
-    for (int i = tid; i < TPB * H; i += kRouterThreads) {
-        int t = i / H, h = i - t * H;
-        xs[i] = t < nt ? bf2f(x[(int64_t)(t0 + t) * H + h]) : 0.0f;
+    const uint4* x4 = reinterpret_cast<const uint4*>(x);
+    for (int i = tid; i < TT * nch; i += kRouterThreads) {
+        const int t = i / nch, c = i - t * nch;
+        xs4[i] = t < nt ? x4[(int64_t)(t0 + t) * nch + c] : make_uint4(0, 0, 0, 0);
     }
     __syncthreads();
-
     const int rows = E + (sgw ? 1 : 0);
-    for (int r = wv; r < rows; r += kRouterThreads / kWave) {
-        float acc[TPB];
+    const int r_end = min(rows, (int)(blockIdx.y + 1) * rows_per_block);
+    for (int r = blockIdx.y * rows_per_block + wv; r < r_end; r += kRouterThreads / kWave) {
+        const bool wf32 = WF32 && r < E;
+        uint4 wv4[kNJ][2];
 #pragma unroll
-        for (int t = 0; t < TPB; ++t) acc[t] = 0.0f;
-        for (int c = lane; c < nch; c += kWave) {
-            float wv8[8];
-            if (r < E) load_w8<WF32>(w, r, H, c, wv8);
-            else load_w8<false>(sgw, 0, H, c, wv8);
-#pragma unroll
-            for (int t = 0; t < TPB; ++t) {
-                const float* xt = xs + t * H + 8 * c;
-#pragma unroll
-                for (int i = 0; i < 8; ++i) acc[t] = fmaf(xt[i], wv8[i], acc[t]);
+        for (int j = 0; j < kNJ; ++j) {
+            const int c = min(lane + kWave * j, nch - 1);
+            if (wf32) {
+                const uint4* p = reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(w) + (int64_t)r * H + 8 * c);
+                wv4[j][0] = p[0];
+                wv4[j][1] = p[1];
+            } else {
+                const uint16_t* src = r < E ? reinterpret_cast<const uint16_t*>(w) + (int64_t)r * H : sgw;
+                wv4[j][0] = *reinterpret_cast<const uint4*>(src + 8 * c);
+                wv4[j][1] = make_uint4(0, 0, 0, 0);
             }
         }
+        float acc[TT];
 #pragma unroll
-        for (int t = 0; t < TPB; ++t) {
-            float s = wave_sum_xor(acc[t]);
-            if (lane == 0) lg[t * (E + 1) + r] = (r < E && bias) ? s + bias[r] : s;
-        }
-    }
-    __syncthreads();
-
-    // one wave per token: top-k on logits, then the routing weights
-    constexpr int kPer = kMaxE / kWave;
-    for (int t = wv; t < nt; t += kRouterThreads / kWave) {
-        const float* l = lg + t * (E + 1);
-        float v[kPer];
+        for (int t = 0; t < TT; ++t) acc[t] = 0.0f;
 #pragma unroll
-        for (int i = 0; i < kPer; ++i) {
-            int e = lane + kWave * i;
-            v[i] = e < E ? l[e] : 0.0f;
+        for (int j = 0; j < kNJ; ++j) {
+            const int c = lane + kWave * j;
+            if (c >= nch) continue;
+            float wf[8];
+            if (wf32) {
+                wf[0] = __uint_as_float(wv4[j][0].x); wf[1] = __uint_as_float(wv4[j][0].y);
+                wf[2] = __uint_as_float(wv4[j][0].z); wf[3] = __uint_as_float(wv4[j][0].w);
+                wf[4] = __uint_as_float(wv4[j][1].x); wf[5] = __uint_as_float(wv4[j][1].y);
+                wf[6] = __uint_as_float(wv4[j][1].z); wf[7] = __uint_as_float(wv4[j][1].w);
+            } else {
+                const uint32_t ww[4] = {wv4[j][0].x, wv4[j][0].y, wv4[j][0].z, wv4[j][0].w};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    wf[2 * i] = bf2f(ww[i] & 0xFFFFu);
+                    wf[2 * i + 1] = bf2f(ww[i] >> 16);
+                }
+            }
+#pragma unroll
+            for (int t = 0; t < TT; ++t) {
+                const uint4 xv = xs4[t * nch + c];
+                const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    acc[t] = fmaf(bf2f(xw[i] & 0xFFFFu), wf[2 * i], acc[t]);
+                    acc[t] = fmaf(bf2f(xw[i] >> 16), wf[2 * i + 1], acc[t]);
+                }
+            }
         }
-        int my_id;
-        float my_v;
-        wave_topk<kPer>(v, E, k, my_id, my_v);
-        const float wt = wave_route_weight<kPer>(v, E, k, mode, my_v);
-        const int64_t tt = t0 + t;
-        if (lane < k) {
-            out_idx[tt * k + lane] = my_id;
-            out_w[tt * k + lane] = wt;
+        // transposed butterfly: strides 32, 16, 8, 4 halve the tokens a lane keeps
+        const bool b5 = lane & 32, b4 = lane & 16, b3 = lane & 8, b2 = lane & 4;
+        float v8[8], v4[4], v2[2];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float mine = b5 ? acc[8 + i] : acc[i], other = b5 ? acc[i] : acc[8 + i];
+            v8[i] = mine + __shfl_xor(other, 32, kWave);
         }
-        if (lane == 0 && sgw && out_sg) out_sg[tt] = 1.0f / (1.0f + expf(-l[E]));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float mine = b4 ? v8[4 + i] : v8[i], other = b4 ? v8[i] : v8[4 + i];
+            v4[i] = mine + __shfl_xor(other, 16, kWave);
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const float mine = b3 ? v4[2 + i] : v4[i], other = b3 ? v4[i] : v4[2 + i];
+            v2[i] = mine + __shfl_xor(other, 8, kWave);
+        }
+        float v1;
+        {
+            const float mine = b2 ? v2[1] : v2[0], other = b2 ? v2[0] : v2[1];
+            v1 = mine + __shfl_xor(other, 4, kWave);
+        }
+        v1 += __shfl_xor(v1, 2, kWave);
+        v1 += __shfl_xor(v1, 1, kWave);
+        const int tau = lane >> 2;
+        if ((lane & 3) == 0 && tau < nt)
+            logits[(int64_t)(t0 + tau) * (E + 1) + r] = (r < E && bias) ? v1 + bias[r] : v1;
     }
 }
 
@@ -217,18 +234,6 @@ __global__ __launch_bounds__(kRouterThreads) void k_router_topk(
     topk_row<kPer>(logits + (int64_t)t * (E + 1), t, E, k, mode, has_sg, out_idx, out_w, out_sg);
 }
 
-template <bool WF32, int TPB>
-hipError_t launch_tpb(const brx_layer_desc& d, const void* x, const void* w, const float* bias,
-                      const void* sgw, int T, int32_t* out_idx, float* out_w, float* out_sg,
-                      hipStream_t s) {
-    size_t lds = sizeof(float) * ((size_t)TPB * d.hidden + (size_t)TPB * (d.n_experts + 1));
-    dim3 grid((T + TPB - 1) / TPB);
-    hipLaunchKernelGGL((k_router<WF32, TPB>), grid, dim3(kRouterThreads), lds, s,
-                       (const uint16_t*)x, w, bias, (const uint16_t*)sgw, T, d.hidden,
-                       d.n_experts, d.top_k, d.route_mode, out_idx, out_w, out_sg);
-    return hipGetLastError();
-}
-
 template <bool WF32>
 hipError_t logits_launch(const brx_layer_desc& d, const void* x, const void* w_router, const float* bias,
                          const void* sgw, int T, float* logits, hipStream_t s) {
@@ -258,7 +263,7 @@ hipError_t topk_launch(const brx_layer_desc& d, int T, int has_sg, const float* 
 }  // namespace
 
 size_t router_workspace_bytes(const brx_layer_desc& d, int T) {
-    return T <= kSmallT ? sizeof(float) * (size_t)T * (d.n_experts + 1) : 0;
+    return sizeof(float) * (size_t)T * (d.n_experts + 1);
 }
 
 hipError_t launch_router_logits(const brx_layer_desc& d, const void* x, const void* w_router,
@@ -278,13 +283,20 @@ hipError_t launch_router(const brx_layer_desc& d, const void* x, const void* w_r
         if (e != hipSuccess) return e;
         return topk_launch(d, T, sgw ? 1 : 0, ws_logits, out_idx, out_w, out_sg, s);
     }
-    // x staged as fp32: keep TPB * H * 4 within 48 KB of LDS
-    if (d.hidden <= 2880) {
-        return f32 ? launch_tpb<true, 4>(d, x, w_router, bias, sgw, T, out_idx, out_w, out_sg, s)
-                   : launch_tpb<false, 4>(d, x, w_router, bias, sgw, T, out_idx, out_w, out_sg, s);
-    }
-    return f32 ? launch_tpb<true, 1>(d, x, w_router, bias, sgw, T, out_idx, out_w, out_sg, s)
-               : launch_tpb<false, 1>(d, x, w_router, bias, sgw, T, out_idx, out_w, out_sg, s);
+    // many tokens: logits by token tiles, then the same top-k kernel
+    constexpr int TT = 16, RPB = 32;
+    const int rows = d.n_experts + (sgw ? 1 : 0);
+    dim3 grid((T + TT - 1) / TT, (rows + RPB - 1) / RPB);
+    const size_t lds = sizeof(uint16_t) * (size_t)TT * d.hidden;
+    if (f32)
+        hipLaunchKernelGGL((k_router_tiled<true, TT>), grid, dim3(kRouterThreads), lds, s, (const uint16_t*)x,
+                           w_router, bias, (const uint16_t*)sgw, T, d.hidden, d.n_experts, RPB, ws_logits);
+    else
+        hipLaunchKernelGGL((k_router_tiled<false, TT>), grid, dim3(kRouterThreads), lds, s, (const uint16_t*)x,
+                           w_router, bias, (const uint16_t*)sgw, T, d.hidden, d.n_experts, RPB, ws_logits);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    return topk_launch(d, T, sgw ? 1 : 0, ws_logits, out_idx, out_w, out_sg, s);
 }
 
 }  // namespace brx
