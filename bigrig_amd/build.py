@@ -4,7 +4,10 @@
 
 The library is one hipcc invocation over every `csrc/*.hip` file. Packed FP32 instructions are
 disabled for device code (`-Xclang -target-feature -Xclang -packed-fp32-ops`); the host pass
-warns that it does not know that feature, which is harmless.
+warns that it does not know that feature, which is harmless. MFMA accumulators are allocated in
+ordinary VGPRs (`-mllvm -amdgpu-mfma-vgpr-form=1`): with them in AGPRs the register allocator
+rotated the prefill GEMM's accumulators between loop iterations, costing ~190 register copies
+per K step.
 """
 from __future__ import annotations
 
@@ -36,6 +39,7 @@ def build(verbose: bool = False) -> str:
     tmp = LIB + ".tmp"
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
            "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+           "-mllvm", "-amdgpu-mfma-vgpr-form=1",
            "-Wno-unused-command-line-argument", "-I", INCLUDE, "-I", CSRC,
            *srcs, "-o", tmp]
     if verbose:

@@ -6,18 +6,27 @@
 // restores (token, k) order (stream.py:1558-1561, _scatter_unsort 1829-1831), followed by the
 // caller's router-weighted combine (stream.py:1523-1525).
 //
-//   k_bucket     one block per expert: histogram of all pairs, the expert's run offset and
-//                M-tile offset, and the stable (pair-order) compaction of its pairs.
-//   k_pf_gateup  tile = (M tile of one expert's pairs, 64 intermediate features): A rows are
-//                the pairs' token activations gathered from x, B rows are the gate and up
-//                weights of those features dequantized to bf16 in LDS, one 64-wide K step
-//                (= one affine group) at a time; v_mfma_f32_16x16x32_bf16 accumulates fp32;
-//                the epilogue applies act() and stores h (bf16) in bucketed order.
-//   k_pf_down    tile = (M tile, 128 output columns): A = h rows, B = down weights; the
-//                epilogue stores each pair's bf16 row at its (token, k) position.
-//   k_combine    out[t] = sum_j w[t,j] * y[t,j] (+ shared_gate[t] * y_shared[t]), k-ordered.
+//   k_bucket   one block per expert: histogram of all pairs, the expert's run offset and
+//              M-tile offset, the stable (pair-order) compaction of its pairs, and one tile
+//              descriptor {expert, first bucketed row, rows, slot} per 128-row M tile.
+//   k_pf_gemm  grouped GEMM, tile = (M tile of one expert's pairs, 256 columns), one wave
+//              per SIMD.  KIND 0 (gate/up): A rows are the pairs' token activations gathered
+//              from x, B rows the gate and up weights of 128 intermediate features; the
+//              epilogue applies act() and stores h (bf16) in bucketed order.  KIND 1 (down):
+//              A = h rows, B = down weights of 256 output columns; the epilogue stores each
+//              pair's bf16 row at its (token, k) position.  A is staged through LDS, B is
+//              dequantized from 4-bit straight into MFMA operand registers; v_mfma_f32_16x16x32
+//              _bf16 with fp32 accumulators (details at the kernel).
+//   k_combine  out[t] = sum_j w[t,j] * y[t,j] (+ shared_gate[t] * y_shared[t]), k-ordered.
 // Every output element is one MFMA accumulation over K in a fixed K order, so a row's value
 // does not depend on which other pairs share its tile.
+//
+// Blocks are dispatched round-robin over the 8 XCDs (block b runs on XCD b % 8).  The GEMM
+// grids are 1-D and map b to (M tile, N tile) so that an XCD sweeps every N tile of an M
+// tile before the next one: the tile's A rows are read into that XCD's L2 once and reused by
+// all its N tiles.
+#include <type_traits>
+
 #include "brx_internal.h"
 
 namespace brx {
@@ -25,15 +34,17 @@ namespace {
 
 constexpr int kBM = 128;          // pairs per M tile
 constexpr int kBK = 64;           // K step
-constexpr int kLdsRow = 72;       // bf16 per LDS row (64 + 8 pad)
 constexpr int kThreads = 256;
+constexpr int kXcd = 8;
 
 // ------------------------------------------------------------------ bucketing
 __global__ __launch_bounds__(1024) void k_bucket(const int32_t* __restrict__ pexp, int P, int E,
                                                   int E_ext, int T_sh, int BM,
+                                                  const int32_t* __restrict__ g2s, int capacity,
                                                   int32_t* __restrict__ order,
                                                   int32_t* __restrict__ offsets,
-                                                  int32_t* __restrict__ tile_start) {
+                                                  int32_t* __restrict__ tile_start,
+                                                  int4* __restrict__ tinfo) {
     // E_ext = E + 1 when a shared expert exists (id E); T_sh shared pairs follow the P routed
     extern __shared__ int32_t hist[];     // [E_ext]
     __shared__ int32_t wsum[16];
@@ -56,6 +67,7 @@ __global__ __launch_bounds__(1024) void k_bucket(const int32_t* __restrict__ pex
         for (int s = 32; s >= 1; s >>= 1) { off += __shfl_xor(off, s, 64); toff += __shfl_xor(toff, s, 64); }
         if (lane == 0) {
             base_s[0] = off;
+            base_s[1] = toff;
             offsets[e] = off;
             tile_start[e] = toff;
             if (e == E_ext - 1) {
@@ -65,6 +77,13 @@ __global__ __launch_bounds__(1024) void k_bucket(const int32_t* __restrict__ pex
         }
     }
     __syncthreads();
+    if (tinfo) {
+        const int n = hist[e], off = base_s[0], toff = base_s[1];
+        int slot = 0;
+        if (e < E && g2s) slot = min(max(g2s[e], 0), capacity - 1);
+        for (int j = tid; j * BM < n; j += blockDim.x)
+            tinfo[toff + j] = make_int4(e, off + j * BM, min(BM, n - j * BM), slot);
+    }
     int run = base_s[0];
     for (int p0 = 0; p0 < P_ext; p0 += blockDim.x) {
         int p = p0 + tid;
@@ -84,267 +103,366 @@ __global__ __launch_bounds__(1024) void k_bucket(const int32_t* __restrict__ pex
     }
 }
 
-__device__ __forceinline__ const uint8_t* pf_expert_base(const FwdArgs& a, int e) {
-    if (e >= a.E) return a.shared;
-    int s = a.g2s[e];
-    s = min(max(s, 0), a.capacity - 1);
-    return a.slots + (int64_t)s * a.slot_stride;
-}
-
-// M tile -> (expert, first bucketed row, valid rows); false if past the last tile.
-__device__ __forceinline__ bool find_tile(const int32_t* tile_start, const int32_t* offsets,
-                                          int E_ext, int mt, int& e, int& m0, int& rows) {
-    if (mt >= tile_start[E_ext]) return false;
-    int lo = 0, hi = E_ext - 1;          // largest e with tile_start[e] <= mt
-    while (lo < hi) {
-        int mid = (lo + hi + 1) >> 1;
-        if (tile_start[mid] <= mt) lo = mid; else hi = mid - 1;
-    }
-    e = lo;
-    m0 = offsets[e] + (mt - tile_start[e]) * kBM;
-    rows = min(kBM, offsets[e + 1] - m0);
-    return rows > 0;
-}
-
-// Dequantize 32 weights (one 16-byte chunk) of row `row`, K offset k, into 16 bf16x2 words.
-template <int MODE>
-__device__ __forceinline__ void dequant32(const uint8_t* base, const Proj& P, int row, int k,
-                                          int scale_f16, uint32_t out[16]) {
-    const int n_in = P.n_in;
-    uint4 v = *reinterpret_cast<const uint4*>(base + P.w + (int64_t)row * (n_in / 2) + k / 2);
-    uint32_t wd[4] = {v.x, v.y, v.z, v.w};
-    if constexpr (MODE == BRX_QUANT_AFFINE) {
-        const int G = n_in / 64;
-        float s = load_scale(base + P.s, (int64_t)row * G + k / 64, scale_f16);
-        float b = load_scale(base + P.b, (int64_t)row * G + k / 64, scale_f16);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                float v0 = fmaf(s, (float)((wd[q] >> (8 * i)) & 0xFu), b);
-                float v1 = fmaf(s, (float)((wd[q] >> (8 * i + 4)) & 0xFu), b);
-                out[4 * q + i] = f2bf(v0) | (f2bf(v1) << 16);
-            }
-        }
-    } else {
-        const int G = n_in / 32;
-        float s = e8m0_f32(base[P.s + (int64_t)row * G + k / 32]);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                float v0 = e2m1_f32((wd[q] >> (8 * i)) & 0xFu) * s;
-                float v1 = e2m1_f32((wd[q] >> (8 * i + 4)) & 0xFu) * s;
-                out[4 * q + i] = f2bf(v0) | (f2bf(v1) << 16);
-            }
-        }
-    }
-}
-
 __device__ __forceinline__ int pair_token(const FwdArgs& a, int pair) {
     return pair < a.P ? pair_tok(a, pair) : pair - a.P;
 }
 
-// ------------------------------------------------------------------ gate/up
+__device__ __forceinline__ uint32_t pk_bf16(float lo, float hi) {
+    return __builtin_bit_cast(uint32_t, bf16x2_t{(__bf16)lo, (__bf16)hi});
+}
+
+// native vector (not HIP's uint4 struct, whose copies are memcpys that keep arrays of it in
+// scratch memory)
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+// ------------------------------------------------------------------ grouped GEMM
+// One block = 256 threads = 4 waves, one wave per SIMD (accumulators in AGPRs); the tile is
+// MF * 16 rows (one M tile of one expert, MF in {2, 4, 8} chosen by the tile's row count) by
+// 256 columns, wave w owning columns [64 w, 64 w + 64) and every row, so each weight is
+// dequantized by exactly one lane and each A fragment read from LDS feeds 4 MFMAs.  KIND 0
+// (gate/up): a wave's 64 columns are 32 gate features and the up rows of the same 32
+// features; KIND 1 (down): 64 output columns.
+//
+// K order inside a 64-wide stage: v_mfma_f32_16x16x32_bf16 takes from lane l the 8
+// consecutive K of group q = l >> 4.  Here MFMA kc (0, 1) of a stage feeds lane group q the
+// stage's K = 16 q + 8 kc .. + 8, so a lane's B operand for MFMA kc is the 32-bit word
+// 2q + kc of its weight row, and its A operand the 16-byte chunk 2q + kc of the activation
+// row.  Each output is still the sum over all K.
+//
+// Everything a stage needs is copied global -> LDS by the buffer unit (buffer_load ... lds,
+// no registers): the A tile (128 rows x 64 bf16, 16-byte chunks XOR-swizzled by row so the
+// 16 rows an MFMA operand read touches fall in 16 distinct bank groups), the block's 256
+// weight rows x 32 bytes (the two 16-byte halves of rows 8..15 of every 16 swapped, for the
+// same reason) and one 16-bit scale (and bias) per row, each in a 32-bit slot (a 16-bit copy
+// to LDS writes 4 bytes per lane).  A ring of kNS stages keeps
+// kNS - 2 stages in flight while the MFMAs consume one; per stage s:
+//   wait until stage s + 1 has landed (s_waitcnt vmcnt(N), N = the later stages' loads);
+//   barrier (so every wave's copies are visible and stage s - 1's slot is free);
+//   issue the copies of stage s + kNS - 1;
+//   MFMA kc 0 of stage s  | dequantize B(s) kc 1 from LDS into operand registers
+//   MFMA kc 1 of stage s  | dequantize B(s + 1) kc 0
+// Copies past the last stage repeat it.  The waits are explicit (inline asm with a memory
+// clobber, so the compiler moves no LDS access across them); the MFMA-interleaved VALU code
+// is plain C++ so that the compiler's MFMA hazard checks cover it.
+constexpr int kGemmWaves = 4;
+constexpr int kGemmThreads = 64 * kGemmWaves;
+constexpr int kNF = 4;                       // 16-column fragments per wave
+constexpr int kWaveN = 16 * kNF;             // columns per wave
+constexpr int kBlockN = kGemmWaves * kWaveN; // columns per block
+constexpr int kNS = 3;                       // LDS ring stages
+constexpr int kStA = kBM * kBK * 2;          // stage bytes: A tile
+constexpr int kStB = kBlockN * kBK / 2;      // B rows, 4-bit
+constexpr int kStS = kBlockN * 4 * 2;        // scale and bias per row, one 32-bit LDS slot each
+constexpr int kStage = kStA + kStB + kStS;
+
+typedef __attribute__((address_space(3))) void* LDS_PTR;
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+// swizzle key of A tile row m: 16-byte chunk c of the row sits in slot c ^ a_key(m); rows
+// 2t and 2t + 1 share a 256-byte bank row, so keys (m >> 1) & 7 spread 16 consecutive rows
+// over 16 distinct bank groups
+__device__ __forceinline__ int a_key(int m) { return (m >> 1) & 7; }
+
+// waits for this wave's LDS accesses, then for every wave
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// waits until at most N of this wave's copies into LDS are in flight, then for every wave
+template <int N>
+__device__ __forceinline__ void dma_wait_barrier() {
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+
+// Dequantize one 32-bit word (8 weights, natural K order) into a bf16x8 MFMA operand.
+//   affine: w = fmaf(s, q, b) rounded to bf16 (v_cvt_pk_bf16_f32).  The word splits into its
+//     even nibbles (one per byte) and odd nibbles, so each weight converts with one
+//     v_cvt_f32_ubyte{0..3}.  An empty asm statement hides the masked words from the
+//     compiler, which would otherwise fold mask and byte select into one bit-field extract
+//     per nibble; it emits no instruction, so the hazard checks between these VALU ops and
+//     the MFMAs they interleave with stay the compiler's.
+//   MXFP4: the hardware converts two e2m1 codes with the e8m0 scale, exact in bf16.
 template <int MODE>
-__global__ __launch_bounds__(kThreads) void k_pf_gateup(FwdArgs a, const int32_t* __restrict__ order,
-                                                        const int32_t* __restrict__ offsets,
-                                                        const int32_t* __restrict__ tile_start,
-                                                        uint16_t* __restrict__ hbuf, int hstride) {
-    __shared__ __attribute__((aligned(16))) uint16_t As[kBM * kLdsRow];
-    __shared__ __attribute__((aligned(16))) uint16_t Bs[128 * kLdsRow];
-    __shared__ int32_t tok_s[kBM];
-    const int E_ext = a.E + (a.shared ? 1 : 0);
-    int e, m0, rows;
-    if (!find_tile(tile_start, offsets, E_ext, blockIdx.x, e, m0, rows)) return;
+__device__ __forceinline__ bf16x8_t dq8(uint32_t w, float s, float b, float sc) {
+    uint32_t o[4];
+    if constexpr (MODE == BRX_QUANT_AFFINE) {
+        uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+        asm("" : "+v"(lo), "+v"(hi));
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            o[j] = pk_bf16(fmaf(s, (float)((lo >> (8 * j)) & 0xFFu), b),
+                           fmaf(s, (float)((hi >> (8 * j)) & 0xFFu), b));
+    } else {
+        o[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 0));
+        o[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 1));
+        o[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 2));
+        o[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 3));
+    }
+    return __builtin_bit_cast(bf16x8_t, u32x4_t{o[0], o[1], o[2], o[3]});
+}
+
+template <int MODE, bool F16, int KIND, int MF>
+__device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restrict__ order,
+                                        uint16_t* __restrict__ hbuf, int hstride,
+                                        uint16_t* __restrict__ y_routed, uint16_t* __restrict__ y_shared,
+                                        uint8_t* ring, int32_t* dst_s, int e, int m0, int rows, int slot,
+                                        int nt) {
+    constexpr int NA = MF * 16 * 8 / 64 / kGemmWaves;   // A wave-instructions per wave per stage
+    constexpr int NV = NA + 2 + (MODE == BRX_QUANT_AFFINE ? 2 : 1);   // loads per wave per stage
     const bool sh = e >= a.E;
     const int inter = sh ? a.I_sh : a.I;
-    const int f0 = blockIdx.y * 64;
-    if (f0 >= inter) return;
-    const Layout& L = sh ? a.lay_sh : a.lay;
-    const uint8_t* base = pf_expert_base(a, e);
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int wm = wv & 1, wn = wv >> 1;
     const int H = a.H;
+    const int K = KIND == 0 ? H : inter;
+    const int nsteps = K / kBK;
+    const Layout& L = sh ? a.lay_sh : a.lay;
+    const uint8_t* base = sh ? a.shared : a.slots + (int64_t)slot * a.slot_stride;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int q = lane >> 4;
 
-    if (tid < kBM) tok_s[tid] = tid < rows ? pair_token(a, order[m0 + tid]) : -1;
-    __syncthreads();
-
-    f32x4_t acc[4][4];
+    // ---- A: wave wv fills 1 KB chunks [wv * NA, wv * NA + NA) of a stage's A tile; lane l of
+    // chunk ii lands in 16-byte slot ii * 64 + l = (row, physical slot p) and carries the
+    // row's logical K chunk p ^ key(row)
+    const __amdgpu_buffer_rsrc_t ra_rsrc = KIND == 0
+        ? make_rsrc(a.x, (uint32_t)((int64_t)a.T * H * 2))
+        : make_rsrc(hbuf, (uint32_t)((int64_t)(m0 + rows) * hstride * 2));
+    uint32_t va[NA];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < NA; ++i) {
+        const int ci = (wv * NA + i) * 64 + lane;
+        const int rl = ci >> 3;                            // LDS row
+        const int r = min(rl, rows - 1);                   // source row (past `rows`: repeat)
+        const int c = (ci & 7) ^ a_key(rl);
+        if constexpr (KIND == 0) {
+            va[i] = (uint32_t)pair_token(a, order[m0 + r]) * (uint32_t)(H * 2) + c * 16;
+        } else {
+            va[i] = (uint32_t)(m0 + r) * (uint32_t)(hstride * 2) + c * 16;
+        }
+    }
+    // ---- B: the block's 256 weight rows (KIND 0: gate rows of features nt * 128 + [0, 128),
+    // then the up rows of the same features; KIND 1: down rows nt * 256 + [0, 256)), 32 bytes
+    // of each per stage; wave wv fills 1 KB chunks 2 wv, 2 wv + 1 (64 rows), and the rows'
+    // scales (one 16-bit value per row and stage: affine scale and bias; MXFP4 the e8m0 bytes
+    // of the stage's two groups)
+    const __amdgpu_buffer_rsrc_t rb_rsrc = make_rsrc(base, (uint32_t)L.bytes);
+    const int p_w = KIND == 0 ? (wv >= 2 ? 1 : 0) : 2;  // matrix of this wave's 64 rows
+    auto mat_row = [&](int br) __attribute__((always_inline)) {
+        return KIND == 0 ? min(nt * 128 + (br & 127), inter - 1) : min(nt * 256 + br, H - 1);
+    };
+    uint32_t vb[2];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-
-    const int lrow = tid >> 1, lhalf = tid & 1;
-    for (int k0 = 0; k0 < H; k0 += kBK) {
-        // A: 128 rows x 64 bf16 of gathered activations
-        {
-            int t = tok_s[lrow];
-            uint4 v[4];
-            if (t >= 0) {
-                const uint4* src = reinterpret_cast<const uint4*>(a.x + (int64_t)t * H + k0 + lhalf * 32);
-#pragma unroll
-                for (int q = 0; q < 4; ++q) v[q] = src[q];
-            } else {
-#pragma unroll
-                for (int q = 0; q < 4; ++q) v[q] = make_uint4(0, 0, 0, 0);
+    for (int i = 0; i < 2; ++i) {
+        const int sl = (wv * 2 + i) * 64 + lane;           // 16-byte slot of the stage's B
+        const int br = sl >> 1;
+        const int h = (sl & 1) ^ ((br >> 3) & 1);
+        vb[i] = (uint32_t)mat_row(br) * (uint32_t)(K / 2) + h * 16;
+    }
+    const int wo = (int)L.p[p_w].w, so = (int)L.p[p_w].s, bo = (int)L.p[p_w].b;
+    const uint32_t vsc = MODE == BRX_QUANT_AFFINE
+        ? (uint32_t)mat_row(wv * 64 + lane) * (uint32_t)(K / 64) * 2
+        : (uint32_t)mat_row(wv * 64 + lane) * (uint32_t)(K / 32);
+    if constexpr (KIND == 1) {
+        if (tid < kBM) {
+            int d = -1;
+            if (tid < rows) {
+                const int pair = order[m0 + tid];
+                d = pair < a.P ? pair_row(a, pair) : -2 - (pair - a.P);
             }
-            uint4* dst = reinterpret_cast<uint4*>(As + lrow * kLdsRow + lhalf * 32);
-#pragma unroll
-            for (int q = 0; q < 4; ++q) dst[q] = v[q];
+            dst_s[tid] = d;
         }
-        // B: rows 0-63 gate features f0.., rows 64-127 up features f0..
-        {
-            int mat = lrow >> 6;
-            int row = f0 + (lrow & 63);
-            uint32_t wq[16];
-            dequant32<MODE>(base, L.p[mat], row, k0 + lhalf * 32, a.scale_f16, wq);
-            uint4* dst = reinterpret_cast<uint4*>(Bs + lrow * kLdsRow + lhalf * 32);
-#pragma unroll
-            for (int q = 0; q < 4; ++q) dst[q] = make_uint4(wq[4 * q], wq[4 * q + 1], wq[4 * q + 2], wq[4 * q + 3]);
-        }
-        __syncthreads();
-#pragma unroll
-        for (int kc = 0; kc < 2; ++kc) {
-            const int ko = kc * 32 + (lane >> 4) * 8;
-            bf16x8_t af[4], bfr[4];
-#pragma unroll
-            for (int mi = 0; mi < 4; ++mi)
-                af[mi] = *reinterpret_cast<const bf16x8_t*>(As + (wm * 64 + mi * 16 + (lane & 15)) * kLdsRow + ko);
-#pragma unroll
-            for (int nj = 0; nj < 4; ++nj) {
-                int brow = (nj >> 1) * 64 + wn * 32 + (nj & 1) * 16 + (lane & 15);
-                bfr[nj] = *reinterpret_cast<const bf16x8_t*>(Bs + brow * kLdsRow + ko);
-            }
-#pragma unroll
-            for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-                for (int nj = 0; nj < 4; ++nj)
-                    acc[mi][nj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[mi], bfr[nj], acc[mi][nj], 0, 0, 0);
-        }
-        __syncthreads();
     }
 
-    // epilogue: frags nj=0,1 are gate, nj=2,3 the up rows of the same features
+    auto issue = [&](int s) __attribute__((always_inline)) {
+        const int g = min(s, nsteps - 1);
+        uint8_t* st = ring + (s % kNS) * kStage;
 #pragma unroll
-    for (int nj = 0; nj < 2; ++nj) {
-        const int f = f0 + wn * 32 + nj * 16 + (lane & 15);
-        float bg = 0.f, bu = 0.f;
-        if (L.p[0].bias >= 0) {
-            bg = bf2f(reinterpret_cast<const uint16_t*>(base + L.p[0].bias)[f]);
-            bu = bf2f(reinterpret_cast<const uint16_t*>(base + L.p[1].bias)[f]);
+        for (int i = 0; i < NA; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra_rsrc, (LDS_PTR)(st + (wv * NA + i) * 1024), 16,
+                                                     va[i], g * 128, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rb_rsrc, (LDS_PTR)(st + kStA + (wv * 2 + i) * 1024), 16,
+                                                     vb[i], wo + g * 32, 0, 0);
+        // a 16-bit copy to LDS fills a 32-bit slot per lane (zero-extended)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rb_rsrc, (LDS_PTR)(st + kStA + kStB + wv * 256), 2, vsc,
+                                                 so + g * 2, 0, 0);
+        if constexpr (MODE == BRX_QUANT_AFFINE)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rb_rsrc, (LDS_PTR)(st + kStA + kStB + 1024 + wv * 256), 2,
+                                                     vsc, bo + g * 2, 0, 0);
+    };
+    // block row of fragment nj for this lane
+    int brow[kNF];
+#pragma unroll
+    for (int nj = 0; nj < kNF; ++nj)
+        brow[nj] = KIND == 0 ? (nj >> 1) * 128 + wv * 32 + (nj & 1) * 16 + (lane & 15)
+                             : wv * 64 + nj * 16 + (lane & 15);
+    // the lane's B words (both kc) and scales of stage s, read from LDS once per stage
+    // (8-byte reads: conflict-free with the half swap above)
+    struct Frag {
+        u32x2_t w[kNF];
+        uint32_t s[kNF], b[kNF];
+    };
+    auto fetch = [&](Frag& f, int s) __attribute__((always_inline)) {
+        const uint8_t* st = ring + (s % kNS) * kStage;
+#pragma unroll
+        for (int nj = 0; nj < kNF; ++nj) {
+            const int br = brow[nj];
+            const int h = (q >> 1) ^ ((br >> 3) & 1);
+            f.w[nj] = *reinterpret_cast<const u32x2_t*>(st + kStA + (2 * br + h) * 16 + (q & 1) * 8);
+            f.s[nj] = *reinterpret_cast<const uint32_t*>(st + kStA + kStB + br * 4);
+            if constexpr (MODE == BRX_QUANT_AFFINE)
+                f.b[nj] = *reinterpret_cast<const uint32_t*>(st + kStA + kStB + 1024 + br * 4);
         }
+    };
+    // word kc of the lane's K chunks, dequantized into MFMA operands
+    auto deq = [&](bf16x8_t (&bop)[kNF], const Frag& f, int kc) __attribute__((always_inline)) {
 #pragma unroll
-        for (int mi = 0; mi < 4; ++mi) {
+        for (int nj = 0; nj < kNF; ++nj) {
+            float sv = 0.f, bv = 0.f, sc = 0.f;
+            if constexpr (MODE == BRX_QUANT_AFFINE) {
+                sv = F16 ? h2f(f.s[nj]) : bf2f(f.s[nj]);
+                bv = F16 ? h2f(f.b[nj]) : bf2f(f.b[nj]);
+            } else {
+                // the lane's K chunk 2q + kc lies in group 2g + (q >> 1) of the stage
+                sc = e8m0_f32((f.s[nj] >> (8 * (q >> 1))) & 0xFFu);
+            }
+            bop[nj] = dq8<MODE>(kc ? f.w[nj].y : f.w[nj].x, sv, bv, sc);
+        }
+    };
+
+    f32x4_t acc[MF][kNF];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                int r = wm * 64 + mi * 16 + (lane >> 4) * 4 + i;
-                if (r < rows) {
-                    float h = act_apply(a.act, acc[mi][nj][i] + bg, acc[mi][nj + 2][i] + bu, a.alpha, a.limit);
-                    hbuf[(int64_t)(m0 + r) * hstride + f] = (uint16_t)f2bf(h);
+    for (int i = 0; i < MF; ++i)
+#pragma unroll
+        for (int j = 0; j < kNF; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+    auto mma = [&](int s, const bf16x8_t (&bop)[kNF], int kc) __attribute__((always_inline)) {
+        const uint16_t* As = reinterpret_cast<const uint16_t*>(ring + (s % kNS) * kStage);
+#pragma unroll
+        for (int mi = 0; mi < MF; ++mi) {
+            const int m = mi * 16 + (lane & 15);
+            const int c = (2 * q + kc) ^ a_key(m);
+            const bf16x8_t af = *reinterpret_cast<const bf16x8_t*>(As + m * 64 + c * 8);
+#pragma unroll
+            for (int nj = 0; nj < kNF; ++nj)
+                acc[mi][nj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bop[nj], acc[mi][nj], 0, 0, 0);
+        }
+    };
+
+    // prologue: stages 0 .. kNS - 2 in flight; wait for stages 0 and 1; B(0) kc 0 dequantized
+#pragma unroll
+    for (int s = 0; s < kNS - 1; ++s) issue(s);
+    dma_wait_barrier<NV * (kNS - 3)>();
+    bf16x8_t bop0[kNF], bop1[kNF];
+    Frag fc, fn;
+    fetch(fc, 0);
+    deq(bop0, fc, 0);
+    for (int s = 0; s < nsteps; ++s) {
+        // stage s + 1 landed in every wave; stage s - 1's slot is free for stage s + kNS - 1
+        dma_wait_barrier<NV * (kNS - 3)>();
+        issue(s + kNS - 1);
+        mma(s, bop0, 0);
+        deq(bop1, fc, 1);
+        fetch(fn, s + 1);
+        mma(s, bop1, 1);
+        deq(bop0, fn, 0);
+        fc = fn;
+    }
+
+    // ---- epilogue: the output tile goes through LDS (the ring, once every copy into it has
+    // landed and every wave is done reading it) so that the global stores are 16-byte chunks
+    // of contiguous row segments
+    dma_wait_barrier<0>();
+    uint16_t* T = reinterpret_cast<uint16_t*>(ring);
+    if constexpr (KIND == 0) {
+        constexpr int TS = kBlockN / 2 + 8;                // LDS row stride (elements)
+        constexpr int CH = kBlockN / 2 / 8;                // 16-byte chunks per row
+        // fragments nj < kNF / 2 are gate, nj + kNF / 2 the up rows of the same features
+#pragma unroll
+        for (int nj = 0; nj < kNF / 2; ++nj) {
+            const int fl = wv * (kWaveN / 2) + nj * 16 + (lane & 15);
+            const int f = min(nt * (kBlockN / 2) + fl, inter - 1);
+            float bg = 0.f, bu = 0.f;
+            if (L.p[0].bias >= 0) {
+                bg = bf2f(reinterpret_cast<const uint16_t*>(base + L.p[0].bias)[f]);
+                bu = bf2f(reinterpret_cast<const uint16_t*>(base + L.p[1].bias)[f]);
+            }
+#pragma unroll
+            for (int mi = 0; mi < MF; ++mi) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float h = act_apply(a.act, acc[mi][nj][i] + bg, acc[mi][nj + kNF / 2][i] + bu,
+                                              a.alpha, a.limit);
+                    T[(mi * 16 + q * 4 + i) * TS + fl] = __builtin_bit_cast(uint16_t, (__bf16)h);
                 }
+            }
+        }
+        lds_barrier();
+        for (int c = tid; c < MF * 16 * CH; c += kGemmThreads) {
+            const int r = c / CH, f0 = nt * (kBlockN / 2) + (c % CH) * 8;
+            if (r < rows && f0 < inter)
+                *reinterpret_cast<u32x4_t*>(hbuf + (int64_t)(m0 + r) * hstride + f0) =
+                    *reinterpret_cast<const u32x4_t*>(T + r * TS + (c % CH) * 8);
+        }
+    } else {
+        constexpr int TS = kBlockN + 8;
+        constexpr int CH = kBlockN / 8;
+#pragma unroll
+        for (int nj = 0; nj < kNF; ++nj) {
+            const int nl = wv * kWaveN + nj * 16 + (lane & 15);
+            float bd = 0.f;
+            if (L.p[2].bias >= 0)
+                bd = bf2f(reinterpret_cast<const uint16_t*>(base + L.p[2].bias)[min(nt * kBlockN + nl, H - 1)]);
+#pragma unroll
+            for (int mi = 0; mi < MF; ++mi) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    T[(mi * 16 + q * 4 + i) * TS + nl] = __builtin_bit_cast(uint16_t, (__bf16)(acc[mi][nj][i] + bd));
+            }
+        }
+        lds_barrier();
+        for (int c = tid; c < MF * 16 * CH; c += kGemmThreads) {
+            const int r = c / CH, n0 = nt * kBlockN + (c % CH) * 8;
+            if (r < rows && n0 < H) {
+                const int d = dst_s[r];
+                uint16_t* dst = d >= 0 ? y_routed + (int64_t)d * H + n0 : y_shared + (int64_t)(-2 - d) * H + n0;
+                *reinterpret_cast<u32x4_t*>(dst) = *reinterpret_cast<const u32x4_t*>(T + r * TS + (c % CH) * 8);
             }
         }
     }
 }
 
-// ------------------------------------------------------------------ down
-template <int MODE>
-__global__ __launch_bounds__(kThreads) void k_pf_down(FwdArgs a, const int32_t* __restrict__ order,
-                                                      const int32_t* __restrict__ offsets,
-                                                      const int32_t* __restrict__ tile_start,
-                                                      const uint16_t* __restrict__ hbuf, int hstride,
-                                                      uint16_t* __restrict__ y_routed,
-                                                      uint16_t* __restrict__ y_shared) {
-    __shared__ __attribute__((aligned(16))) uint16_t As[kBM * kLdsRow];
-    __shared__ __attribute__((aligned(16))) uint16_t Bs[128 * kLdsRow];
-    const int E_ext = a.E + (a.shared ? 1 : 0);
-    int e, m0, rows;
-    if (!find_tile(tile_start, offsets, E_ext, blockIdx.x, e, m0, rows)) return;
-    const bool sh = e >= a.E;
-    const int inter = sh ? a.I_sh : a.I;
-    const Layout& L = sh ? a.lay_sh : a.lay;
-    const uint8_t* base = pf_expert_base(a, e);
-    const int n0 = blockIdx.y * 128;
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int wm = wv & 1, wn = wv >> 1;
-    const int P = a.P, H = a.H;
-
-    f32x4_t acc[4][4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-
-    const int lrow = tid >> 1, lhalf = tid & 1;
-    for (int k0 = 0; k0 < inter; k0 += kBK) {
-        {
-            uint4 v[4];
-            if (lrow < rows) {
-                const uint4* src = reinterpret_cast<const uint4*>(hbuf + (int64_t)(m0 + lrow) * hstride + k0 + lhalf * 32);
-#pragma unroll
-                for (int q = 0; q < 4; ++q) v[q] = src[q];
-            } else {
-#pragma unroll
-                for (int q = 0; q < 4; ++q) v[q] = make_uint4(0, 0, 0, 0);
-            }
-            uint4* dst = reinterpret_cast<uint4*>(As + lrow * kLdsRow + lhalf * 32);
-#pragma unroll
-            for (int q = 0; q < 4; ++q) dst[q] = v[q];
-        }
-        {
-            uint32_t wq[16];
-            if (n0 + lrow < H) {
-                dequant32<MODE>(base, L.p[2], n0 + lrow, k0 + lhalf * 32, a.scale_f16, wq);
-            } else {
-#pragma unroll
-                for (int q = 0; q < 16; ++q) wq[q] = 0u;
-            }
-            uint4* dst = reinterpret_cast<uint4*>(Bs + lrow * kLdsRow + lhalf * 32);
-#pragma unroll
-            for (int q = 0; q < 4; ++q) dst[q] = make_uint4(wq[4 * q], wq[4 * q + 1], wq[4 * q + 2], wq[4 * q + 3]);
-        }
-        __syncthreads();
-#pragma unroll
-        for (int kc = 0; kc < 2; ++kc) {
-            const int ko = kc * 32 + (lane >> 4) * 8;
-            bf16x8_t af[4], bfr[4];
-#pragma unroll
-            for (int mi = 0; mi < 4; ++mi)
-                af[mi] = *reinterpret_cast<const bf16x8_t*>(As + (wm * 64 + mi * 16 + (lane & 15)) * kLdsRow + ko);
-#pragma unroll
-            for (int nj = 0; nj < 4; ++nj)
-                bfr[nj] = *reinterpret_cast<const bf16x8_t*>(Bs + (wn * 64 + nj * 16 + (lane & 15)) * kLdsRow + ko);
-#pragma unroll
-            for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-                for (int nj = 0; nj < 4; ++nj)
-                    acc[mi][nj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[mi], bfr[nj], acc[mi][nj], 0, 0, 0);
-        }
-        __syncthreads();
+template <int MODE, bool F16, int KIND>
+__global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void k_pf_gemm(FwdArgs a, const int32_t* __restrict__ order, const int32_t* __restrict__ tile_start,
+               const int4* __restrict__ tinfo, int E_ext, int ntn, uint16_t* __restrict__ hbuf,
+               int hstride, uint16_t* __restrict__ y_routed, uint16_t* __restrict__ y_shared) {
+    __shared__ __attribute__((aligned(16))) uint8_t ring[kNS * kStage];
+    __shared__ int32_t dst_s[KIND == 1 ? kBM : 1];
+    const int blk = blockIdx.x;
+    const int loc = blk / kXcd;
+    const int nt = loc % ntn;
+    const int mt = (loc / ntn) * kXcd + blk % kXcd;
+    const int total = tile_start[E_ext];
+    const int4 ti = tinfo[mt];
+    if (mt >= total) return;
+    const int e = ti.x, m0 = ti.y, rows = ti.z;
+    if (KIND == 0) {
+        const int inter = e >= a.E ? a.I_sh : a.I;
+        if (nt * (kBlockN / 2) >= inter) return;
+    } else {
+        if (nt * kBlockN >= a.H) return;
     }
-
-#pragma unroll
-    for (int nj = 0; nj < 4; ++nj) {
-        const int n = n0 + wn * 64 + nj * 16 + (lane & 15);
-        if (n >= H) continue;
-        float bd = 0.f;
-        if (L.p[2].bias >= 0) bd = bf2f(reinterpret_cast<const uint16_t*>(base + L.p[2].bias)[n]);
-#pragma unroll
-        for (int mi = 0; mi < 4; ++mi) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                int r = wm * 64 + mi * 16 + (lane >> 4) * 4 + i;
-                if (r < rows) {
-                    int pair = order[m0 + r];
-                    uint16_t yb = (uint16_t)f2bf(acc[mi][nj][i] + bd);
-                    if (pair < P) y_routed[(int64_t)pair_row(a, pair) * H + n] = yb;
-                    else y_shared[(int64_t)(pair - P) * H + n] = yb;
-                }
-            }
-        }
-    }
+    if (rows <= 32)
+        pf_tile<MODE, F16, KIND, 2>(a, order, hbuf, hstride, y_routed, y_shared, ring, dst_s, e, m0, rows, ti.w, nt);
+    else if (rows <= 64)
+        pf_tile<MODE, F16, KIND, 4>(a, order, hbuf, hstride, y_routed, y_shared, ring, dst_s, e, m0, rows, ti.w, nt);
+    else
+        pf_tile<MODE, F16, KIND, 8>(a, order, hbuf, hstride, y_routed, y_shared, ring, dst_s, e, m0, rows, ti.w, nt);
 }
 
 // ------------------------------------------------------------------ combine
@@ -375,9 +493,11 @@ struct PfWs {
     int32_t* order;
     int32_t* offsets;
     int32_t* tile_start;
+    int4* tinfo;
     uint16_t* hbuf;
     uint16_t* y_routed;
     uint16_t* y_shared;
+    int mt_pad;                 // M tiles the grids cover (a multiple of kXcd)
     size_t bytes;
 };
 
@@ -389,17 +509,48 @@ PfWs carve(const FwdArgs& a, void* ws) {
     const int P_ext = P + T_sh;
     const int E_ext = a.E + (a.shared ? 1 : 0);
     const int Imax = a.I > a.I_sh ? a.I : a.I_sh;
+    // at most ceil(P_ext / kBM) full tiles plus one partial tile per expert
+    const int mt_max = (P_ext + kBM - 1) / kBM + E_ext;
     PfWs w{};
+    w.mt_pad = (mt_max + kXcd - 1) / kXcd * kXcd;
     size_t off = 0;
     char* b = reinterpret_cast<char*>(ws);
     w.order = reinterpret_cast<int32_t*>(b + off); off = align256(off + sizeof(int32_t) * P_ext);
     w.offsets = reinterpret_cast<int32_t*>(b + off); off = align256(off + sizeof(int32_t) * (E_ext + 1));
     w.tile_start = reinterpret_cast<int32_t*>(b + off); off = align256(off + sizeof(int32_t) * (E_ext + 1));
+    w.tinfo = reinterpret_cast<int4*>(b + off); off = align256(off + sizeof(int4) * w.mt_pad);
     w.hbuf = reinterpret_cast<uint16_t*>(b + off); off = align256(off + 2ull * P_ext * Imax);
     w.y_routed = reinterpret_cast<uint16_t*>(b + off); off = align256(off + 2ull * P * a.H);
     w.y_shared = reinterpret_cast<uint16_t*>(b + off); off = align256(off + 2ull * T_sh * a.H);
     w.bytes = off;
     return w;
+}
+
+template <int MODE, bool F16>
+hipError_t launch_gemm(const FwdArgs& a, const PfWs& w, int E_ext, int Imax, uint16_t* y_routed,
+                       int phases, hipStream_t s) {
+    if (phases & 1) {
+        const int ntn = (Imax + kBlockN / 2 - 1) / (kBlockN / 2);
+        hipLaunchKernelGGL((k_pf_gemm<MODE, F16, 0>), dim3(w.mt_pad * ntn), dim3(kGemmThreads), 0, s,
+                           a, w.order, w.tile_start, w.tinfo, E_ext, ntn, w.hbuf, Imax, y_routed, w.y_shared);
+        hipError_t err = hipGetLastError();
+        if (err != hipSuccess) return err;
+    }
+    if (phases & 2) {
+        const int ntn = (a.H + kBlockN - 1) / kBlockN;
+        hipLaunchKernelGGL((k_pf_gemm<MODE, F16, 1>), dim3(w.mt_pad * ntn), dim3(kGemmThreads), 0, s,
+                           a, w.order, w.tile_start, w.tinfo, E_ext, ntn, w.hbuf, Imax, y_routed, w.y_shared);
+        return hipGetLastError();
+    }
+    return hipSuccess;
+}
+
+hipError_t launch_bucket(const int32_t* pexp, int P, int E, int E_ext, int T_sh, int BM,
+                         const int32_t* g2s, int capacity, int32_t* order, int32_t* offsets,
+                         int32_t* tile_start, int4* tinfo, hipStream_t s) {
+    hipLaunchKernelGGL(k_bucket, dim3(E_ext), dim3(1024), sizeof(int32_t) * E_ext, s, pexp, P, E,
+                       E_ext, T_sh, BM, g2s, capacity, order, offsets, tile_start, tinfo);
+    return hipGetLastError();
 }
 
 }  // namespace
@@ -408,9 +559,7 @@ size_t prefill_workspace_bytes(const FwdArgs& a) { return carve(a, nullptr).byte
 
 hipError_t launch_sort_pairs(const int32_t* pexp, int P, int E, int E_ext, int T_sh, int BM,
                              int32_t* order, int32_t* offsets, int32_t* tile_start, hipStream_t s) {
-    hipLaunchKernelGGL(k_bucket, dim3(E_ext), dim3(1024), sizeof(int32_t) * E_ext, s, pexp, P, E,
-                       E_ext, T_sh, BM, order, offsets, tile_start);
-    return hipGetLastError();
+    return launch_bucket(pexp, P, E, E_ext, T_sh, BM, nullptr, 1, order, offsets, tile_start, nullptr, s);
 }
 
 hipError_t launch_combine(const uint16_t* y_routed, const uint16_t* y_shared, const float* w,
@@ -425,37 +574,27 @@ hipError_t launch_prefill(const FwdArgs& a, void* ws, size_t ws_bytes, int phase
     if (w.bytes > ws_bytes) return hipErrorInvalidValue;
     const int P = a.P;
     const int T_sh = a.auto_shared ? a.T : 0;
-    const int P_ext = P + T_sh;
     const int E_ext = a.E + (a.shared ? 1 : 0);
     const int Imax = a.I > a.I_sh ? a.I : a.I_sh;
-    const int mt_max = (P_ext + kBM - 1) / kBM + E_ext;
+    // the GEMMs address activations and h rows with 32-bit buffer offsets
+    if ((int64_t)a.T * a.H * 2 >= (int64_t)1 << 32 || (int64_t)(P + T_sh) * Imax * 2 >= (int64_t)1 << 32)
+        return hipErrorInvalidValue;
     uint16_t* y_routed = a.yun ? a.yun : w.y_routed;
     hipError_t err = hipSuccess;
     if (phases & 1) {
-        err = launch_sort_pairs(a.pexp, P, a.E, E_ext, T_sh, kBM, w.order, w.offsets, w.tile_start, s);
-        if (err != hipSuccess) return err;
-        if (a.quant_mode == BRX_QUANT_AFFINE)
-            hipLaunchKernelGGL(k_pf_gateup<BRX_QUANT_AFFINE>, dim3(mt_max, Imax / 64), dim3(kThreads), 0, s,
-                               a, w.order, w.offsets, w.tile_start, w.hbuf, Imax);
-        else
-            hipLaunchKernelGGL(k_pf_gateup<BRX_QUANT_MXFP4>, dim3(mt_max, Imax / 64), dim3(kThreads), 0, s,
-                               a, w.order, w.offsets, w.tile_start, w.hbuf, Imax);
-        err = hipGetLastError();
+        err = launch_bucket(a.pexp, P, a.E, E_ext, T_sh, kBM, a.g2s, a.capacity, w.order, w.offsets,
+                            w.tile_start, w.tinfo, s);
         if (err != hipSuccess) return err;
     }
-    if (phases & 2) {
-        if (a.quant_mode == BRX_QUANT_AFFINE)
-            hipLaunchKernelGGL(k_pf_down<BRX_QUANT_AFFINE>, dim3(mt_max, (a.H + 127) / 128), dim3(kThreads), 0, s,
-                               a, w.order, w.offsets, w.tile_start, w.hbuf, Imax, y_routed, w.y_shared);
-        else
-            hipLaunchKernelGGL(k_pf_down<BRX_QUANT_MXFP4>, dim3(mt_max, (a.H + 127) / 128), dim3(kThreads), 0, s,
-                               a, w.order, w.offsets, w.tile_start, w.hbuf, Imax, y_routed, w.y_shared);
-        err = hipGetLastError();
-        if (err != hipSuccess) return err;
-        if (a.out)
-            err = launch_combine(y_routed, a.auto_shared ? w.y_shared : nullptr, a.w, a.sgate, a.T, a.k,
-                                 a.H, a.out, s);
-    }
+    if (a.quant_mode == BRX_QUANT_AFFINE)
+        err = a.scale_f16 ? launch_gemm<BRX_QUANT_AFFINE, true>(a, w, E_ext, Imax, y_routed, phases, s)
+                          : launch_gemm<BRX_QUANT_AFFINE, false>(a, w, E_ext, Imax, y_routed, phases, s);
+    else
+        err = launch_gemm<BRX_QUANT_MXFP4, false>(a, w, E_ext, Imax, y_routed, phases, s);
+    if (err != hipSuccess) return err;
+    if ((phases & 2) && a.out)
+        err = launch_combine(y_routed, a.auto_shared ? w.y_shared : nullptr, a.w, a.sgate, a.T, a.k,
+                             a.H, a.out, s);
     return err;
 }
 
