@@ -485,7 +485,7 @@ def main():
             "roofline": {"bound": "mfma", "achieved": round(pre["gateup_tflops"], 1),
                          "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(pre["gateup_tflops"] / BF16_PEAK_TFLOPS, 4),
-                         "kernel": "k_pf_gateup (+ bucketing)"},
+                         "kernel": "k_pf_gemm gate/up + SwiGLU (+ k_bucket)"},
             "layer_tflops": round(pre["layer_tflops"], 1),
             "max_expert_rows": pre["max_expert_rows"], "experts_hit": pre["experts_hit"],
         }
