@@ -342,6 +342,56 @@ __device__ __forceinline__ void stage_store(int K, int nrows, int base, const St
     }
 }
 
+// The same staging with the pieces of all rows numbered densely (piece g of the block is row
+// g / (8U), unit (g / 8) % U, piece g % 8) and handed to the threads kStageB at a time, so rows
+// shorter than the block (h rows of 8-16 units) still take one round trip per kStageB * kThreads
+// pieces. The 8 pieces of a unit stay on 8 consecutive lanes.
+template <int MODE, typename RowOf>
+__device__ __forceinline__ void stage_dense(const uint16_t* __restrict__ src, int K, int nrows, RowOf row_of,
+                                            uint8_t* xs, float* sums) {
+    const int U = K / 64;
+    const int pcs = U * 8;
+    const int total = nrows * pcs;
+    for (int base = 0; base < total; base += kStageB * kThreads) {
+        uint4 v[kStageB];
+        int gi[kStageB];
+#pragma unroll
+        for (int b = 0; b < kStageB; ++b) {
+            const int g = min(base + b * kThreads + (int)threadIdx.x, total - 1);
+            gi[b] = g;
+            const int r = g / pcs, pi = g - r * pcs;
+            const int off = row_of(r) * K + (pi >> 3) * 64 + (pi & 7) * 8;
+            v[b] = *reinterpret_cast<const uint4*>(src + off);
+        }
+#pragma unroll
+        for (int b = 0; b < kStageB; ++b) {
+            if (base + b * kThreads >= total) break;   // uniform
+            const bool ok = base + b * kThreads + (int)threadIdx.x < total;
+            const int g = gi[b];
+            const int r = g / pcs, pi = g - r * pcs;
+            const int un = pi >> 3, q = pi & 7;
+            uint32_t in[4] = {v[b].x, v[b].y, v[b].z, v[b].w}, o[4];
+            float part = 0.0f;
+            if constexpr (MODE == BRX_QUANT_AFFINE) {
+                perm8(in, o);
+#pragma unroll
+                for (int z = 0; z < 4; ++z)
+                    part = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, in[z]),
+                                                           __builtin_bit_cast(bf16x2_t, 0x3F803F80u), part, false);
+            } else {
+#pragma unroll
+                for (int z = 0; z < 4; ++z) o[z] = in[z];
+            }
+            if (ok)
+                *reinterpret_cast<uint4*>(xs + ((int64_t)r * U + un) * kXU + q * 16) = make_uint4(o[0], o[1], o[2], o[3]);
+            if constexpr (MODE == BRX_QUANT_AFFINE) {
+                part = sum8_dpp(part);
+                if (ok && q == 0) sums[r * U + un] = part;
+            }
+        }
+    }
+}
+
 // Stage `nrows` activation rows of K bf16 (row i at src + row_of(i) * K) into LDS as units of
 // 8 pieces (kXU bytes a unit), each piece in the order the dot product wants (affine: pairs
 // (x_i, x_{i+4}); MXFP4: natural), and each unit's sum (affine) in `sums` [nrows][U]. A thread
@@ -552,7 +602,7 @@ __global__ __launch_bounds__(kThreads) void k_dec_down(FwdArgs a, const uint16_t
     const int slot_first = table->ent[min(it_first >> lrbd, kMaxU - 1)].slot;
     const bool all_fit = (size_t)PT * Umax * (kXU + 4) <= (size_t)hs_bytes;
     float* hsum_all = reinterpret_cast<float*>(hs + (size_t)PT * Umax * kXU);
-    if (all_fit) stage_rows<MODE>(hbuf, hstride, PT, [](int i) { return i; }, hs, hsum_all);
+    if (all_fit) stage_dense<MODE>(hbuf, hstride, PT, [](int i) { return i; }, hs, hsum_all);
     Units<MODE, UPL> ud;
     const bool have_first = all_fit;
     if (have_first) {
@@ -614,7 +664,7 @@ __global__ __launch_bounds__(kThreads) void k_dec_down(FwdArgs a, const uint16_t
         }
         float* hsum = all_fit ? hsum_all : reinterpret_cast<float*>(hs + (size_t)rows * Umax * kXU);
         if (!all_fit) {
-            stage_rows<MODE>(hbuf, hstride, rows, [&](int i) { return s_pair[row0 + i]; }, hs, hsum);
+            stage_dense<MODE>(hbuf, hstride, rows, [&](int i) { return s_pair[row0 + i]; }, hs, hsum);
             __syncthreads();
         }
         for (int it0 = 0; it0 < items; it0 += kWaves * RW) {
@@ -694,7 +744,7 @@ __global__ __launch_bounds__(kThreads) void k_dec_down_fit(FwdArgs a, const uint
         const uint4* ep = reinterpret_cast<const uint4*>(&table->ent[u]);
         const uint4 hd = ep[0], p0 = ep[1], p1 = ep[2];
         if (it0 == 0) {   // h rows of every pair, in the same round trip
-            stage_rows<MODE>(hbuf, hstride, PT, [](int i) { return i; }, hs, hsum);
+            stage_dense<MODE>(hbuf, hstride, PT, [](int i) { return i; }, hs, hsum);
         }
         const int nt = in_range ? (int)hd.y : 0;
         int slot = nt > 0 ? (int)hd.x : 0;
@@ -801,7 +851,10 @@ hipError_t launch_mode(const FwdArgs& a, uint16_t* hbuf, DecTable* table, int ph
     const int Imax = a.I > a.I_sh ? a.I : a.I_sh;
     if (phases & 1) {
         int SP, upl_;
-        pick_split(a.H / 64, 2, SP, upl_);
+        // one unit per lane where the row allows it: twice the waves of two units per lane,
+        // each with half the dequant-dot work and far fewer registers (measured faster on
+        // H = 2048: 11.1 -> 10.2 us per layer)
+        pick_split(a.H / 64, 1, SP, upl_);
         hipError_t err = [&]() -> hipError_t { BRX_UPL_CASES(launch_gateup, a, hbuf, table, nu, Imax, SP, s); }();
         if (err != hipSuccess) return err;
     }
