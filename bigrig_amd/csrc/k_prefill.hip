@@ -6,9 +6,11 @@
 // restores (token, k) order (stream.py:1558-1561, _scatter_unsort 1829-1831), followed by the
 // caller's router-weighted combine (stream.py:1523-1525).
 //
-//   k_bucket   one block per expert: histogram of all pairs, the expert's run offset and
-//              M-tile offset, the stable (pair-order) compaction of its pairs, and one tile
-//              descriptor {expert, first bucketed row, rows, slot} per 128-row M tile.
+//   k_bucket   one block per expert: histogram of all pairs, the expert's run offset, the
+//              stable (pair-order) compaction of its pairs, and one tile descriptor {expert,
+//              first bucketed row, rows, slot} per 128-row M tile, placed in a tile list that
+//              holds every tile of more than 64 rows before the smaller ones, so the GEMM grids
+//              dispatch the long tiles first and the short ones fill the end.
 //   k_pf_gemm  grouped GEMM, tile = (M tile of one expert's pairs, 256 columns), one wave
 //              per SIMD.  KIND 0 (gate/up): A rows are the pairs' token activations gathered
 //              from x, B rows the gate and up weights of 128 intermediate features; the
@@ -38,66 +40,120 @@ constexpr int kThreads = 256;
 constexpr int kXcd = 8;
 
 // ------------------------------------------------------------------ bucketing
-__global__ __launch_bounds__(1024) void k_bucket(const int32_t* __restrict__ pexp, int P, int E,
-                                                  int E_ext, int T_sh, int BM,
-                                                  const int32_t* __restrict__ g2s, int capacity,
-                                                  int32_t* __restrict__ order,
-                                                  int32_t* __restrict__ offsets,
-                                                  int32_t* __restrict__ tile_start,
-                                                  int4* __restrict__ tinfo) {
+// Pairs are read coalesced: in each pass of kBucketPass pairs, wave w takes the 1024 pairs
+// [w * 1024, w * 1024 + 1024) and its lane l the pairs l + 64 i (i < 16), so a load
+// instruction reads 64 consecutive pairs, and the histogram's LDS atomics of one instruction
+// (8 tokens x top-8, distinct experts within a token) hit one address at most 8 times. The
+// stable compaction of a pass is 16 ballots per wave and one scan of the 16 wave totals.
+constexpr int kBucketThreads = 1024;
+constexpr int kBucketPer = 16;                                 // pairs per lane per pass
+constexpr int kBucketWaveRun = kWave * kBucketPer;            // pairs per wave per pass
+constexpr int kBucketPass = kBucketThreads * kBucketPer;
+
+__device__ __forceinline__ int bucket_expert(const int32_t* __restrict__ pexp, int p, int P, int E, int emax) {
+    return p < P ? min(max(pexp[p], 0), emax) : E;
+}
+
+__global__ __launch_bounds__(kBucketThreads) void k_bucket(const int32_t* __restrict__ pexp, int P, int E,
+                                                           int E_ext, int T_sh, int BM,
+                                                           const int32_t* __restrict__ g2s, int capacity,
+                                                           int32_t* __restrict__ order,
+                                                           int32_t* __restrict__ offsets,
+                                                           int32_t* __restrict__ tile_start,
+                                                           int4* __restrict__ tinfo) {
     // E_ext = E + 1 when a shared expert exists (id E); T_sh shared pairs follow the P routed
     extern __shared__ int32_t hist[];     // [E_ext]
-    __shared__ int32_t wsum[16];
-    __shared__ int32_t base_s[2];
+    constexpr int kNw = kBucketThreads / kWave;
+    __shared__ int32_t wsum[kNw];
+    __shared__ int32_t base_s[3];
     const int P_ext = P + T_sh;
     const int emax = E_ext - 1;
     const int e = blockIdx.x;
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, nw = blockDim.x >> 6;
-    for (int i = tid; i < E_ext; i += blockDim.x) hist[i] = 0;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    for (int i = tid; i < E_ext; i += kBucketThreads) hist[i] = 0;
     __syncthreads();
-    for (int p = tid; p < P_ext; p += blockDim.x) {
-        int ex = p < P ? min(max(pexp[p], 0), emax) : E;
-        atomicAdd(&hist[ex], 1);
+    // histogram of every pair's expert (each block needs all counts below its own expert)
+    for (int p0 = 0; p0 < P_ext; p0 += kBucketPass) {
+        const int pb = p0 + wv * kBucketWaveRun + lane;
+        int ex[kBucketPer];
+#pragma unroll
+        for (int i = 0; i < kBucketPer; ++i) ex[i] = bucket_expert(pexp, min(pb + i * kWave, P_ext - 1), P, E, emax);
+#pragma unroll
+        for (int i = 0; i < kBucketPer; ++i)
+            if (pb + i * kWave < P_ext) atomicAdd(&hist[ex[i]], 1);
     }
     __syncthreads();
     if (wv == 0) {
-        // offsets of expert e: sum of the counts (and of the M tiles) of the experts before it
-        int off = 0, toff = 0;
-        for (int j = lane; j < e; j += 64) { off += hist[j]; toff += (hist[j] + BM - 1) / BM; }
-        for (int s = 32; s >= 1; s >>= 1) { off += __shfl_xor(off, s, 64); toff += __shfl_xor(toff, s, 64); }
+        // expert e's run offset (counts of the experts before it) and its tiles' places in the
+        // tile list, which holds the tiles of more than BM / 2 rows of every expert first, then
+        // the smaller ones (at most one per expert, its last), each class in expert order, so
+        // the GEMMs take the long tiles first
+        int off = 0, big = 0, small = 0, big_all = 0, small_all = 0;
+        for (int j = lane; j < E_ext; j += 64) {
+            const int n = hist[j], r = n % BM;
+            const int nb = n / BM + (r > BM / 2 ? 1 : 0), ns = (r > 0 && r <= BM / 2) ? 1 : 0;
+            if (j < e) { off += n; big += nb; small += ns; }
+            big_all += nb;
+            small_all += ns;
+        }
+        for (int sft = 32; sft >= 1; sft >>= 1) {
+            off += __shfl_xor(off, sft, 64);
+            big += __shfl_xor(big, sft, 64);
+            small += __shfl_xor(small, sft, 64);
+            big_all += __shfl_xor(big_all, sft, 64);
+            small_all += __shfl_xor(small_all, sft, 64);
+        }
         if (lane == 0) {
             base_s[0] = off;
-            base_s[1] = toff;
+            base_s[1] = big;
+            base_s[2] = big_all + small;
             offsets[e] = off;
-            tile_start[e] = toff;
+            tile_start[e] = big;
             if (e == E_ext - 1) {
                 offsets[E_ext] = P_ext;
-                tile_start[E_ext] = toff + (hist[e] + BM - 1) / BM;
+                tile_start[E_ext] = big_all + small_all;   // tiles in all (what the GEMMs read)
             }
         }
     }
     __syncthreads();
     if (tinfo) {
-        const int n = hist[e], off = base_s[0], toff = base_s[1];
+        const int n = hist[e], off = base_s[0], big = base_s[1], small = base_s[2];
         int slot = 0;
         if (e < E && g2s) slot = min(max(g2s[e], 0), capacity - 1);
-        for (int j = tid; j * BM < n; j += blockDim.x)
-            tinfo[toff + j] = make_int4(e, off + j * BM, min(BM, n - j * BM), slot);
-    }
-    int run = base_s[0];
-    for (int p0 = 0; p0 < P_ext; p0 += blockDim.x) {
-        int p = p0 + tid;
-        bool m = false;
-        if (p < P_ext) {
-            int ex = p < P ? min(max(pexp[p], 0), emax) : E;
-            m = ex == e;
+        for (int j = tid; j * BM < n; j += kBucketThreads) {
+            const int rows = min(BM, n - j * BM);
+            tinfo[rows > BM / 2 ? big + j : small] = make_int4(e, off + j * BM, rows, slot);
         }
-        uint64_t b = __ballot(m);
-        if (lane == 0) wsum[wv] = __popcll(b);
+    }
+    // stable compaction of expert e's pairs, pair order = (pass, wave, i, lane)
+    const uint64_t below = (1ull << lane) - 1ull;
+    int run = base_s[0];
+    for (int p0 = 0; p0 < P_ext; p0 += kBucketPass) {
+        const int pb = p0 + wv * kBucketWaveRun + lane;
+        uint64_t m[kBucketPer];
+        int cnt = 0;
+#pragma unroll
+        for (int i = 0; i < kBucketPer; ++i) {
+            const int p = pb + i * kWave;
+            const int ex = bucket_expert(pexp, min(p, P_ext - 1), P, E, emax);
+            m[i] = __ballot(p < P_ext && ex == e);
+            cnt += __popcll(m[i]);
+        }
+        if (lane == 0) wsum[wv] = cnt;
         __syncthreads();
         int before = 0, total = 0;
-        for (int w = 0; w < nw; ++w) { if (w < wv) before += wsum[w]; total += wsum[w]; }
-        if (m) order[run + before + __popcll(b & ((1ull << lane) - 1ull))] = p;
+#pragma unroll
+        for (int w = 0; w < kNw; ++w) {
+            const int v = wsum[w];
+            before += w < wv ? v : 0;
+            total += v;
+        }
+        int dst = run + before;
+#pragma unroll
+        for (int i = 0; i < kBucketPer; ++i) {
+            if ((m[i] >> lane) & 1ull) order[dst + __popcll(m[i] & below)] = pb + i * kWave;
+            dst += __popcll(m[i]);
+        }
         run += total;
         __syncthreads();
     }
@@ -548,7 +604,7 @@ hipError_t launch_gemm(const FwdArgs& a, const PfWs& w, int E_ext, int Imax, uin
 hipError_t launch_bucket(const int32_t* pexp, int P, int E, int E_ext, int T_sh, int BM,
                          const int32_t* g2s, int capacity, int32_t* order, int32_t* offsets,
                          int32_t* tile_start, int4* tinfo, hipStream_t s) {
-    hipLaunchKernelGGL(k_bucket, dim3(E_ext), dim3(1024), sizeof(int32_t) * E_ext, s, pexp, P, E,
+    hipLaunchKernelGGL(k_bucket, dim3(E_ext), dim3(kBucketThreads), sizeof(int32_t) * E_ext, s, pexp, P, E,
                        E_ext, T_sh, BM, g2s, capacity, order, offsets, tile_start, tinfo);
     return hipGetLastError();
 }
