@@ -56,7 +56,7 @@ def parse():
     ap.add_argument("--pool-capacity", type=int, default=32)
     ap.add_argument("--pool-tokens", type=int, default=64)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--skip", default="", help="comma list of: prefill,pool,cpu,graph")
+    ap.add_argument("--skip", default="", help="comma list of: prefill,pool,cpu,graph,report")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB (--steps times): the "
                          "known-size reference for scaling HBM byte counters")
@@ -89,6 +89,7 @@ class Stack:
         self.spec = spec
         self.layers = layers
         self.pools, self.routers, self.biases, self.xbank = [], [], [], []
+        self.shared, self.shared_gate = [], []   # per layer, when the spec has a shared expert
         self.host = HostStore()
         t0 = time.time()
         for l in range(layers):
@@ -107,6 +108,12 @@ class Stack:
             self.routers.append(synth.router_weights(spec, seed=2000 + l))
             self.biases.append(synth.zipf_bias_torch(spec.n_experts, 1.1, seed=3000 + l))
             self.xbank.append(synth.activations(bank, spec.hidden, seed=4000 + l))
+            if spec.shared_inter:
+                self.shared.append(synth.make_layer_experts(spec, seed=5000 + l, shared=True)[0].contiguous())
+                g = torch.Generator(device="cuda")
+                g.manual_seed(5500 + l)
+                self.shared_gate.append((torch.randn(spec.hidden, generator=g, device="cuda") * 0.02)
+                                        .to(torch.bfloat16))
         torch.cuda.synchronize()
         for p in self.pools:
             p.g2s_device(torch.cuda.current_stream().cuda_stream)
@@ -303,6 +310,137 @@ def prefill_bench(args, st: "Stack"):
     }
 
 
+def decode_report(st: "Stack", T: int, graphs: int = 4, reps: int = 25):
+    """Kernel-level decode of T tokens through every layer of `st` (one brx_moe_block_forward
+    per layer, all experts resident), replayed as HIP graphs over `graphs` input rows."""
+    import ctypes as C
+
+    import torch
+
+    from bigrig_amd import lib as L
+    spec, Ln = st.spec, st.layers
+    lib = L.load()
+    d = spec.desc()
+    dref = C.byref(d)
+    H, k = spec.hidden, spec.top_k
+    outs = [torch.empty((T, H), dtype=torch.bfloat16, device="cuda") for _ in range(Ln)]
+    idx = [[torch.empty((T, k), dtype=torch.int32, device="cuda") for _ in range(Ln)] for _ in range(graphs)]
+
+    def step(g, stream):
+        for l in range(Ln):
+            x = st.xbank[l][g * T:(g + 1) * T]
+            sh = bool(spec.shared_inter)
+            L.check(lib.brx_moe_block_forward(dref, st.pools[l].device.handle, x.data_ptr(),
+                                              st.routers[l].data_ptr(), st.biases[l].data_ptr(),
+                                              st.shared_gate[l].data_ptr() if sh else None,
+                                              st.shared[l].data_ptr() if sh else None, T,
+                                              outs[l].data_ptr(), idx[g][l].data_ptr(), None,
+                                              L.FWD_FORCE_DECODE, stream))
+
+    gs = []
+    for g in range(graphs):
+        step(g, torch.cuda.current_stream().cuda_stream)
+        cg = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(cg):
+            step(g, torch.cuda.current_stream().cuda_stream)
+        gs.append(cg)
+    torch.cuda.synchronize()
+    for cg in gs:
+        cg.replay()
+    torch.cuda.synchronize()
+    s = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(s)
+    for r in range(reps):
+        gs[r % graphs].replay()
+    e1.record(s)
+    torch.cuda.synchronize()
+    us_layer = e0.elapsed_time(e1) * 1e3 / (reps * Ln)
+    distinct = sum(len(torch.unique(i)) for row in idx for i in row) / (graphs * Ln)
+    router_b = spec.n_experts * H * (4 if spec.router_dtype == "float32" else 2)
+    nbytes = distinct * spec.bytes_per_expert + router_b + 2 * T * H * 2
+    if spec.shared_inter:
+        from bigrig_amd import formats as F
+        nbytes += F.spec_bytes(spec.expert_spec(True)) + 2 * H
+    del gs
+    return {"tokens": T, "layers": Ln, "us_per_layer": round(us_layer, 3),
+            "layer_tokens_per_s": round(T * 1e6 / us_layer, 1),
+            "distinct_experts": round(distinct, 2), "bytes_per_layer_step": int(nbytes),
+            "hbm_gbs": round(nbytes / (us_layer * 1e-6) / 1e9, 1),
+            "hbm_frac": round(nbytes / (us_layer * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
+def prefill_report(st: "Stack", T: int, reps: int = 3):
+    """One T-token chunk through every layer of `st`: router, bucketing, grouped GEMMs, combine."""
+    import ctypes as C
+
+    import torch
+
+    from bigrig_amd import lib as L
+    from bigrig_amd import synth
+    spec, Ln = st.spec, st.layers
+    lib = L.load()
+    d = spec.desc()
+    dref = C.byref(d)
+    H, k = spec.hidden, spec.top_k
+    xs = [synth.activations(T, H, seed=7000 + l) for l in range(Ln)]
+    out = torch.empty((T, H), dtype=torch.bfloat16, device="cuda")
+    idx = [torch.empty((T, k), dtype=torch.int32, device="cuda") for _ in range(Ln)]
+    sp = torch.cuda.current_stream().cuda_stream
+
+    def chunk():
+        for l in range(Ln):
+            sh = bool(spec.shared_inter)
+            L.check(lib.brx_moe_block_forward(dref, st.pools[l].device.handle, xs[l].data_ptr(),
+                                              st.routers[l].data_ptr(), st.biases[l].data_ptr(),
+                                              st.shared_gate[l].data_ptr() if sh else None,
+                                              st.shared[l].data_ptr() if sh else None, T,
+                                              out.data_ptr(), idx[l].data_ptr(), None,
+                                              L.FWD_FORCE_PREFILL, sp))
+
+    chunk()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        chunk()
+    torch.cuda.synchronize()
+    us_layer = (time.perf_counter() - t0) * 1e6 / (reps * Ln)
+    hit = sum(len(torch.unique(i)) for i in idx) / Ln
+    nbytes = hit * spec.bytes_per_expert + spec.n_experts * H * 2 + 2 * 2 * T * H
+    flops = 2.0 * T * k * 3 * H * spec.inter
+    return {"tokens": T, "layers": Ln, "us_per_layer": round(us_layer, 2),
+            "tokens_per_s_all_layers": round(T * 1e6 / (us_layer * Ln), 1),
+            "experts_hit": round(hit, 1), "bytes_per_layer": int(nbytes),
+            "hbm_gbs": round(nbytes / (us_layer * 1e-6) / 1e9, 1),
+            "hbm_frac": round(nbytes / (us_layer * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "tflops": round(flops / (us_layer * 1e-6) / 1e12, 1),
+            "mfma_frac": round(flops / (us_layer * 1e-6) / 1e12 / BF16_PEAK_TFLOPS, 4)}
+
+
+def config_report():
+    """The other shapes of the workload list, kernel level, all experts resident: OLMoE decode,
+    256 experts + shared expert decode at batch 1 and 8, gpt-oss MXFP4 decode and a 512-token
+    prefill. Fewer layers than the full stacks (distinct layers, 1.8-6.8 GB of weights, far
+    beyond the 256 MB last-level cache, so every step reads its experts from HBM)."""
+    import torch
+
+    from bigrig_amd.spec import E256_SHARED, GPT_OSS_120B, OLMOE_1B_7B
+    rep = {}
+    st = Stack(OLMOE_1B_7B, 8, bank=32)
+    rep["olmoe_1b_7b_decode_b1"] = decode_report(st, 1)
+    del st
+    st = Stack(E256_SHARED, 8, bank=32)
+    rep["e256_shared_decode_b1"] = decode_report(st, 1)
+    rep["e256_shared_decode_b8"] = decode_report(st, 8)
+    del st
+    st = Stack(GPT_OSS_120B, 4, bank=32)
+    rep["gpt_oss_120b_decode_b1"] = decode_report(st, 1)
+    rep["gpt_oss_120b_prefill_512"] = prefill_report(st, 512)
+    del st
+    torch.cuda.empty_cache()
+    return rep
+
+
 def pool_bench(args, st: "Stack"):
     """Bounded pool end to end: C of E experts per layer resident, misses copied from pinned
     host memory, one routing read-back per layer. PCIe-inclusive; never the headline value."""
@@ -426,6 +564,12 @@ def main():
     if "cpu" not in skip:
         log("cpu baseline")
         cpu = cpu_bench(args, st)
+    report = None
+    if "report" not in skip:
+        log("other shapes")
+        del st
+        torch.cuda.empty_cache()
+        report = config_report()
     traffic = None
     tp = os.path.join(ROOT, "profiles", "traffic_decode_gateup.json")
     if os.path.exists(tp):
@@ -489,6 +633,8 @@ def main():
             "layer_tflops": round(pre["layer_tflops"], 1),
             "max_expert_rows": pre["max_expert_rows"], "experts_hit": pre["experts_hit"],
         }
+    if report is not None:
+        rec["report"] = report
     if pool is not None:
         rec["bounded_pool"] = {k2: (round(v, 4) if isinstance(v, float) else v)
                                for k2, v in pool.items()}

@@ -6,10 +6,11 @@
 // router-weighted combine (stream.py:1523-1525).
 //
 // Two kernels per layer:
-//   k_dec_gateup  grid (row block, expert entry): gate and up rows of one expert for every
-//                 token routed to it, act() in the epilogue, h -> bf16 workspace; its blocks of
-//                 row block 0 also record the entry table the down kernel reads. With the
-//                 layer's router logits given, every block first ranks the top-k itself.
+//   k_dec_gateup  grid (row block, entry row y < 16): gate and up rows of one expert for every
+//                 token routed to it (entries y, y + 16, ... of the step), act() in the
+//                 epilogue, h -> bf16 workspace; its blocks of row block 0 also record the
+//                 entry table the down kernel reads. With the layer's router logits given,
+//                 every block first ranks the top-k itself.
 //   k_dec_down    grid (row block of H): down rows of every entry, each pair's bf16 row result,
 //                 and the k-ordered combine out[t] = sum_j w[t,j] * y[t,j].
 // An entry is a run of at most 8 pairs routed to one expert (so an expert is read once for all
@@ -413,10 +414,10 @@ __device__ __forceinline__ void stage_rows(const uint16_t* __restrict__ src, int
 // ------------------------------------------------------------------ gate/up
 // Wave w of the block owns rows w * RW + g (g = lane / SP, RW = 64 / SP) of the block's
 // RB = 4 RW rows, for both the gate and the up projection.
-template <int MODE, int UPL, int KP>
+template <int MODE, int UPL, int KP, bool MULTI>
 __global__ __launch_bounds__(kThreads) void k_dec_gateup(FwdArgs a, uint16_t* __restrict__ hbuf,
                                                          int hstride, DecTable* __restrict__ table,
-                                                         int lsp) {
+                                                         int lsp, int nu) {
     prefetch_args(a);
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     __shared__ int32_t s_e[kWave];   // P <= 64 pairs
@@ -436,77 +437,159 @@ __global__ __launch_bounds__(kThreads) void k_dec_gateup(FwdArgs a, uint16_t* __
     if constexpr (KP == 0) pe = a.pexp[min(lane, a.P - 1)];
     RouteRegs<(KP > 0 ? KP : 1)> rg;
     if constexpr (KP > 0) route_load<KP>(a, rg);
+    // MULTI (several tokens): most of the P + 1 possible entries are empty, so a block takes
+    // entries y, y + 16, ... and stages x only once it has one, after the routing; otherwise
+    // (one token) every block has its entry and x rides in the routing round trip
+    constexpr bool late_x = MULTI;
     StageRegs st;
     auto tok_row = [](int i) { return i; };
-    stage_issue(a.x, H, a.T, tok_row, 0, st);
+    if (!late_x) stage_issue(a.x, H, a.T, tok_row, 0, st);
     if (tid < a.E) s_g2s[tid] = g2s0;
     if (tid + kThreads < a.E) s_g2s[tid + kThreads] = g2s1;
     if constexpr (KP == 0)
         if (tid < a.P) s_e[tid] = pe;
-    stage_store<MODE>(H, a.T, 0, st, xs, xsum);
-    stage_rows<MODE>(a.x, H, a.T, tok_row, xs, xsum, kStageB);
+    if (!late_x) {
+        stage_store<MODE>(H, a.T, 0, st, xs, xsum);
+        stage_rows<MODE>(a.x, H, a.T, tok_row, xs, xsum, kStageB);
+    }
     if constexpr (KP > 0) route_rank<KP>(a, rg, s_e, blockIdx.x == 0 && blockIdx.y == 0);
     __syncthreads();
-    const int e_raw = lane < a.P ? s_e[lane] : 0;
-    Entry en;
-    int n;
-    if (!plan_entry(a, blockIdx.y, e_raw, s_g2s, en, n)) {
-        if (blockIdx.x == 0 && tid == 0) {    // no entry here: an empty table row
-            table->ent[blockIdx.y].slot = 0;
-            table->ent[blockIdx.y].nt = 0;
+    if constexpr (!MULTI) {
+        const int e_raw = lane < a.P ? s_e[lane] : 0;
+        Entry en;
+        int n;
+        if (!plan_entry(a, blockIdx.y, e_raw, s_g2s, en, n)) {
+            if (blockIdx.x == 0 && tid == 0) {    // no entry here: an empty table row
+                table->ent[blockIdx.y].slot = 0;
+                table->ent[blockIdx.y].nt = 0;
+            }
+            return;
         }
-        return;
-    }
-    if (blockIdx.x == 0 && tid == 0) {        // the entry table for the down kernel
-        DecEntry& d = table->ent[blockIdx.y];
-        d.slot = en.slot;
-        d.nt = en.nt;
-        PairIter it{en.mm, 0};
+        if (blockIdx.x == 0 && tid == 0) {        // the entry table for the down kernel
+            DecEntry& d = table->ent[blockIdx.y];
+            d.slot = en.slot;
+            d.nt = en.nt;
+            PairIter it{en.mm, 0};
+            for (int i = 0; i < en.nt; ++i) {
+                int tok;
+                d.pair[i] = it.next(a, en, tok);
+            }
+            if (blockIdx.y == 0) table->n = n;
+        }
+        const bool sh = en.e >= a.E;
+        const int inter = sh ? a.I_sh : a.I;
+        const int RW = kWave >> lsp;
+        const int r0 = blockIdx.x * kWaves * RW;
+        if (r0 >= inter) return;
+        const Layout& L = sh ? a.lay_sh : a.lay;
+        const uint8_t* base = slot_base(a, en.slot);
+        const int g = lane >> lsp, sl = lane & (SP - 1);
+        const int rr = (tid >> 6) * RW + g;
+        const int row = min(r0 + rr, inter - 1);
+
+        Units<MODE, UPL> ug, uu;
+        units_load<MODE, UPL>(base, L.p[0], row, sl, SP, ug);
+        units_load<MODE, UPL>(base, L.p[1], row, sl, SP, uu);
+        float bg = 0.f, bu = 0.f;
+        if (L.p[0].bias >= 0) {
+            bg = bf2f(reinterpret_cast<const uint16_t*>(base + L.p[0].bias)[row]);
+            bu = bf2f(reinterpret_cast<const uint16_t*>(base + L.p[1].bias)[row]);
+        }
+        PairIter pit{en.mm, 0};
         for (int i = 0; i < en.nt; ++i) {
             int tok;
-            d.pair[i] = it.next(a, en, tok);
-        }
-        if (blockIdx.y == 0) table->n = n;
-    }
-    const bool sh = en.e >= a.E;
-    const int inter = sh ? a.I_sh : a.I;
-    const int RW = kWave >> lsp;
-    const int r0 = blockIdx.x * kWaves * RW;
-    if (r0 >= inter) return;
-    const Layout& L = sh ? a.lay_sh : a.lay;
-    const uint8_t* base = slot_base(a, en.slot);
-    const int g = lane >> lsp, sl = lane & (SP - 1);
-    const int rr = (tid >> 6) * RW + g;
-    const int row = min(r0 + rr, inter - 1);
-
-    Units<MODE, UPL> ug, uu;
-    units_load<MODE, UPL>(base, L.p[0], row, sl, SP, ug);
-    units_load<MODE, UPL>(base, L.p[1], row, sl, SP, uu);
-    float bg = 0.f, bu = 0.f;
-    if (L.p[0].bias >= 0) {
-        bg = bf2f(reinterpret_cast<const uint16_t*>(base + L.p[0].bias)[row]);
-        bu = bf2f(reinterpret_cast<const uint16_t*>(base + L.p[1].bias)[row]);
-    }
-    PairIter pit{en.mm, 0};
-    for (int i = 0; i < en.nt; ++i) {
-        int tok;
-        const int pair = pit.next(a, en, tok);
-        float pg = 0.f, pu = 0.f;
-#pragma unroll
-        for (int j = 0; j < UPL; ++j) {
-            const int un = sl + SP * j;
-            if (un < U) {
-                const uint4* xu = reinterpret_cast<const uint4*>(xs + ((int64_t)tok * U + un) * kXU);
-                const float sx = MODE == BRX_QUANT_AFFINE ? xsum[tok * U + un] : 0.0f;
-                pg += unit_dot<MODE, UPL>(ug, j, xu, sx, a.scale_f16);
-                pu += unit_dot<MODE, UPL>(uu, j, xu, sx, a.scale_f16);
+            const int pair = pit.next(a, en, tok);
+            float pg = 0.f, pu = 0.f;
+    #pragma unroll
+            for (int j = 0; j < UPL; ++j) {
+                const int un = sl + SP * j;
+                if (un < U) {
+                    const uint4* xu = reinterpret_cast<const uint4*>(xs + ((int64_t)tok * U + un) * kXU);
+                    const float sx = MODE == BRX_QUANT_AFFINE ? xsum[tok * U + un] : 0.0f;
+                    pg += unit_dot<MODE, UPL>(ug, j, xu, sx, a.scale_f16);
+                    pu += unit_dot<MODE, UPL>(uu, j, xu, sx, a.scale_f16);
+                }
+            }
+            pg = group_sum(pg, SP);
+            pu = group_sum(pu, SP);
+            if (sl == 0 && r0 + rr < inter) {
+                const float h = act_apply(a.act, pg + bg, pu + bu, a.alpha, a.limit);
+                hbuf[(int64_t)pair * hstride + r0 + rr] = (uint16_t)f2bf(h);
             }
         }
-        pg = group_sum(pg, SP);
-        pu = group_sum(pu, SP);
-        if (sl == 0 && r0 + rr < inter) {
-            const float h = act_apply(a.act, pg + bg, pu + bu, a.alpha, a.limit);
-            hbuf[(int64_t)pair * hstride + r0 + rr] = (uint16_t)f2bf(h);
+    } else {
+        const int e_raw = lane < a.P ? s_e[lane] : 0;
+        // entries by, by + NB, ... (NB = gridDim.y); x is staged once, with the first entry
+        const int NB = gridDim.y;
+        bool staged = false;
+        for (int u = blockIdx.y; u < nu; u += NB) {
+            Entry en;
+            int n;
+            if (!plan_entry(a, u, e_raw, s_g2s, en, n)) {
+                if (blockIdx.x == 0 && tid == 0)      // entry rows past the last: empty table rows
+                    for (int v = u; v < nu; v += NB) {
+                        table->ent[v].slot = 0;
+                        table->ent[v].nt = 0;
+                    }
+                return;
+            }
+            if (blockIdx.x == 0 && tid == 0) {        // the entry table for the down kernel
+                DecEntry& d = table->ent[u];
+                d.slot = en.slot;
+                d.nt = en.nt;
+                PairIter it{en.mm, 0};
+                for (int i = 0; i < en.nt; ++i) {
+                    int tok;
+                    d.pair[i] = it.next(a, en, tok);
+                }
+                if (u == 0) table->n = n;
+            }
+            const bool sh = en.e >= a.E;
+            const int inter = sh ? a.I_sh : a.I;
+            const int RW = kWave >> lsp;
+            const int r0 = blockIdx.x * kWaves * RW;
+            if (r0 >= inter) continue;   // uniform
+            const Layout& L = sh ? a.lay_sh : a.lay;
+            const uint8_t* base = slot_base(a, en.slot);
+            const int g = lane >> lsp, sl = lane & (SP - 1);
+            const int rr = (tid >> 6) * RW + g;
+            const int row = min(r0 + rr, inter - 1);
+
+            Units<MODE, UPL> ug, uu;
+            units_load<MODE, UPL>(base, L.p[0], row, sl, SP, ug);
+            units_load<MODE, UPL>(base, L.p[1], row, sl, SP, uu);
+            float bg = 0.f, bu = 0.f;
+            if (L.p[0].bias >= 0) {
+                bg = bf2f(reinterpret_cast<const uint16_t*>(base + L.p[0].bias)[row]);
+                bu = bf2f(reinterpret_cast<const uint16_t*>(base + L.p[1].bias)[row]);
+            }
+            if (!staged) {   // the weights are in flight
+                stage_dense<MODE>(a.x, H, a.T, tok_row, xs, xsum);
+                __syncthreads();
+                staged = true;
+            }
+            PairIter pit{en.mm, 0};
+            for (int i = 0; i < en.nt; ++i) {
+                int tok;
+                const int pair = pit.next(a, en, tok);
+                float pg = 0.f, pu = 0.f;
+    #pragma unroll
+                for (int j = 0; j < UPL; ++j) {
+                    const int un = sl + SP * j;
+                    if (un < U) {
+                        const uint4* xu = reinterpret_cast<const uint4*>(xs + ((int64_t)tok * U + un) * kXU);
+                        const float sx = MODE == BRX_QUANT_AFFINE ? xsum[tok * U + un] : 0.0f;
+                        pg += unit_dot<MODE, UPL>(ug, j, xu, sx, a.scale_f16);
+                        pu += unit_dot<MODE, UPL>(uu, j, xu, sx, a.scale_f16);
+                    }
+                }
+                pg = group_sum(pg, SP);
+                pu = group_sum(pu, SP);
+                if (sl == 0 && r0 + rr < inter) {
+                    const float h = act_apply(a.act, pg + bg, pu + bu, a.alpha, a.limit);
+                    hbuf[(int64_t)pair * hstride + r0 + rr] = (uint16_t)f2bf(h);
+                }
+            }
         }
     }
 }
@@ -736,6 +819,7 @@ __global__ __launch_bounds__(kThreads) void k_dec_down_fit(FwdArgs a, const uint
     const int items = nu * RBD;
 
     for (int it0 = 0; it0 < items; it0 += kWaves * RW) {
+        if (it0 > 0 && it0 >= table->n * RBD) break;   // passes past the step's entries: no work
         const int it = it0 + (tid >> 6) * RW + g;
         const bool in_range = it < items;
         const int u = min(it >> lrbd, nu - 1);
@@ -800,11 +884,19 @@ template <int MODE, int UPL>
 hipError_t launch_gateup(const FwdArgs& a, uint16_t* hbuf, DecTable* table, int nu, int Imax, int SP,
                          hipStream_t s) {
     const int RB = kWaves * (kWave / SP);
-    dim3 grid((Imax + RB - 1) / RB, nu), block(kThreads);
+    // entry rows: one per block row up to 16; past that (several tokens, where most of the
+    // P + 1 possible entries are empty) a block takes entries y, y + 16, ...
+    dim3 grid((Imax + RB - 1) / RB, a.T > 1 && nu > 16 ? 16 : nu), block(kThreads);
     // staged x of up to T tokens
     const size_t lds = (size_t)a.T * (a.H / 64) * (kXU + 4);
     const int lsp = __builtin_ctz(SP);
-#define BRX_GU(KP) hipLaunchKernelGGL((k_dec_gateup<MODE, UPL, KP>), grid, block, lds, s, a, hbuf, Imax, table, lsp)
+#define BRX_GU(KP)                                                                                     \
+    do {                                                                                               \
+        if (a.T > 1)                                                                                   \
+            hipLaunchKernelGGL((k_dec_gateup<MODE, UPL, KP, true>), grid, block, lds, s, a, hbuf, Imax, table, lsp, nu); \
+        else                                                                                           \
+            hipLaunchKernelGGL((k_dec_gateup<MODE, UPL, KP, false>), grid, block, lds, s, a, hbuf, Imax, table, lsp, nu); \
+    } while (0)
     if (!a.logits) BRX_GU(0);
     else if (a.E <= 64) BRX_GU(1);
     else if (a.E <= 128) BRX_GU(2);
@@ -821,6 +913,10 @@ hipError_t launch_down(const FwdArgs& a, uint16_t* hbuf, DecTable* table, int nu
     const int per_pass = kWaves * (kWave / SP);
     int RBD = 1;
     while (RBD < 64 && nu * RBD * 2 <= per_pass && a.H % (RBD * 2) == 0) RBD *= 2;
+    // every block stages the h rows of every pair: when they are many (several tokens), give
+    // each block at least H / 256 output rows so the staging is shared by enough of them
+    if ((size_t)PT * Imax * 2 > 32 * 1024)
+        while (RBD < 64 && RBD * 256 < a.H && a.H % (RBD * 2) == 0) RBD *= 2;
     const int Umax = Imax / 64;
     const size_t need = (size_t)PT * Umax * (kXU + 4);
     const int hs_bytes = (int)(need < (size_t)kDownLds ? need : (size_t)kDownLds);
@@ -851,10 +947,11 @@ hipError_t launch_mode(const FwdArgs& a, uint16_t* hbuf, DecTable* table, int ph
     const int Imax = a.I > a.I_sh ? a.I : a.I_sh;
     if (phases & 1) {
         int SP, upl_;
-        // one unit per lane where the row allows it: twice the waves of two units per lane,
-        // each with half the dequant-dot work and far fewer registers (measured faster on
-        // H = 2048: 11.1 -> 10.2 us per layer)
-        pick_split(a.H / 64, 1, SP, upl_);
+        // one token: one unit per lane where the row allows it (twice the waves of two units
+        // per lane, each with half the dequant-dot work and far fewer registers: 11.1 -> 10.2
+        // us per layer on H = 2048); several tokens: two units per lane, half the blocks,
+        // each staging x once for twice the rows
+        pick_split(a.H / 64, a.T > 1 ? 2 : 1, SP, upl_);
         hipError_t err = [&]() -> hipError_t { BRX_UPL_CASES(launch_gateup, a, hbuf, table, nu, Imax, SP, s); }();
         if (err != hipSuccess) return err;
     }
