@@ -269,6 +269,11 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
                                         int nt) {
     constexpr int NA = MF * 16 * 8 / 64 / kGemmWaves;   // A wave-instructions per wave per stage
     constexpr int NV = NA + 2 + (MODE == BRX_QUANT_AFFINE ? 2 : 1);   // loads per wave per stage
+    // stage layout for this tile height: a shorter A tile leaves room in the same ring for
+    // more stages in flight (3 at 128 rows, 4 at 64, 5 at 32)
+    constexpr int SA = MF * 16 * kBK * 2;               // A bytes per stage
+    constexpr int SS = SA + kStB + kStS;                // stage bytes
+    constexpr int NS = (kNS * kStage) / SS;             // stages in the ring
     const bool sh = e >= a.E;
     const int inter = sh ? a.I_sh : a.I;
     const int H = a.H;
@@ -334,20 +339,20 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
 
     auto issue = [&](int s) __attribute__((always_inline)) {
         const int g = min(s, nsteps - 1);
-        uint8_t* st = ring + (s % kNS) * kStage;
+        uint8_t* st = ring + (s % NS) * SS;
 #pragma unroll
         for (int i = 0; i < NA; ++i)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(ra_rsrc, (LDS_PTR)(st + (wv * NA + i) * 1024), 16,
                                                      va[i], g * 128, 0, 0);
 #pragma unroll
         for (int i = 0; i < 2; ++i)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rb_rsrc, (LDS_PTR)(st + kStA + (wv * 2 + i) * 1024), 16,
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rb_rsrc, (LDS_PTR)(st + SA + (wv * 2 + i) * 1024), 16,
                                                      vb[i], wo + g * 32, 0, 0);
         // a 16-bit copy to LDS fills a 32-bit slot per lane (zero-extended)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rb_rsrc, (LDS_PTR)(st + kStA + kStB + wv * 256), 2, vsc,
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rb_rsrc, (LDS_PTR)(st + SA + kStB + wv * 256), 2, vsc,
                                                  so + g * 2, 0, 0);
         if constexpr (MODE == BRX_QUANT_AFFINE)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rb_rsrc, (LDS_PTR)(st + kStA + kStB + 1024 + wv * 256), 2,
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rb_rsrc, (LDS_PTR)(st + SA + kStB + 1024 + wv * 256), 2,
                                                      vsc, bo + g * 2, 0, 0);
     };
     // block row of fragment nj for this lane
@@ -363,15 +368,15 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
         uint32_t s[kNF], b[kNF];
     };
     auto fetch = [&](Frag& f, int s) __attribute__((always_inline)) {
-        const uint8_t* st = ring + (s % kNS) * kStage;
+        const uint8_t* st = ring + (s % NS) * SS;
 #pragma unroll
         for (int nj = 0; nj < kNF; ++nj) {
             const int br = brow[nj];
             const int h = (q >> 1) ^ ((br >> 3) & 1);
-            f.w[nj] = *reinterpret_cast<const u32x2_t*>(st + kStA + (2 * br + h) * 16 + (q & 1) * 8);
-            f.s[nj] = *reinterpret_cast<const uint32_t*>(st + kStA + kStB + br * 4);
+            f.w[nj] = *reinterpret_cast<const u32x2_t*>(st + SA + (2 * br + h) * 16 + (q & 1) * 8);
+            f.s[nj] = *reinterpret_cast<const uint32_t*>(st + SA + kStB + br * 4);
             if constexpr (MODE == BRX_QUANT_AFFINE)
-                f.b[nj] = *reinterpret_cast<const uint32_t*>(st + kStA + kStB + 1024 + br * 4);
+                f.b[nj] = *reinterpret_cast<const uint32_t*>(st + SA + kStB + 1024 + br * 4);
         }
     };
     // word kc of the lane's K chunks, dequantized into MFMA operands
@@ -397,7 +402,7 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
         for (int j = 0; j < kNF; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
     auto mma = [&](int s, const bf16x8_t (&bop)[kNF], int kc) __attribute__((always_inline)) {
-        const uint16_t* As = reinterpret_cast<const uint16_t*>(ring + (s % kNS) * kStage);
+        const uint16_t* As = reinterpret_cast<const uint16_t*>(ring + (s % NS) * SS);
 #pragma unroll
         for (int mi = 0; mi < MF; ++mi) {
             const int m = mi * 16 + (lane & 15);
@@ -409,18 +414,18 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
         }
     };
 
-    // prologue: stages 0 .. kNS - 2 in flight; wait for stages 0 and 1; B(0) kc 0 dequantized
+    // prologue: stages 0 .. NS - 2 in flight; wait for stages 0 and 1; B(0) kc 0 dequantized
 #pragma unroll
-    for (int s = 0; s < kNS - 1; ++s) issue(s);
-    dma_wait_barrier<NV * (kNS - 3)>();
+    for (int s = 0; s < NS - 1; ++s) issue(s);
+    dma_wait_barrier<NV * (NS - 3)>();
     bf16x8_t bop0[kNF], bop1[kNF];
     Frag fc, fn;
     fetch(fc, 0);
     deq(bop0, fc, 0);
     for (int s = 0; s < nsteps; ++s) {
-        // stage s + 1 landed in every wave; stage s - 1's slot is free for stage s + kNS - 1
-        dma_wait_barrier<NV * (kNS - 3)>();
-        issue(s + kNS - 1);
+        // stage s + 1 landed in every wave; stage s - 1's slot is free for stage s + NS - 1
+        dma_wait_barrier<NV * (NS - 3)>();
+        issue(s + NS - 1);
         mma(s, bop0, 0);
         deq(bop1, fc, 1);
         fetch(fn, s + 1);

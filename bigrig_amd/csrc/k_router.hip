@@ -284,9 +284,14 @@ hipError_t launch_router(const brx_layer_desc& d, const void* x, const void* w_r
         return topk_launch(d, T, sgw ? 1 : 0, ws_logits, out_idx, out_w, out_sg, s);
     }
     // many tokens: logits by token tiles, then the same top-k kernel
-    constexpr int TT = 16, RPB = 32;
+    // rows per block: 32 (each weight row read once per 16-token tile, by one wave), fewer
+    // when there are too few token tiles for about 512 blocks (a wave then takes fewer rows)
+    constexpr int TT = 16;
     const int rows = d.n_experts + (sgw ? 1 : 0);
-    dim3 grid((T + TT - 1) / TT, (rows + RPB - 1) / RPB);
+    const int tiles = (T + TT - 1) / TT;
+    int RPB = 32;
+    while (RPB > 4 && tiles * ((rows + RPB - 1) / RPB) < 512) RPB /= 2;
+    dim3 grid(tiles, (rows + RPB - 1) / RPB);
     const size_t lds = sizeof(uint16_t) * (size_t)TT * d.hidden;
     if (f32)
         hipLaunchKernelGGL((k_router_tiled<true, TT>), grid, dim3(kRouterThreads), lds, s, (const uint16_t*)x,
