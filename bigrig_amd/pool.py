@@ -163,8 +163,17 @@ class DeviceSlots:
         self._stage_ev.record(self.copy_stream)
         return raw.nbytes
 
-    def write_device(self, slot: int, dev_ptr: int, nbytes: int) -> int:
+    def write_device(self, slot: int, dev_ptr: int, nbytes: int, src_stream=None) -> int:
+        """Queue the copy of an expert staged in device memory into `slot`. The source is
+        written by work on `src_stream` (default: the current stream), so the copy stream
+        first waits for everything queued there; without that wait the copy can read the
+        staging buffer before its producer has finished writing it."""
+        import torch
         L = self._L
+        src = src_stream if src_stream is not None else torch.cuda.current_stream()
+        ready = torch.cuda.Event()
+        ready.record(src)
+        self.copy_stream.wait_event(ready)
         L.check(L.load().brx_pool_refill_from_device_async(self.handle, slot, dev_ptr, nbytes,
                                                            self.copy_stream.cuda_stream))
         return nbytes
@@ -322,13 +331,15 @@ class ExpertPool:
         self._place(e, slot, t0)
         return slot
 
-    def admit_device(self, e: int, dev_ptr: int, protect=()) -> int:
-        """Admit from device memory (an expert staged on the GPU, stream.py:957-961)."""
+    def admit_device(self, e: int, dev_ptr: int, protect=(), src_stream=None) -> int:
+        """Admit from device memory (an expert staged on the GPU, stream.py:957-961). The copy
+        is ordered after the work queued on `src_stream` (default: the current stream), which
+        is where the staged bytes were written."""
         if not self._built:
             raise RuntimeError("build() must run before admit()")
         t0 = time.perf_counter()
         slot = self._victim(protect=protect)
-        self._slots.write_device(slot, dev_ptr, self.bytes_per_expert)
+        self._slots.write_device(slot, dev_ptr, self.bytes_per_expert, src_stream)
         self._place(e, slot, t0)
         return slot
 

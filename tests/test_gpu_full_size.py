@@ -1,0 +1,99 @@
+"""The workload's full-size layers on the GPU (every expert resident, synthetic weights generated
+and quantized on the device, admitted through the pool's device path): every output is finite,
+and a sample of tokens matches the oracle -- routing indices bit-exact, routing weights to 1e-5,
+layer outputs within 1e-2 relative L2. The oracle cannot run the whole chunk in seconds, so the
+full sizes are checked through the sampled tokens and the all-finite property, which a tile,
+workspace or slot-addressing mistake at these sizes breaks (small layers share none of those
+sizes).
+
+The sizes: Qwen3-30B-A3B shape (hidden 2048, 128 experts, top-8, inter 768, 4-bit affine) for a
+2048-token prefill chunk and a 1-token decode step; gpt-oss-120b shape (hidden 2880, 128
+experts, top-4, inter 2880, MXFP4 + biases, clamped SwiGLU) for a 512-token chunk and one
+decode token; 256 experts + shared expert (inter 512) at batch 8.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from bigrig_amd import formats as F
+from bigrig_amd import layer as ops
+from bigrig_amd.spec import E256_SHARED, GPT_OSS_120B, QWEN3_30B_A3B
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-2
+
+
+def _bits(t):
+    import torch
+    return t.detach().contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def _layer(spec, seed):
+    """(pool, experts uint8 [E, bytes] on the GPU, router w, Zipf bias, shared, shared gate w)."""
+    import torch
+
+    from bigrig_amd import synth
+    from bigrig_amd.pool import ExpertPool
+    experts = synth.make_layer_experts(spec, seed=seed)
+    pool = ExpertPool(0, spec, spec.n_experts).build()
+    for e in range(spec.n_experts):
+        pool.touch([e], [0])
+        pool.admit_device(e, experts[e].data_ptr())
+    pool.g2s_device(torch.cuda.current_stream().cuda_stream)
+    pool.device.sync()
+    wr = synth.router_weights(spec, seed=seed + 1)
+    bias = synth.zipf_bias_torch(spec.n_experts, 1.1, seed=seed + 2)
+    shared = sgw = None
+    if spec.shared_inter:
+        shared = synth.make_layer_experts(spec, seed=seed + 3, shared=True)[0].contiguous()
+        g = torch.Generator(device="cuda")
+        g.manual_seed(seed + 4)
+        sgw = (torch.randn(spec.hidden, generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+    return pool, experts, wr, bias, shared, sgw
+
+
+@pytest.mark.parametrize("spec,T", [(QWEN3_30B_A3B, 2048), (QWEN3_30B_A3B, 1), (GPT_OSS_120B, 512),
+                                    (GPT_OSS_120B, 1), (E256_SHARED, 8)],
+                         ids=["qwen3-prefill2048", "qwen3-decode1", "gptoss-prefill512",
+                              "gptoss-decode1", "e256shared-decode8"])
+def test_full_size_layer(gpu, spec, T):
+    import torch
+
+    from bigrig_amd import synth
+    print(f"[full-size] H={spec.hidden} E={spec.n_experts} I={spec.inter} T={T}", flush=True)
+    pool, experts, wr, bias, shared, sgw = _layer(spec, seed=100 + T)
+    x = synth.activations(T, spec.hidden, seed=200 + T)
+    k = spec.top_k
+    idx = torch.empty((T, k), dtype=torch.int32, device=gpu)
+    w = torch.empty((T, k), dtype=torch.float32, device=gpu)
+    out = ops.moe_block(spec, pool, x, wr, bias, sgw, shared, out_idx=idx, out_w=w,
+                        flags=ops.path_flag(T))
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(out.float()).all()), "non-finite layer outputs"
+
+    toks = sorted({0, T // 3, T // 2, T - 1})
+    xb = _bits(x)[toks]
+    wr_h = wr.cpu().numpy() if spec.router_dtype == "float32" else _bits(wr)
+    sgw_h = None if sgw is None else _bits(sgw)
+    _, oidx, ow, osg = oracle.router(xb, wr_h, spec.router_dtype == "float32", bias.cpu().numpy(),
+                                     k, spec.route_mode, sgw_h)
+    gidx = idx.cpu().numpy()[toks]
+    assert np.array_equal(gidx, oidx), "routing indices differ from the oracle"
+    np.testing.assert_allclose(w.cpu().numpy()[toks], ow, rtol=1e-5, atol=1e-7)
+
+    # only the sampled tokens' experts travel to the host; the other entries alias one of them
+    need = sorted(set(int(e) for e in oidx.reshape(-1)))
+    host = {e: experts[e].cpu().numpy().tobytes() for e in need}
+    elist = [host.get(e, host[need[0]]) for e in range(spec.n_experts)]
+    sh = None if shared is None else shared.cpu().numpy().tobytes()
+    ref, _ = oracle.moe_forward(spec, elist, xb, oidx, ow, sh, osg)
+    got = F.bf16_bits_to_f32(_bits(out)[toks])
+    want = F.bf16_bits_to_f32(ref)
+    assert np.abs(want).max() > 1e-3, "degenerate layer: the oracle output is (near) zero"
+    r = oracle.rel_l2(got, want)
+    print(f"[full-size] sampled tokens {toks}: rel L2 {r:.2e}", flush=True)
+    assert r < TOL, f"rel L2 {r:.3e} against the oracle"
+    pool.close()
+    del experts
+    torch.cuda.empty_cache()
