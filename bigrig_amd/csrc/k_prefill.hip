@@ -230,6 +230,15 @@ __device__ __forceinline__ void dma_wait_barrier() {
     asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
 }
 
+// Copies into LDS a wave has issued after stage s + 1's when it waits for stage s + 1 at
+// iteration s (s of parity par): those of stages s + 2 .. s + ns - 2, nv0 for an even stage,
+// nv1 for an odd one.
+constexpr int loads_after(int ns, int nv0, int nv1, int par) {
+    int n = 0;
+    for (int i = 2; i <= ns - 2; ++i) n += ((par + i) & 1) ? nv1 : nv0;
+    return n;
+}
+
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
 }
@@ -268,7 +277,10 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
                                         uint8_t* ring, int32_t* dst_s, int e, int m0, int rows, int slot,
                                         int nt) {
     constexpr int NA = MF * 16 * 8 / 64 / kGemmWaves;   // A wave-instructions per wave per stage
-    constexpr int NV = NA + 2 + (MODE == BRX_QUANT_AFFINE ? 2 : 1);   // loads per wave per stage
+    // loads per wave of an odd stage (A, B) and of an even stage (A, B and the scale pair of it
+    // and the next stage)
+    constexpr int NV1 = NA + 2;
+    constexpr int NV0 = NV1 + (MODE == BRX_QUANT_AFFINE ? 2 : 1);
     // stage layout for this tile height: a shorter A tile leaves room in the same ring for
     // more stages in flight (3 at 128 rows, 4 at 64, 5 at 32)
     constexpr int SA = MF * 16 * kBK * 2;               // A bytes per stage
@@ -323,6 +335,16 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
         vb[i] = (uint32_t)mat_row(br) * (uint32_t)(K / 2) + h * 16;
     }
     const int wo = (int)L.p[p_w].w, so = (int)L.p[p_w].s, bo = (int)L.p[p_w].b;
+    // the scales of two stages are one 4-byte copy when every scale row and array of the
+    // block's matrices is 4-byte aligned (affine: K / 64 even; MXFP4: K a multiple of 128);
+    // otherwise each stage copies its own 2 bytes (the waits below assume the paired count,
+    // which then makes them wait for one or two more copies than they need)
+    const int rb = K / 32;   // scale bytes per row (affine: K / 64 16-bit values; MXFP4: K / 32 bytes)
+    bool spair = (rb & 3) == 0;
+#pragma unroll
+    for (int pj = 0; pj < 3; ++pj)
+        if (KIND == 0 ? pj < 2 : pj == 2)
+            spair = spair && ((L.p[pj].s & 3) == 0) && (MODE != BRX_QUANT_AFFINE || (L.p[pj].b & 3) == 0);
     const uint32_t vsc = MODE == BRX_QUANT_AFFINE
         ? (uint32_t)mat_row(wv * 64 + lane) * (uint32_t)(K / 64) * 2
         : (uint32_t)mat_row(wv * 64 + lane) * (uint32_t)(K / 32);
@@ -348,12 +370,26 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
         for (int i = 0; i < 2; ++i)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rb_rsrc, (LDS_PTR)(st + SA + (wv * 2 + i) * 1024), 16,
                                                      vb[i], wo + g * 32, 0, 0);
-        // a 16-bit copy to LDS fills a 32-bit slot per lane (zero-extended)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rb_rsrc, (LDS_PTR)(st + SA + kStB + wv * 256), 2, vsc,
-                                                 so + g * 2, 0, 0);
-        if constexpr (MODE == BRX_QUANT_AFFINE)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rb_rsrc, (LDS_PTR)(st + SA + kStB + 1024 + wv * 256), 2,
-                                                     vsc, bo + g * 2, 0, 0);
+        // scales: one 32-bit LDS slot per row. Paired: an even stage's slot holds its 16-bit
+        // scale (and bias) value in the low half and the next stage's in the high half; an odd
+        // stage copies nothing. Unpaired: every stage copies its own 16 bits (a 16-bit copy to
+        // LDS fills a 32-bit slot, zero-extended).
+        if (spair) {
+            if ((s & 1) == 0) {
+                const int gp = g & ~1;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rb_rsrc, (LDS_PTR)(st + SA + kStB + wv * 256), 4, vsc,
+                                                         so + gp * 2, 0, 0);
+                if constexpr (MODE == BRX_QUANT_AFFINE)
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(rb_rsrc, (LDS_PTR)(st + SA + kStB + 1024 + wv * 256),
+                                                             4, vsc, bo + gp * 2, 0, 0);
+            }
+        } else {
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rb_rsrc, (LDS_PTR)(st + SA + kStB + wv * 256), 2, vsc,
+                                                     so + g * 2, 0, 0);
+            if constexpr (MODE == BRX_QUANT_AFFINE)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rb_rsrc, (LDS_PTR)(st + SA + kStB + 1024 + wv * 256), 2,
+                                                         vsc, bo + g * 2, 0, 0);
+        }
     };
     // block row of fragment nj for this lane
     int brow[kNF];
@@ -369,14 +405,18 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
     };
     auto fetch = [&](Frag& f, int s) __attribute__((always_inline)) {
         const uint8_t* st = ring + (s % NS) * SS;
+        // paired scales of an odd stage: the high halves of the previous (even) stage's slots
+        const bool hi = spair && (s & 1);
+        const uint8_t* ss = hi ? ring + ((s - 1) % NS) * SS : st;
+        const int sh = hi ? 16 : 0;
 #pragma unroll
         for (int nj = 0; nj < kNF; ++nj) {
             const int br = brow[nj];
             const int h = (q >> 1) ^ ((br >> 3) & 1);
             f.w[nj] = *reinterpret_cast<const u32x2_t*>(st + SA + (2 * br + h) * 16 + (q & 1) * 8);
-            f.s[nj] = *reinterpret_cast<const uint32_t*>(st + SA + kStB + br * 4);
+            f.s[nj] = (*reinterpret_cast<const uint32_t*>(ss + SA + kStB + br * 4) >> sh) & 0xFFFFu;
             if constexpr (MODE == BRX_QUANT_AFFINE)
-                f.b[nj] = *reinterpret_cast<const uint32_t*>(st + SA + kStB + 1024 + br * 4);
+                f.b[nj] = (*reinterpret_cast<const uint32_t*>(ss + SA + kStB + 1024 + br * 4) >> sh) & 0xFFFFu;
         }
     };
     // word kc of the lane's K chunks, dequantized into MFMA operands
@@ -417,14 +457,17 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
     // prologue: stages 0 .. NS - 2 in flight; wait for stages 0 and 1; B(0) kc 0 dequantized
 #pragma unroll
     for (int s = 0; s < NS - 1; ++s) issue(s);
-    dma_wait_barrier<NV * (NS - 3)>();
+    dma_wait_barrier<loads_after(NS, NV0, NV1, 0)>();
     bf16x8_t bop0[kNF], bop1[kNF];
     Frag fc, fn;
     fetch(fc, 0);
     deq(bop0, fc, 0);
     for (int s = 0; s < nsteps; ++s) {
         // stage s + 1 landed in every wave; stage s - 1's slot is free for stage s + NS - 1
-        dma_wait_barrier<NV * (NS - 3)>();
+        if (s & 1)
+            dma_wait_barrier<loads_after(NS, NV0, NV1, 1)>();
+        else
+            dma_wait_barrier<loads_after(NS, NV0, NV1, 0)>();
         issue(s + NS - 1);
         mma(s, bop0, 0);
         deq(bop1, fc, 1);
