@@ -238,6 +238,7 @@ __device__ __forceinline__ float wave_route_weight(const float v[kPer], int E, i
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
 // sum_{i} (128 + q_i) * x_i over the 8 nibbles of `wd`, accumulated into acc.
 // xp[i] packs (x_{i}, x_{i+4}) as bf16x2: nibble i and nibble i+4 of the word land in the

@@ -12,13 +12,13 @@
 //              holds every tile of more than 64 rows before the smaller ones, so the GEMM grids
 //              dispatch the long tiles first and the short ones fill the end.
 //   k_pf_gemm  grouped GEMM, tile = (M tile of one expert's pairs, 256 columns), one wave
-//              per SIMD.  KIND 0 (gate/up): A rows are the pairs' token activations gathered
+//              per SIMD, v_mfma_f32_32x32x16_bf16.  KIND 0 (gate/up): A rows are the pairs' token activations gathered
 //              from x, B rows the gate and up weights of 128 intermediate features; the
 //              epilogue applies act() and stores h (bf16) in bucketed order.  KIND 1 (down):
 //              A = h rows, B = down weights of 256 output columns; the epilogue stores each
 //              pair's bf16 row at its (token, k) position.  A is staged through LDS, B is
-//              dequantized from 4-bit straight into MFMA operand registers; v_mfma_f32_16x16x32
-//              _bf16 with fp32 accumulators (details at the kernel).
+//              dequantized from 4-bit straight into MFMA operand registers; fp32 accumulators
+//              (details at the kernel).
 //   k_combine  out[t] = sum_j w[t,j] * y[t,j] (+ shared_gate[t] * y_shared[t]), k-ordered.
 // Every output element is one MFMA accumulation over K in a fixed K order, so a row's value
 // does not depend on which other pairs share its tile.
@@ -172,38 +172,38 @@ __device__ __forceinline__ uint32_t pk_bf16(float lo, float hi) {
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 // ------------------------------------------------------------------ grouped GEMM
-// One block = 256 threads = 4 waves, one wave per SIMD (accumulators in AGPRs); the tile is
-// MF * 16 rows (one M tile of one expert, MF in {2, 4, 8} chosen by the tile's row count) by
-// 256 columns, wave w owning columns [64 w, 64 w + 64) and every row, so each weight is
-// dequantized by exactly one lane and each A fragment read from LDS feeds 4 MFMAs.  KIND 0
-// (gate/up): a wave's 64 columns are 32 gate features and the up rows of the same 32
-// features; KIND 1 (down): 64 output columns.
+// One block = 256 threads = 4 waves, one wave per SIMD; the tile is MF * 16 rows (one M tile
+// of one expert, MF in {2, 4, 8} chosen by the tile's row count) by 256 columns, wave w owning
+// columns [64 w, 64 w + 64) and every row, so each weight is dequantized by exactly one lane
+// and each A fragment read from LDS feeds two MFMAs.  KIND 0 (gate/up): a wave's 64 columns
+// are 32 gate features and the up rows of the same 32 features; KIND 1 (down): 64 output
+// columns.  The MFMA is v_mfma_f32_32x32x16_bf16 (32 x 32 fragments, fp32 accumulators in
+// VGPRs): on gfx950 it issues at close to the bf16 peak next to the dequantization's VALU
+// work, where 16x16x32 loses a third.
 //
-// K order inside a 64-wide stage: v_mfma_f32_16x16x32_bf16 takes from lane l the 8
-// consecutive K of group q = l >> 4.  Here MFMA kc (0, 1) of a stage feeds lane group q the
-// stage's K = 16 q + 8 kc .. + 8, so a lane's B operand for MFMA kc is the 32-bit word
-// 2q + kc of its weight row, and its A operand the 16-byte chunk 2q + kc of the activation
-// row.  Each output is still the sum over all K.
+// K order inside a 64-wide stage: MFMA kk (0..3) takes from lane l the 8 K of chunk
+// 4 (l >> 5) + kk, so a lane's B operands for the stage are the four words of one 16-byte half
+// of its weight row's 32-byte stage segment, and its A operand the matching 16-byte chunk of
+// the activation row.  Each output is still the sum over all K.
 //
 // Everything a stage needs is copied global -> LDS by the buffer unit (buffer_load ... lds,
 // no registers): the A tile (128 rows x 64 bf16, 16-byte chunks XOR-swizzled by row so the
-// 16 rows an MFMA operand read touches fall in 16 distinct bank groups), the block's 256
-// weight rows x 32 bytes (the two 16-byte halves of rows 8..15 of every 16 swapped, for the
-// same reason) and one 16-bit scale (and bias) per row, each in a 32-bit slot (a 16-bit copy
-// to LDS writes 4 bytes per lane).  A ring of kNS stages keeps
-// kNS - 2 stages in flight while the MFMAs consume one; per stage s:
-//   wait until stage s + 1 has landed (s_waitcnt vmcnt(N), N = the later stages' loads);
+// rows an MFMA operand read touches fall in distinct bank groups), the block's 256 weight rows
+// x 32 bytes (the two 16-byte halves of rows 8..15 of every 16 swapped) and each row's scale
+// (and bias) in a 32-bit slot, two stages' values per slot when the scale rows are 4-byte
+// aligned.  A ring of NS stages keeps NS - 2 stages in flight while the MFMAs consume one;
+// per stage s:
+//   wait until stage s + 1 has landed (s_waitcnt vmcnt(N), N = the later stages' copies);
 //   barrier (so every wave's copies are visible and stage s - 1's slot is free);
-//   issue the copies of stage s + kNS - 1;
-//   MFMA kc 0 of stage s  | dequantize B(s) kc 1 from LDS into operand registers
-//   MFMA kc 1 of stage s  | dequantize B(s + 1) kc 0
+//   issue the copies of stage s + NS - 1; read B(s + 1) and its scales from LDS;
+//   MFMA kk of stage s  | dequantize B(s) kk + 1 (kk = 3: B(s + 1) kk 0)
 // Copies past the last stage repeat it.  The waits are explicit (inline asm with a memory
 // clobber, so the compiler moves no LDS access across them); the MFMA-interleaved VALU code
 // is plain C++ so that the compiler's MFMA hazard checks cover it.
 constexpr int kGemmWaves = 4;
 constexpr int kGemmThreads = 64 * kGemmWaves;
-constexpr int kNF = 4;                       // 16-column fragments per wave
-constexpr int kWaveN = 16 * kNF;             // columns per wave
+constexpr int kNJ = 2;                       // 32-column fragments per wave
+constexpr int kWaveN = 32 * kNJ;             // columns per wave
 constexpr int kBlockN = kGemmWaves * kWaveN; // columns per block
 constexpr int kNS = 3;                       // LDS ring stages
 constexpr int kStA = kBM * kBK * 2;          // stage bytes: A tile
@@ -295,7 +295,6 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
     const uint8_t* base = sh ? a.shared : a.slots + (int64_t)slot * a.slot_stride;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int q = lane >> 4;
 
     // ---- A: wave wv fills 1 KB chunks [wv * NA, wv * NA + NA) of a stage's A tile; lane l of
     // chunk ii lands in 16-byte slot ii * 64 + l = (row, physical slot p) and carries the
@@ -391,17 +390,23 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
                                                          vsc, bo + g * 2, 0, 0);
         }
     };
-    // block row of fragment nj for this lane
-    int brow[kNF];
+    // Fragments are 32 x 32 (v_mfma_f32_32x32x16_bf16): MR row blocks of 32 by kNJ column
+    // blocks of 32 per wave. Lane l works on row / column l % 32 of a fragment and on K half
+    // kh = l / 32: MFMA kk (0..3) of a stage takes the 8 K of chunk 4 kh + kk (8 K per chunk),
+    // so a lane's B operands for the whole stage are the 4 consecutive words of the 16-byte
+    // half kh of its weight row's stage segment -- one LDS read -- and its A operand for kk is
+    // the 16-byte chunk 4 kh + kk of the activation row. Each output is still the sum over
+    // all K of the stage.
+    constexpr int MR = MF / 2;
+    const int kh = lane >> 5, l32 = lane & 31;
+    int brow[kNJ];
 #pragma unroll
-    for (int nj = 0; nj < kNF; ++nj)
-        brow[nj] = KIND == 0 ? (nj >> 1) * 128 + wv * 32 + (nj & 1) * 16 + (lane & 15)
-                             : wv * 64 + nj * 16 + (lane & 15);
-    // the lane's B words (both kc) and scales of stage s, read from LDS once per stage
-    // (8-byte reads: conflict-free with the half swap above)
+    for (int nj = 0; nj < kNJ; ++nj)
+        brow[nj] = KIND == 0 ? nj * 128 + wv * 32 + l32 : wv * 64 + nj * 32 + l32;
+    // the lane's B words (all four kk) and scales of stage s, read from LDS once per stage
     struct Frag {
-        u32x2_t w[kNF];
-        uint32_t s[kNF], b[kNF];
+        u32x4_t w[kNJ];
+        uint32_t s[kNJ], b[kNJ];
     };
     auto fetch = [&](Frag& f, int s) __attribute__((always_inline)) {
         const uint8_t* st = ring + (s % NS) * SS;
@@ -410,55 +415,57 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
         const uint8_t* ss = hi ? ring + ((s - 1) % NS) * SS : st;
         const int sh = hi ? 16 : 0;
 #pragma unroll
-        for (int nj = 0; nj < kNF; ++nj) {
+        for (int nj = 0; nj < kNJ; ++nj) {
             const int br = brow[nj];
-            const int h = (q >> 1) ^ ((br >> 3) & 1);
-            f.w[nj] = *reinterpret_cast<const u32x2_t*>(st + SA + (2 * br + h) * 16 + (q & 1) * 8);
+            const int h = kh ^ ((br >> 3) & 1);
+            f.w[nj] = *reinterpret_cast<const u32x4_t*>(st + SA + (2 * br + h) * 16);
             f.s[nj] = (*reinterpret_cast<const uint32_t*>(ss + SA + kStB + br * 4) >> sh) & 0xFFFFu;
             if constexpr (MODE == BRX_QUANT_AFFINE)
                 f.b[nj] = (*reinterpret_cast<const uint32_t*>(ss + SA + kStB + 1024 + br * 4) >> sh) & 0xFFFFu;
         }
     };
-    // word kc of the lane's K chunks, dequantized into MFMA operands
-    auto deq = [&](bf16x8_t (&bop)[kNF], const Frag& f, int kc) __attribute__((always_inline)) {
+    // word kk of the lane's stage half, dequantized into MFMA operands
+    auto deq = [&](bf16x8_t (&bop)[kNJ], const Frag& f, int kk) __attribute__((always_inline)) {
 #pragma unroll
-        for (int nj = 0; nj < kNF; ++nj) {
+        for (int nj = 0; nj < kNJ; ++nj) {
             float sv = 0.f, bv = 0.f, sc = 0.f;
             if constexpr (MODE == BRX_QUANT_AFFINE) {
                 sv = F16 ? h2f(f.s[nj]) : bf2f(f.s[nj]);
                 bv = F16 ? h2f(f.b[nj]) : bf2f(f.b[nj]);
             } else {
-                // the lane's K chunk 2q + kc lies in group 2g + (q >> 1) of the stage
-                sc = e8m0_f32((f.s[nj] >> (8 * (q >> 1))) & 0xFFu);
+                // chunk 4 kh + kk lies in the stage's 32-wide group kh
+                sc = e8m0_f32((f.s[nj] >> (8 * kh)) & 0xFFu);
             }
-            bop[nj] = dq8<MODE>(kc ? f.w[nj].y : f.w[nj].x, sv, bv, sc);
+            bop[nj] = dq8<MODE>(f.w[nj][kk], sv, bv, sc);
         }
     };
 
-    f32x4_t acc[MF][kNF];
+    f32x16_t acc[MR][kNJ];
 #pragma unroll
-    for (int i = 0; i < MF; ++i)
+    for (int i = 0; i < MR; ++i)
 #pragma unroll
-        for (int j = 0; j < kNF; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < kNJ; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-    auto mma = [&](int s, const bf16x8_t (&bop)[kNF], int kc) __attribute__((always_inline)) {
+    auto mma = [&](int s, const bf16x8_t (&bop)[kNJ], int kk) __attribute__((always_inline)) {
         const uint16_t* As = reinterpret_cast<const uint16_t*>(ring + (s % NS) * SS);
 #pragma unroll
-        for (int mi = 0; mi < MF; ++mi) {
-            const int m = mi * 16 + (lane & 15);
-            const int c = (2 * q + kc) ^ a_key(m);
+        for (int mi = 0; mi < MR; ++mi) {
+            const int m = mi * 32 + l32;
+            const int c = (4 * kh + kk) ^ a_key(m);
             const bf16x8_t af = *reinterpret_cast<const bf16x8_t*>(As + m * 64 + c * 8);
 #pragma unroll
-            for (int nj = 0; nj < kNF; ++nj)
-                acc[mi][nj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bop[nj], acc[mi][nj], 0, 0, 0);
+            for (int nj = 0; nj < kNJ; ++nj)
+                acc[mi][nj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, bop[nj], acc[mi][nj], 0, 0, 0);
         }
     };
 
-    // prologue: stages 0 .. NS - 2 in flight; wait for stages 0 and 1; B(0) kc 0 dequantized
+    // prologue: stages 0 .. NS - 2 in flight; wait for stages 0 and 1; B(0) kk 0 dequantized
 #pragma unroll
     for (int s = 0; s < NS - 1; ++s) issue(s);
     dma_wait_barrier<loads_after(NS, NV0, NV1, 0)>();
-    bf16x8_t bop0[kNF], bop1[kNF];
+    bf16x8_t bop0[kNJ], bop1[kNJ];
     Frag fc, fn;
     fetch(fc, 0);
     deq(bop0, fc, 0);
@@ -469,10 +476,14 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
         else
             dma_wait_barrier<loads_after(NS, NV0, NV1, 0)>();
         issue(s + NS - 1);
+        fetch(fn, s + 1);
         mma(s, bop0, 0);
         deq(bop1, fc, 1);
-        fetch(fn, s + 1);
         mma(s, bop1, 1);
+        deq(bop0, fc, 2);
+        mma(s, bop0, 2);
+        deq(bop1, fc, 3);
+        mma(s, bop1, 3);
         deq(bop0, fn, 0);
         fc = fn;
     }
@@ -485,10 +496,10 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
     if constexpr (KIND == 0) {
         constexpr int TS = kBlockN / 2 + 8;                // LDS row stride (elements)
         constexpr int CH = kBlockN / 2 / 8;                // 16-byte chunks per row
-        // fragments nj < kNF / 2 are gate, nj + kNF / 2 the up rows of the same features
-#pragma unroll
-        for (int nj = 0; nj < kNF / 2; ++nj) {
-            const int fl = wv * (kWaveN / 2) + nj * 16 + (lane & 15);
+        // fragment 0 holds gate, fragment 1 the up rows of the same 32 features; element i of
+        // a 32 x 32 fragment is row 8 (i / 4) + 4 kh + i % 4, column l32
+        {
+            const int fl = wv * (kWaveN / 2) + l32;
             const int f = min(nt * (kBlockN / 2) + fl, inter - 1);
             float bg = 0.f, bu = 0.f;
             if (L.p[0].bias >= 0) {
@@ -496,12 +507,11 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
                 bu = bf2f(reinterpret_cast<const uint16_t*>(base + L.p[1].bias)[f]);
             }
 #pragma unroll
-            for (int mi = 0; mi < MF; ++mi) {
+            for (int mi = 0; mi < MR; ++mi) {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const float h = act_apply(a.act, acc[mi][nj][i] + bg, acc[mi][nj + kNF / 2][i] + bu,
-                                              a.alpha, a.limit);
-                    T[(mi * 16 + q * 4 + i) * TS + fl] = __builtin_bit_cast(uint16_t, (__bf16)h);
+                for (int i = 0; i < 16; ++i) {
+                    const float h = act_apply(a.act, acc[mi][0][i] + bg, acc[mi][1][i] + bu, a.alpha, a.limit);
+                    T[(mi * 32 + 8 * (i >> 2) + 4 * kh + (i & 3)) * TS + fl] = __builtin_bit_cast(uint16_t, (__bf16)h);
                 }
             }
         }
@@ -516,16 +526,17 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
         constexpr int TS = kBlockN + 8;
         constexpr int CH = kBlockN / 8;
 #pragma unroll
-        for (int nj = 0; nj < kNF; ++nj) {
-            const int nl = wv * kWaveN + nj * 16 + (lane & 15);
+        for (int nj = 0; nj < kNJ; ++nj) {
+            const int nl = wv * kWaveN + nj * 32 + l32;
             float bd = 0.f;
             if (L.p[2].bias >= 0)
                 bd = bf2f(reinterpret_cast<const uint16_t*>(base + L.p[2].bias)[min(nt * kBlockN + nl, H - 1)]);
 #pragma unroll
-            for (int mi = 0; mi < MF; ++mi) {
+            for (int mi = 0; mi < MR; ++mi) {
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    T[(mi * 16 + q * 4 + i) * TS + nl] = __builtin_bit_cast(uint16_t, (__bf16)(acc[mi][nj][i] + bd));
+                for (int i = 0; i < 16; ++i)
+                    T[(mi * 32 + 8 * (i >> 2) + 4 * kh + (i & 3)) * TS + nl] =
+                        __builtin_bit_cast(uint16_t, (__bf16)(acc[mi][nj][i] + bd));
             }
         }
         lds_barrier();
