@@ -12,9 +12,10 @@
 //              holds every tile of more than 64 rows before the smaller ones, so the GEMM grids
 //              dispatch the long tiles first and the short ones fill the end.
 //   k_pf_gemm  grouped GEMM, tile = (M tile of one expert's pairs, 256 columns), one wave
-//              per SIMD, v_mfma_f32_32x32x16_bf16.  KIND 0 (gate/up): A rows are the pairs' token activations gathered
-//              from x, B rows the gate and up weights of 128 intermediate features; the
-//              epilogue applies act() and stores h (bf16) in bucketed order.  KIND 1 (down):
+//              per SIMD, v_mfma_f32_32x32x16_bf16.  KIND 0 (gate/up): A rows are the pairs'
+//              token activations gathered from x, B rows the gate and up weights of 128
+//              intermediate features; the epilogue applies act() and stores h (bf16) in
+//              bucketed order.  KIND 1 (down):
 //              A = h rows, B = down weights of 256 output columns; the epilogue stores each
 //              pair's bf16 row at its (token, k) position.  A is staged through LDS, B is
 //              dequantized from 4-bit straight into MFMA operand registers; fp32 accumulators
