@@ -187,30 +187,31 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 // of its weight row's 32-byte stage segment, and its A operand the matching 16-byte chunk of
 // the activation row.  Each output is still the sum over all K.
 //
-// Everything a stage needs is copied global -> LDS by the buffer unit (buffer_load ... lds,
-// no registers): the A tile (128 rows x 64 bf16, 16-byte chunks XOR-swizzled by row so the
-// rows an MFMA operand read touches fall in distinct bank groups), the block's 256 weight rows
-// x 32 bytes (the two 16-byte halves of rows 8..15 of every 16 swapped) and each row's scale
-// (and bias) in a 32-bit slot, two stages' values per slot when the scale rows are 4-byte
-// aligned.  A ring of NS stages keeps NS - 2 stages in flight while the MFMAs consume one;
-// per stage s:
-//   wait until stage s + 1 has landed (s_waitcnt vmcnt(N), N = the later stages' copies);
+// Per stage, the A tile (128 rows x 64 bf16) and the rows' scales are copied global -> LDS by
+// the buffer unit (buffer_load ... lds, no registers): A's 16-byte chunks XOR-swizzled by row
+// so the rows an MFMA operand read touches fall in distinct bank groups, each weight row's
+// scale (and bias) in a 32-bit slot, two stages' values per slot when the scale rows are
+// 4-byte aligned. The weights are not shared between waves, so each lane loads its own B
+// words straight into registers (one 16-byte load per fragment and stage); keeping them out
+// of LDS leaves room for a ring of NS = 4 stages, two of them in flight while the MFMAs consume
+// one (under a full load HBM answers in ~4 us, so the bytes in flight per CU bound the rate).
+// Per stage s:
+//   wait until stage s + 1 has landed (s_waitcnt vmcnt(N), N = the later stages' loads);
 //   barrier (so every wave's copies are visible and stage s - 1's slot is free);
-//   issue the copies of stage s + NS - 1; read B(s + 1) and its scales from LDS;
+//   issue the loads of stage s + NS - 1; read the scales of stage s + 1 from LDS;
 //   MFMA kk of stage s  | dequantize B(s) kk + 1 (kk = 3: B(s + 1) kk 0)
-// Copies past the last stage repeat it.  The waits are explicit (inline asm with a memory
-// clobber, so the compiler moves no LDS access across them); the MFMA-interleaved VALU code
-// is plain C++ so that the compiler's MFMA hazard checks cover it.
+// Loads past the last stage repeat it. The MFMA-interleaved VALU code is plain C++ so that
+// the compiler's MFMA hazard checks cover it.
 constexpr int kGemmWaves = 4;
 constexpr int kGemmThreads = 64 * kGemmWaves;
 constexpr int kNJ = 2;                       // 32-column fragments per wave
 constexpr int kWaveN = 32 * kNJ;             // columns per wave
 constexpr int kBlockN = kGemmWaves * kWaveN; // columns per block
-constexpr int kNS = 3;                       // LDS ring stages
+constexpr int kNS = 4;                       // LDS ring stages (even: see pf_tile)
 constexpr int kStA = kBM * kBK * 2;          // stage bytes: A tile
-constexpr int kStB = kBlockN * kBK / 2;      // B rows, 4-bit
 constexpr int kStS = kBlockN * 4 * 2;        // scale and bias per row, one 32-bit LDS slot each
-constexpr int kStage = kStA + kStB + kStS;
+constexpr int kStage = kStA + kStS;
+static_assert(kNS % 2 == 0, "the paired scale copies follow stage parity through the unrolled ring");
 
 typedef __attribute__((address_space(3))) void* LDS_PTR;
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
@@ -225,10 +226,15 @@ __device__ __forceinline__ void lds_barrier() {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-// waits until at most N of this wave's copies into LDS are in flight, then for every wave
+// waits until at most N of this wave's memory loads (copies into LDS and loads into registers)
+// are in flight, then for every wave. The wait is the builtin, so the compiler's own wait
+// placement knows which loads it covers and adds none for the registers it has made ready;
+// the barrier is inline asm with a memory clobber, so no LDS access moves across it.
 template <int N>
 __device__ __forceinline__ void dma_wait_barrier() {
-    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
+    asm volatile("s_barrier" ::: "memory");
 }
 
 // Copies into LDS a wave has issued after stage s + 1's when it waits for stage s + 1 at
@@ -277,16 +283,14 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
                                         uint16_t* __restrict__ y_routed, uint16_t* __restrict__ y_shared,
                                         uint8_t* ring, int32_t* dst_s, int e, int m0, int rows, int slot,
                                         int nt) {
-    constexpr int NA = MF * 16 * 8 / 64 / kGemmWaves;   // A wave-instructions per wave per stage
-    // loads per wave of an odd stage (A, B) and of an even stage (A, B and the scale pair of it
-    // and the next stage)
-    constexpr int NV1 = NA + 2;
-    constexpr int NV0 = NV1 + (MODE == BRX_QUANT_AFFINE ? 2 : 1);
-    // stage layout for this tile height: a shorter A tile leaves room in the same ring for
-    // more stages in flight (3 at 128 rows, 4 at 64, 5 at 32)
+    constexpr int NA = MF * 16 * 8 / 64 / kGemmWaves;   // A copies per wave per stage
+    constexpr int NS = kNS;                             // stages in the ring
     constexpr int SA = MF * 16 * kBK * 2;               // A bytes per stage
-    constexpr int SS = SA + kStB + kStS;                // stage bytes
-    constexpr int NS = (kNS * kStage) / SS;             // stages in the ring
+    constexpr int SS = SA + kStS;                       // stage bytes in the ring
+    // loads per wave of an odd stage (A copies, B loads) and of an even stage (+ the scale copies
+    // of it and the next stage)
+    constexpr int NV1 = NA + kNJ;
+    constexpr int NV0 = NV1 + (MODE == BRX_QUANT_AFFINE ? 2 : 1);
     const bool sh = e >= a.E;
     const int inter = sh ? a.I_sh : a.I;
     const int H = a.H;
@@ -296,6 +300,7 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
     const uint8_t* base = sh ? a.shared : a.slots + (int64_t)slot * a.slot_stride;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int kh = lane >> 5, l32 = lane & 31;
 
     // ---- A: wave wv fills 1 KB chunks [wv * NA, wv * NA + NA) of a stage's A tile; lane l of
     // chunk ii lands in 16-byte slot ii * 64 + l = (row, physical slot p) and carries the
@@ -318,23 +323,29 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
     }
     // ---- B: the block's 256 weight rows (KIND 0: gate rows of features nt * 128 + [0, 128),
     // then the up rows of the same features; KIND 1: down rows nt * 256 + [0, 256)), 32 bytes
-    // of each per stage; wave wv fills 1 KB chunks 2 wv, 2 wv + 1 (64 rows), and the rows'
-    // scales (one 16-bit value per row and stage: affine scale and bias; MXFP4 the e8m0 bytes
-    // of the stage's two groups)
+    // of each per stage. A lane loads its own operands straight into registers: the 16-byte
+    // half kh of the stage segment of row brow[nj] (fragment nj, column l32), so one load
+    // instruction reads 32 rows x 32 contiguous bytes. Rows past the matrix repeat its last row.
     const __amdgpu_buffer_rsrc_t rb_rsrc = make_rsrc(base, (uint32_t)L.bytes);
-    const int p_w = KIND == 0 ? (wv >= 2 ? 1 : 0) : 2;  // matrix of this wave's 64 rows
     auto mat_row = [&](int br) __attribute__((always_inline)) {
         return KIND == 0 ? min(nt * 128 + (br & 127), inter - 1) : min(nt * 256 + br, H - 1);
     };
-    uint32_t vb[2];
+    int brow[kNJ];
+    uint32_t vbw[kNJ];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int sl = (wv * 2 + i) * 64 + lane;           // 16-byte slot of the stage's B
-        const int br = sl >> 1;
-        const int h = (sl & 1) ^ ((br >> 3) & 1);
-        vb[i] = (uint32_t)mat_row(br) * (uint32_t)(K / 2) + h * 16;
+    for (int nj = 0; nj < kNJ; ++nj) {
+        brow[nj] = KIND == 0 ? nj * 128 + wv * 32 + l32 : wv * 64 + nj * 32 + l32;
+        const int pj = KIND == 0 ? nj : 2;
+        vbw[nj] = (uint32_t)L.p[pj].w + (uint32_t)mat_row(brow[nj]) * (uint32_t)(K / 2) + kh * 16;
     }
-    const int wo = (int)L.p[p_w].w, so = (int)L.p[p_w].s, bo = (int)L.p[p_w].b;
+    // ---- scales: wave wv copies those of rows 64 wv + lane (one 16-bit value per row and
+    // stage: affine scale and bias; MXFP4 the e8m0 bytes of the stage's two groups) into a
+    // 32-bit LDS slot per row
+    const int p_w = KIND == 0 ? (wv >= 2 ? 1 : 0) : 2;  // matrix of the rows this wave copies
+    const int so = (int)L.p[p_w].s, bo = (int)L.p[p_w].b;
+    const uint32_t vsc = MODE == BRX_QUANT_AFFINE
+        ? (uint32_t)mat_row(wv * 64 + lane) * (uint32_t)(K / 64) * 2
+        : (uint32_t)mat_row(wv * 64 + lane) * (uint32_t)(K / 32);
     // the scales of two stages are one 4-byte copy when every scale row and array of the
     // block's matrices is 4-byte aligned (affine: K / 64 even; MXFP4: K a multiple of 128);
     // otherwise each stage copies its own 2 bytes (the waits below assume the paired count,
@@ -345,9 +356,6 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
     for (int pj = 0; pj < 3; ++pj)
         if (KIND == 0 ? pj < 2 : pj == 2)
             spair = spair && ((L.p[pj].s & 3) == 0) && (MODE != BRX_QUANT_AFFINE || (L.p[pj].b & 3) == 0);
-    const uint32_t vsc = MODE == BRX_QUANT_AFFINE
-        ? (uint32_t)mat_row(wv * 64 + lane) * (uint32_t)(K / 64) * 2
-        : (uint32_t)mat_row(wv * 64 + lane) * (uint32_t)(K / 32);
     if constexpr (KIND == 1) {
         if (tid < kBM) {
             int d = -1;
@@ -359,74 +367,69 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
         }
     }
 
-    auto issue = [&](int s) __attribute__((always_inline)) {
+    // the lane's B words of one stage (fragment nj: words kk = 0..3 of its 16-byte half)
+    struct BReg {
+        u32x4_t w[kNJ];
+    };
+    // issue every load of stage s: A and scale copies into ring slot s % NS, B into `br`
+    auto issue = [&](int s, BReg& br) __attribute__((always_inline)) {
         const int g = min(s, nsteps - 1);
         uint8_t* st = ring + (s % NS) * SS;
 #pragma unroll
         for (int i = 0; i < NA; ++i)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(ra_rsrc, (LDS_PTR)(st + (wv * NA + i) * 1024), 16,
                                                      va[i], g * 128, 0, 0);
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rb_rsrc, (LDS_PTR)(st + SA + (wv * 2 + i) * 1024), 16,
-                                                     vb[i], wo + g * 32, 0, 0);
-        // scales: one 32-bit LDS slot per row. Paired: an even stage's slot holds its 16-bit
-        // scale (and bias) value in the low half and the next stage's in the high half; an odd
-        // stage copies nothing. Unpaired: every stage copies its own 16 bits (a 16-bit copy to
-        // LDS fills a 32-bit slot, zero-extended).
+        // scales: paired, an even stage's slot holds its 16-bit scale (and bias) value in the
+        // low half and the next stage's in the high half and an odd stage copies nothing;
+        // unpaired, every stage copies its own 16 bits (a 16-bit copy to LDS fills a 32-bit
+        // slot, zero-extended)
         if (spair) {
             if ((s & 1) == 0) {
                 const int gp = g & ~1;
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rb_rsrc, (LDS_PTR)(st + SA + kStB + wv * 256), 4, vsc,
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rb_rsrc, (LDS_PTR)(st + SA + wv * 256), 4, vsc,
                                                          so + gp * 2, 0, 0);
                 if constexpr (MODE == BRX_QUANT_AFFINE)
-                    __builtin_amdgcn_raw_ptr_buffer_load_lds(rb_rsrc, (LDS_PTR)(st + SA + kStB + 1024 + wv * 256),
-                                                             4, vsc, bo + gp * 2, 0, 0);
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(rb_rsrc, (LDS_PTR)(st + SA + 1024 + wv * 256), 4,
+                                                             vsc, bo + gp * 2, 0, 0);
             }
         } else {
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rb_rsrc, (LDS_PTR)(st + SA + kStB + wv * 256), 2, vsc,
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rb_rsrc, (LDS_PTR)(st + SA + wv * 256), 2, vsc,
                                                      so + g * 2, 0, 0);
             if constexpr (MODE == BRX_QUANT_AFFINE)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rb_rsrc, (LDS_PTR)(st + SA + kStB + 1024 + wv * 256), 2,
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rb_rsrc, (LDS_PTR)(st + SA + 1024 + wv * 256), 2,
                                                          vsc, bo + g * 2, 0, 0);
         }
+#pragma unroll
+        for (int nj = 0; nj < kNJ; ++nj)
+            br.w[nj] = __builtin_amdgcn_raw_buffer_load_b128(rb_rsrc, vbw[nj], g * 32, 0);
     };
     // Fragments are 32 x 32 (v_mfma_f32_32x32x16_bf16): MR row blocks of 32 by kNJ column
     // blocks of 32 per wave. Lane l works on row / column l % 32 of a fragment and on K half
     // kh = l / 32: MFMA kk (0..3) of a stage takes the 8 K of chunk 4 kh + kk (8 K per chunk),
     // so a lane's B operands for the whole stage are the 4 consecutive words of the 16-byte
-    // half kh of its weight row's stage segment -- one LDS read -- and its A operand for kk is
-    // the 16-byte chunk 4 kh + kk of the activation row. Each output is still the sum over
-    // all K of the stage.
+    // half kh of its weight row's stage segment, and its A operand for kk is the 16-byte
+    // chunk 4 kh + kk of the activation row. Each output is still the sum over all K of the
+    // stage.
     constexpr int MR = MF / 2;
-    const int kh = lane >> 5, l32 = lane & 31;
-    int brow[kNJ];
-#pragma unroll
-    for (int nj = 0; nj < kNJ; ++nj)
-        brow[nj] = KIND == 0 ? nj * 128 + wv * 32 + l32 : wv * 64 + nj * 32 + l32;
-    // the lane's B words (all four kk) and scales of stage s, read from LDS once per stage
-    struct Frag {
-        u32x4_t w[kNJ];
+    // the lane's scales of stage s, read from the ring
+    struct SReg {
         uint32_t s[kNJ], b[kNJ];
     };
-    auto fetch = [&](Frag& f, int s) __attribute__((always_inline)) {
-        const uint8_t* st = ring + (s % NS) * SS;
+    auto fetch_s = [&](SReg& f, int s) __attribute__((always_inline)) {
         // paired scales of an odd stage: the high halves of the previous (even) stage's slots
         const bool hi = spair && (s & 1);
-        const uint8_t* ss = hi ? ring + ((s - 1) % NS) * SS : st;
+        const uint8_t* ss = ring + ((hi ? s - 1 : s) % NS) * SS;
         const int sh = hi ? 16 : 0;
 #pragma unroll
         for (int nj = 0; nj < kNJ; ++nj) {
             const int br = brow[nj];
-            const int h = kh ^ ((br >> 3) & 1);
-            f.w[nj] = *reinterpret_cast<const u32x4_t*>(st + SA + (2 * br + h) * 16);
-            f.s[nj] = (*reinterpret_cast<const uint32_t*>(ss + SA + kStB + br * 4) >> sh) & 0xFFFFu;
+            f.s[nj] = (*reinterpret_cast<const uint32_t*>(ss + SA + br * 4) >> sh) & 0xFFFFu;
             if constexpr (MODE == BRX_QUANT_AFFINE)
-                f.b[nj] = (*reinterpret_cast<const uint32_t*>(ss + SA + kStB + 1024 + br * 4) >> sh) & 0xFFFFu;
+                f.b[nj] = (*reinterpret_cast<const uint32_t*>(ss + SA + 1024 + br * 4) >> sh) & 0xFFFFu;
         }
     };
     // word kk of the lane's stage half, dequantized into MFMA operands
-    auto deq = [&](bf16x8_t (&bop)[kNJ], const Frag& f, int kk) __attribute__((always_inline)) {
+    auto deq = [&](bf16x8_t (&bop)[kNJ], const BReg& bw, const SReg& f, int kk) __attribute__((always_inline)) {
 #pragma unroll
         for (int nj = 0; nj < kNJ; ++nj) {
             float sv = 0.f, bv = 0.f, sc = 0.f;
@@ -437,7 +440,7 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
                 // chunk 4 kh + kk lies in the stage's 32-wide group kh
                 sc = e8m0_f32((f.s[nj] >> (8 * kh)) & 0xFFu);
             }
-            bop[nj] = dq8<MODE>(f.w[nj][kk], sv, bv, sc);
+            bop[nj] = dq8<MODE>(bw.w[nj][kk], sv, bv, sc);
         }
     };
 
@@ -462,31 +465,40 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
         }
     };
 
-    // prologue: stages 0 .. NS - 2 in flight; wait for stages 0 and 1; B(0) kk 0 dequantized
+    // prologue: stages 0 .. NS - 2 in flight; wait for stages 0 and 1; B(0) kk 0 dequantized.
+    // The B registers rotate through NS sets: stage t's words sit in set t % NS, so the loop
+    // is unrolled NS times to keep every set index a constant.
+    BReg bq[NS];
 #pragma unroll
-    for (int s = 0; s < NS - 1; ++s) issue(s);
+    for (int t = 0; t < NS - 1; ++t) issue(t, bq[t]);
     dma_wait_barrier<loads_after(NS, NV0, NV1, 0)>();
     bf16x8_t bop0[kNJ], bop1[kNJ];
-    Frag fc, fn;
-    fetch(fc, 0);
-    deq(bop0, fc, 0);
-    for (int s = 0; s < nsteps; ++s) {
-        // stage s + 1 landed in every wave; stage s - 1's slot is free for stage s + NS - 1
-        if (s & 1)
-            dma_wait_barrier<loads_after(NS, NV0, NV1, 1)>();
-        else
-            dma_wait_barrier<loads_after(NS, NV0, NV1, 0)>();
-        issue(s + NS - 1);
-        fetch(fn, s + 1);
-        mma(s, bop0, 0);
-        deq(bop1, fc, 1);
-        mma(s, bop1, 1);
-        deq(bop0, fc, 2);
-        mma(s, bop0, 2);
-        deq(bop1, fc, 3);
-        mma(s, bop1, 3);
-        deq(bop0, fn, 0);
-        fc = fn;
+    SReg sc, sn;
+    fetch_s(sc, 0);
+    deq(bop0, bq[0], sc, 0);
+    for (int s0 = 0; s0 < nsteps; s0 += NS) {
+#pragma unroll
+        for (int u = 0; u < NS; ++u) {
+            const int s = s0 + u;
+            if (s >= nsteps) break;
+            // stage s + 1 landed in every wave; stage s - 1's slot and registers are free for
+            // stage s + NS - 1 (NS is even, so s and u have the same parity)
+            if (u & 1)
+                dma_wait_barrier<loads_after(NS, NV0, NV1, 1)>();
+            else
+                dma_wait_barrier<loads_after(NS, NV0, NV1, 0)>();
+            issue(s + NS - 1, bq[(u + NS - 1) % NS]);
+            fetch_s(sn, s + 1);
+            mma(s, bop0, 0);
+            deq(bop1, bq[u], sc, 1);
+            mma(s, bop1, 1);
+            deq(bop0, bq[u], sc, 2);
+            mma(s, bop0, 2);
+            deq(bop1, bq[u], sc, 3);
+            mma(s, bop1, 3);
+            deq(bop0, bq[(u + 1) % NS], sn, 0);
+            sc = sn;
+        }
     }
 
     // ---- epilogue: the output tile goes through LDS (the ring, once every copy into it has
