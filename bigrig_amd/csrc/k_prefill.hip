@@ -198,10 +198,11 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 // Per stage s:
 //   wait until stage s + 1 has landed (s_waitcnt vmcnt(N), N = the later stages' loads);
 //   barrier (so every wave's copies are visible and stage s - 1's slot is free);
-//   issue the loads of stage s + NS - 1; read the scales of stage s + 1 from LDS;
+//   issue the loads of stage s + NS - 1 (none past the last stage); read the scales of stage
+//   s + 1 from LDS;
 //   MFMA kk of stage s  | dequantize B(s) kk + 1 (kk = 3: B(s + 1) kk 0)
-// Loads past the last stage repeat it. The MFMA-interleaved VALU code is plain C++ so that
-// the compiler's MFMA hazard checks cover it.
+// The MFMA-interleaved VALU code is plain C++ so that the compiler's MFMA hazard checks cover
+// it.
 constexpr int kGemmWaves = 4;
 constexpr int kGemmThreads = 64 * kGemmWaves;
 constexpr int kNJ = 2;                       // 32-column fragments per wave
@@ -482,12 +483,19 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
             const int s = s0 + u;
             if (s >= nsteps) break;
             // stage s + 1 landed in every wave; stage s - 1's slot and registers are free for
-            // stage s + NS - 1 (NS is even, so s and u have the same parity)
-            if (u & 1)
-                dma_wait_barrier<loads_after(NS, NV0, NV1, 1)>();
-            else
-                dma_wait_barrier<loads_after(NS, NV0, NV1, 0)>();
-            issue(s + NS - 1, bq[(u + NS - 1) % NS]);
+            // stage s + NS - 1 (NS is even, so s and u have the same parity). No stage past the
+            // last is loaded: near the end fewer loads follow stage s + 1's, so the wait counts
+            // only those issued (all of stage s + NS - 2's once it exists, else none).
+            static_assert(NS == 4, "the tail waits below count the loads of one later stage");
+            if (s + NS - 2 < nsteps) {
+                if (u & 1)
+                    dma_wait_barrier<loads_after(NS, NV0, NV1, 1)>();
+                else
+                    dma_wait_barrier<loads_after(NS, NV0, NV1, 0)>();
+            } else {
+                dma_wait_barrier<0>();
+            }
+            if (s + NS - 1 < nsteps) issue(s + NS - 1, bq[(u + NS - 1) % NS]);
             fetch_s(sn, s + 1);
             mma(s, bop0, 0);
             deq(bop1, bq[u], sc, 1);
