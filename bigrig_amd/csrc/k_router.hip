@@ -25,18 +25,21 @@ __device__ __forceinline__ float wave_sum_xor(float v) {
 
 // ---------------------------------------------------------------- many tokens
 // k_router_tiled: a block takes a tile of TT tokens (staged in LDS as bf16) and a group of
-// rows; each row's weights are loaded once per block and used for all TT tokens. Per token the
-// lane partials follow the same fmaf chain as k_router_logits; the TT partials are reduced by a
-// transposed butterfly that forms exactly the sums of the xor butterfly (strides 32, 16, ...,
-// 1; fp32 addition is commutative, so a[i] + a[i^s] is the same value on both lanes): at
-// stride 32 a lane keeps half of the tokens and sends the other half, at 16 a quarter, and so
-// on, so 16 tokens take 17 exchanges instead of 96. Token tau ends on lanes 4 tau .. 4 tau + 3.
+// rows; each row's weights are loaded once per block and used for all TT tokens, and a wave
+// works on two rows at once so each token's activations are converted once for both. Per
+// token the lane partials follow the same fmaf chain as k_router_logits; the TT partials are
+// reduced by a transposed butterfly that forms exactly the sums of the xor butterfly
+// (strides 32, 16, ..., 1; fp32 addition is commutative, so a[i] + a[i^s] is the same value on
+// both lanes): at stride 32 a lane keeps half of the tokens and sends the other half, at 16 a
+// quarter, and so on, so 16 tokens take 17 exchanges instead of 96. Token tau ends on lanes
+// 4 tau .. 4 tau + 3.
 template <bool WF32, int TT>
 __global__ __launch_bounds__(kRouterThreads) void k_router_tiled(
     const uint16_t* __restrict__ x, const void* __restrict__ w, const float* __restrict__ bias,
     const uint16_t* __restrict__ sgw, int T, int H, int E, int rows_per_block, float* __restrict__ logits) {
     static_assert(TT == 16, "the exchange pattern below is written for 16 tokens");
     constexpr int kNJ = 6;                      // chunks per lane: H <= 64 * 8 * 6 = 3072
+    constexpr int RW = 2;                       // rows a wave works on at once (sharing x)
     extern __shared__ uint4 xs4[];              // [TT][H / 8] chunks of 8 bf16
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int t0 = blockIdx.x * TT;
@@ -50,82 +53,105 @@ __global__ __launch_bounds__(kRouterThreads) void k_router_tiled(
     __syncthreads();
     const int rows = E + (sgw ? 1 : 0);
     const int r_end = min(rows, (int)(blockIdx.y + 1) * rows_per_block);
-    for (int r = blockIdx.y * rows_per_block + wv; r < r_end; r += kRouterThreads / kWave) {
-        const bool wf32 = WF32 && r < E;
-        uint4 wv4[kNJ][2];
+    constexpr int kWaves = kRouterThreads / kWave;
+    for (int r0 = blockIdx.y * rows_per_block + wv * RW; r0 < r_end; r0 += kWaves * RW) {
+        // the wave's rows r0, r0 + 1 (a row past the block's range repeats the last one and is
+        // not stored)
+        uint4 wv4[RW][kNJ][2];
+        bool wf32[RW];
 #pragma unroll
-        for (int j = 0; j < kNJ; ++j) {
-            const int c = min(lane + kWave * j, nch - 1);
-            if (wf32) {
-                const uint4* p = reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(w) + (int64_t)r * H + 8 * c);
-                wv4[j][0] = p[0];
-                wv4[j][1] = p[1];
-            } else {
-                const uint16_t* src = r < E ? reinterpret_cast<const uint16_t*>(w) + (int64_t)r * H : sgw;
-                wv4[j][0] = *reinterpret_cast<const uint4*>(src + 8 * c);
-                wv4[j][1] = make_uint4(0, 0, 0, 0);
+        for (int rr = 0; rr < RW; ++rr) {
+            const int r = min(r0 + rr, r_end - 1);
+            wf32[rr] = WF32 && r < E;
+#pragma unroll
+            for (int j = 0; j < kNJ; ++j) {
+                const int c = min(lane + kWave * j, nch - 1);
+                if (wf32[rr]) {
+                    const uint4* p = reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(w) + (int64_t)r * H + 8 * c);
+                    wv4[rr][j][0] = p[0];
+                    wv4[rr][j][1] = p[1];
+                } else {
+                    const uint16_t* src = r < E ? reinterpret_cast<const uint16_t*>(w) + (int64_t)r * H : sgw;
+                    wv4[rr][j][0] = *reinterpret_cast<const uint4*>(src + 8 * c);
+                    wv4[rr][j][1] = make_uint4(0, 0, 0, 0);
+                }
             }
         }
-        float acc[TT];
+        float acc[RW][TT];
 #pragma unroll
-        for (int t = 0; t < TT; ++t) acc[t] = 0.0f;
+        for (int rr = 0; rr < RW; ++rr)
+#pragma unroll
+            for (int t = 0; t < TT; ++t) acc[rr][t] = 0.0f;
 #pragma unroll
         for (int j = 0; j < kNJ; ++j) {
             const int c = lane + kWave * j;
             if (c >= nch) continue;
-            float wf[8];
-            if (wf32) {
-                wf[0] = __uint_as_float(wv4[j][0].x); wf[1] = __uint_as_float(wv4[j][0].y);
-                wf[2] = __uint_as_float(wv4[j][0].z); wf[3] = __uint_as_float(wv4[j][0].w);
-                wf[4] = __uint_as_float(wv4[j][1].x); wf[5] = __uint_as_float(wv4[j][1].y);
-                wf[6] = __uint_as_float(wv4[j][1].z); wf[7] = __uint_as_float(wv4[j][1].w);
-            } else {
-                const uint32_t ww[4] = {wv4[j][0].x, wv4[j][0].y, wv4[j][0].z, wv4[j][0].w};
+            float wf[RW][8];
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    wf[2 * i] = bf2f(ww[i] & 0xFFFFu);
-                    wf[2 * i + 1] = bf2f(ww[i] >> 16);
+            for (int rr = 0; rr < RW; ++rr) {
+                if (wf32[rr]) {
+                    wf[rr][0] = __uint_as_float(wv4[rr][j][0].x); wf[rr][1] = __uint_as_float(wv4[rr][j][0].y);
+                    wf[rr][2] = __uint_as_float(wv4[rr][j][0].z); wf[rr][3] = __uint_as_float(wv4[rr][j][0].w);
+                    wf[rr][4] = __uint_as_float(wv4[rr][j][1].x); wf[rr][5] = __uint_as_float(wv4[rr][j][1].y);
+                    wf[rr][6] = __uint_as_float(wv4[rr][j][1].z); wf[rr][7] = __uint_as_float(wv4[rr][j][1].w);
+                } else {
+                    const uint32_t ww[4] = {wv4[rr][j][0].x, wv4[rr][j][0].y, wv4[rr][j][0].z, wv4[rr][j][0].w};
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        wf[rr][2 * i] = bf2f(ww[i] & 0xFFFFu);
+                        wf[rr][2 * i + 1] = bf2f(ww[i] >> 16);
+                    }
                 }
             }
+            // one conversion of the token's 8 activations serves every row of the wave
 #pragma unroll
             for (int t = 0; t < TT; ++t) {
                 const uint4 xv = xs4[t * nch + c];
                 const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
+                float xf[8];
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    acc[t] = fmaf(bf2f(xw[i] & 0xFFFFu), wf[2 * i], acc[t]);
-                    acc[t] = fmaf(bf2f(xw[i] >> 16), wf[2 * i + 1], acc[t]);
+                    xf[2 * i] = bf2f(xw[i] & 0xFFFFu);
+                    xf[2 * i + 1] = bf2f(xw[i] >> 16);
                 }
+#pragma unroll
+                for (int rr = 0; rr < RW; ++rr)
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) acc[rr][t] = fmaf(xf[i], wf[rr][i], acc[rr][t]);
             }
         }
-        // transposed butterfly: strides 32, 16, 8, 4 halve the tokens a lane keeps
-        const bool b5 = lane & 32, b4 = lane & 16, b3 = lane & 8, b2 = lane & 4;
-        float v8[8], v4[4], v2[2];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const float mine = b5 ? acc[8 + i] : acc[i], other = b5 ? acc[i] : acc[8 + i];
-            v8[i] = mine + __shfl_xor(other, 32, kWave);
-        }
+        for (int rr = 0; rr < RW; ++rr) {
+            const int r = r0 + rr;
+            // transposed butterfly: strides 32, 16, 8, 4 halve the tokens a lane keeps
+            const bool b5 = lane & 32, b4 = lane & 16, b3 = lane & 8, b2 = lane & 4;
+            float v8[8], v4[4], v2[2];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float mine = b4 ? v8[4 + i] : v8[i], other = b4 ? v8[i] : v8[4 + i];
-            v4[i] = mine + __shfl_xor(other, 16, kWave);
-        }
+            for (int i = 0; i < 8; ++i) {
+                const float mine = b5 ? acc[rr][8 + i] : acc[rr][i], other = b5 ? acc[rr][i] : acc[rr][8 + i];
+                v8[i] = mine + __shfl_xor(other, 32, kWave);
+            }
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const float mine = b3 ? v4[2 + i] : v4[i], other = b3 ? v4[i] : v4[2 + i];
-            v2[i] = mine + __shfl_xor(other, 8, kWave);
+            for (int i = 0; i < 4; ++i) {
+                const float mine = b4 ? v8[4 + i] : v8[i], other = b4 ? v8[i] : v8[4 + i];
+                v4[i] = mine + __shfl_xor(other, 16, kWave);
+            }
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const float mine = b3 ? v4[2 + i] : v4[i], other = b3 ? v4[i] : v4[2 + i];
+                v2[i] = mine + __shfl_xor(other, 8, kWave);
+            }
+            float v1;
+            {
+                const float mine = b2 ? v2[1] : v2[0], other = b2 ? v2[0] : v2[1];
+                v1 = mine + __shfl_xor(other, 4, kWave);
+            }
+            v1 += __shfl_xor(v1, 2, kWave);
+            v1 += __shfl_xor(v1, 1, kWave);
+            const int tau = lane >> 2;
+            if ((lane & 3) == 0 && tau < nt && r < r_end)
+                logits[(int64_t)(t0 + tau) * (E + 1) + r] = (r < E && bias) ? v1 + bias[r] : v1;
         }
-        float v1;
-        {
-            const float mine = b2 ? v2[1] : v2[0], other = b2 ? v2[0] : v2[1];
-            v1 = mine + __shfl_xor(other, 4, kWave);
-        }
-        v1 += __shfl_xor(v1, 2, kWave);
-        v1 += __shfl_xor(v1, 1, kWave);
-        const int tau = lane >> 2;
-        if ((lane & 3) == 0 && tau < nt)
-            logits[(int64_t)(t0 + tau) * (E + 1) + r] = (r < E && bias) ? v1 + bias[r] : v1;
     }
 }
 
