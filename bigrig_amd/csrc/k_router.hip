@@ -39,7 +39,7 @@ __global__ __launch_bounds__(kRouterThreads) void k_router_tiled(
     const uint16_t* __restrict__ sgw, int T, int H, int E, int rows_per_block, float* __restrict__ logits) {
     static_assert(TT == 16, "the exchange pattern below is written for 16 tokens");
     constexpr int kNJ = 6;                      // chunks per lane: H <= 64 * 8 * 6 = 3072
-    constexpr int RW = 2;                       // rows a wave works on at once (sharing x)
+    constexpr int RW = WF32 ? 2 : 4;            // rows a wave works on at once (sharing x)
     extern __shared__ uint4 xs4[];              // [TT][H / 8] chunks of 8 bf16
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int t0 = blockIdx.x * TT;
