@@ -252,23 +252,26 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint3
 }
 
 // Dequantize one 32-bit word (8 weights, natural K order) into a bf16x8 MFMA operand.
-//   affine: w = fmaf(s, q, b) rounded to bf16 (v_cvt_pk_bf16_f32).  The word splits into its
-//     even nibbles (one per byte) and odd nibbles, so each weight converts with one
-//     v_cvt_f32_ubyte{0..3}.  An empty asm statement hides the masked words from the
-//     compiler, which would otherwise fold mask and byte select into one bit-field extract
-//     per nibble; it emits no instruction, so the hazard checks between these VALU ops and
-//     the MFMAs they interleave with stay the compiler's.
+//   affine: w = s q + b with one fp32 rounding, then rounded to bf16 (v_cvt_pk_bf16_f32).
+//     Each nibble q is read as the fp16 subnormal q 2^-24 (the nibble alone in a 16-bit half,
+//     exact when widened to fp32) and v_fma_mix_f32 forms fma(q 2^-24, s 2^24, b): the product
+//     is exactly s q, so the result is the same fl(s q + b) as fmaf(s, q, b). `s24` is s 2^24
+//     (exact for any scale below 2^104). A mask of 0x000F000F takes two nibbles at once, so a
+//     word costs 7 extractions, 8 fma_mix and 4 packs.
 //   MXFP4: the hardware converts two e2m1 codes with the e8m0 scale, exact in bf16.
 template <int MODE>
-__device__ __forceinline__ bf16x8_t dq8(uint32_t w, float s, float b, float sc) {
+__device__ __forceinline__ bf16x8_t dq8(uint32_t w, float s24, float b, float sc) {
     uint32_t o[4];
     if constexpr (MODE == BRX_QUANT_AFFINE) {
-        uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
-        asm("" : "+v"(lo), "+v"(hi));
+        float v[8];
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-            o[j] = pk_bf16(fmaf(s, (float)((lo >> (8 * j)) & 0xFFu), b),
-                           fmaf(s, (float)((hi >> (8 * j)) & 0xFFu), b));
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t t = (w >> (4 * i)) & 0x000F000Fu;     // nibbles i (low half), 4 + i
+            v[i] = __builtin_fmaf((float)__builtin_bit_cast(_Float16, (uint16_t)(t & 0xFFFFu)), s24, b);
+            v[4 + i] = __builtin_fmaf((float)__builtin_bit_cast(_Float16, (uint16_t)(t >> 16)), s24, b);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[j] = pk_bf16(v[2 * j], v[2 * j + 1]);
     } else {
         o[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 0));
         o[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 1));
@@ -435,7 +438,7 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
         for (int nj = 0; nj < kNJ; ++nj) {
             float sv = 0.f, bv = 0.f, sc = 0.f;
             if constexpr (MODE == BRX_QUANT_AFFINE) {
-                sv = F16 ? h2f(f.s[nj]) : bf2f(f.s[nj]);
+                sv = (F16 ? h2f(f.s[nj]) : bf2f(f.s[nj])) * 16777216.0f;   // s 2^24, exact
                 bv = F16 ? h2f(f.b[nj]) : bf2f(f.b[nj]);
             } else {
                 // chunk 4 kh + kk lies in the stage's 32-wide group kh
