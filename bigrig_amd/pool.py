@@ -15,6 +15,7 @@ copy after every forward that may still read the slot, and the next forward afte
 from __future__ import annotations
 
 import inspect
+import os
 import time
 from dataclasses import dataclass
 
@@ -79,6 +80,32 @@ class HostStore:
                     raise ValueError(f"region {li}:{x} is {n} bytes, layer says {per}")
                 rows.append(np.asarray(mm[o:o + n]))
             st.add_layer(li, np.stack(rows))
+        return st
+
+    @classmethod
+    def from_checkpoint(cls, model_dir_or_manifest, layers=None) -> "HostStore":
+        """Read every routed expert of `layers` (default: all) straight out of an MLX
+        checkpoint's safetensors shards into pinned memory, each expert's segments in packing
+        order, so a row holds exactly the bytes a packed blob region would (direct.py:145-240)."""
+        import torch
+
+        from . import checkpoint as CK
+        man = (model_dir_or_manifest if isinstance(model_dir_or_manifest, CK.CheckpointManifest)
+               else CK.expert_manifest(model_dir_or_manifest))
+        st = cls()
+        fds = {}
+        try:
+            for li in sorted(int(x) for x in man.layers) if layers is None else layers:
+                ent = man.layers[str(li)]
+                E, per = int(ent["n_experts"]), int(ent["bytes_per_expert"])
+                t = torch.empty((E, per), dtype=torch.uint8, pin_memory=True)
+                rows = t.numpy()
+                for e in range(E):
+                    CK.read_expert_into(man, li, e, rows[e], fds)
+                st._layers[int(li)] = t
+        finally:
+            for fd in fds.values():
+                os.close(fd)
         return st
 
     def region(self, layer: int, e: int) -> PinnedRegion:
