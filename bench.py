@@ -19,6 +19,9 @@ Also reported on the same line:
                 tokens/s and the gate/up GEMM's TFLOP/s vs 2.5 PFLOP/s dense bf16
   bounded_pool  the same decode with 32 of 128 experts per layer resident, misses refilled
                 from pinned host memory over PCIe, one routing read-back per layer (end to end)
+  layer_major_prefill  a 32768-token prompt through 8 layers layer by layer, each layer's
+                experts streamed from pinned host memory into a two-layer HBM ring while the
+                previous layer computes (PCIe-inclusive)
   cpu_baseline  the C restatement (oracle/) on the host cores, on a bounded sample
 """
 from __future__ import annotations
@@ -56,7 +59,7 @@ def parse():
     ap.add_argument("--pool-capacity", type=int, default=32)
     ap.add_argument("--pool-tokens", type=int, default=64)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--skip", default="", help="comma list of: prefill,pool,cpu,graph,report")
+    ap.add_argument("--skip", default="", help="comma list of: prefill,pool,layered,cpu,graph,report")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB (--steps times): the "
                          "known-size reference for scaling HBM byte counters")
@@ -417,6 +420,50 @@ def prefill_report(st: "Stack", T: int, reps: int = 3):
             "mfma_frac": round(flops / (us_layer * 1e-6) / 1e12 / BF16_PEAK_TFLOPS, 4)}
 
 
+def layered_bench(st: "Stack", n_layers: int = 8, prompt: int = 32768, chunk: int = 2048):
+    """Layer-major prefill of a long prompt (bigrig_amd/layered.py) with every layer's experts
+    streamed from pinned host memory over PCIe into a ring of two whole layers in HBM: the next
+    layer's copy overlapping this layer's chunks (read-ahead) against the serial schedule, and
+    the same chunks with the layers already resident (compute alone)."""
+    import torch
+
+    from bigrig_amd import layered, synth
+    spec = st.spec
+    nl = min(n_layers, len(st.host.layers()))
+    if nl < 2:
+        return None
+    ws = [layered.MoEWeights(l, st.routers[l], st.biases[l]) for l in range(nl)]
+    chunks = [synth.activations(chunk, spec.hidden, seed=8000 + j) for j in range(prompt // chunk)]
+    ring = layered.LayerRing(spec)
+
+    def run(layers, read_ahead, reset=True):
+        if reset:
+            ring.reset()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        layered.prefill(spec, layers, st.host, chunks, ring, read_ahead=read_ahead)
+        torch.cuda.synchronize()
+        return time.perf_counter() - t0
+
+    run(ws, True)
+    t_ra = min(run(ws, True) for _ in range(2))
+    t_ser = min(run(ws, False) for _ in range(2))
+    # compute alone: layers 0 and 1 alternate over the two sets, which already hold them
+    alt = [ws[i % 2] for i in range(nl)]
+    run(alt, True)
+    t_cmp = min(run(alt, True, reset=False) for _ in range(2))
+    layer_bytes = spec.n_experts * spec.bytes_per_expert
+    t_copy = max(t_ser - t_cmp, 1e-9)
+    ring.close()
+    return {"layers": nl, "prompt_tokens": len(chunks) * chunk, "chunk": chunk,
+            "layer_bytes": layer_bytes, "read_ahead_ms": round(t_ra * 1e3, 2),
+            "serial_ms": round(t_ser * 1e3, 2), "compute_ms": round(t_cmp * 1e3, 2),
+            "tok_s_read_ahead": round(len(chunks) * chunk / t_ra, 1),
+            "tok_s_serial": round(len(chunks) * chunk / t_ser, 1),
+            "pcie_gbs": round(nl * layer_bytes / t_copy / 1e9, 1),
+            "hidden_frac": round((t_ser - t_ra) / max(min(t_copy, t_cmp), 1e-9), 3)}
+
+
 def config_report():
     """The other shapes of the workload list, kernel level, all experts resident: OLMoE decode,
     256 experts + shared expert decode at batch 1 and 8, gpt-oss MXFP4 decode and a 512-token
@@ -560,6 +607,10 @@ def main():
     if "pool" not in skip:
         log("bounded pool")
         pool = pool_bench(args, st)
+    lay = None
+    if "layered" not in skip and "pool" not in skip:
+        log("layer-major prefill, experts streamed from host")
+        lay = layered_bench(st)
     cpu = None
     if "cpu" not in skip:
         log("cpu baseline")
@@ -638,6 +689,8 @@ def main():
     if pool is not None:
         rec["bounded_pool"] = {k2: (round(v, 4) if isinstance(v, float) else v)
                                for k2, v in pool.items()}
+    if lay is not None:
+        rec["layer_major_prefill"] = lay
     print(json.dumps(rec), flush=True)
 
 
