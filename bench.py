@@ -18,7 +18,10 @@ Also reported on the same line:
   prefill       one 2048-token chunk through the 48 layers (bucketing + grouped MFMA GEMMs),
                 tokens/s and the gate/up GEMM's TFLOP/s vs 2.5 PFLOP/s dense bf16
   bounded_pool  the same decode with 32 of 128 experts per layer resident, misses refilled
-                from pinned host memory over PCIe, one routing read-back per layer (end to end)
+                from pinned host memory over PCIe, one routing read-back per layer (end to end);
+                `host_served`: the kernels read misses from pinned host memory and residency
+                follows behind the forwards (no read-back wait); `host_served_plan`: the same
+                with the whole-layer plan for that memory (some layers whole, the rest smaller)
   layer_major_prefill  a 32768-token prompt through 8 layers layer by layer, each layer's
                 experts streamed from pinned host memory into a two-layer HBM ring while the
                 previous layer computes (PCIe-inclusive)
@@ -488,9 +491,12 @@ def config_report():
     return rep
 
 
-def pool_bench(args, st: "Stack"):
+def pool_bench(args, st: "Stack", host_served: bool = False, capacities=None):
     """Bounded pool end to end: C of E experts per layer resident, misses copied from pinned
-    host memory, one routing read-back per layer. PCIe-inclusive; never the headline value."""
+    host memory. Synchronous: one routing read-back per layer, misses admitted before the layer
+    computes. host_served: the kernels read misses from the pinned store themselves and
+    residency follows behind the forwards. `capacities` gives each layer its own C (a whole-layer
+    plan). PCIe-inclusive; never the headline value."""
     import torch
 
     from bigrig_amd.layer import MoELayer, StreamingSwitchGLU
@@ -499,9 +505,10 @@ def pool_bench(args, st: "Stack"):
     layers = st.host.layers()
     fetcher = PinnedFetcher(st.host)
     mods = []
-    for l in layers:
-        pool = ExpertPool(l, spec, args.pool_capacity).build()
-        sw = StreamingSwitchGLU(pool, fetcher)
+    for i, l in enumerate(layers):
+        cap = args.pool_capacity if capacities is None else capacities[i]
+        pool = ExpertPool(l, spec, cap).build()
+        sw = StreamingSwitchGLU(pool, fetcher, host_served=host_served)
         sw.refresh()
         mods.append(MoELayer(spec, st.routers[l], sw, router_bias=st.biases[l]))
     from bigrig_amd import synth
@@ -527,11 +534,15 @@ def pool_bench(args, st: "Stack"):
     dt = time.perf_counter() - t0
     hits = sum(m.switch._pool.hits for m in mods)
     miss = sum(m.switch._pool.misses for m in mods)
-    res = {"capacity": args.pool_capacity, "layers": len(layers),
+    res = {"capacity": args.pool_capacity if capacities is None else "per layer",
+           "layers": len(layers),
            "tok_s_layers": n / dt,
            "tok_s_48": n / dt * len(layers) / 48.0,
            "miss_rate": miss / max(1, hits + miss),
            "pcie_inclusive": True}
+    if host_served:
+        res["host_waits_s"] = sum(m.switch.sync_seconds for m in mods)
+        res["admit_gb"] = sum(m.switch._serve.admit_bytes for m in mods) / 1e9
     for m in mods:
         m.switch._pool.close()
     return res
@@ -605,8 +616,21 @@ def main():
         pre = prefill_bench(args, st)
     pool = None
     if "pool" not in skip:
+        from bigrig_amd.hostserve import plan_full_layers
         log("bounded pool")
         pool = pool_bench(args, st)
+        log("bounded pool, misses served from host memory")
+        pool["host_served"] = pool_bench(args, st, host_served=True)
+        nl = len(st.host.layers())
+        whole, rest = plan_full_layers(48, st.spec.n_experts, st.spec.top_k,
+                                       args.pool_capacity)
+        if whole:
+            caps = [st.spec.n_experts if i < round(whole * nl / 48) else rest
+                    for i in range(nl)]
+            log(f"bounded pool, host-served, {whole} of 48 layers whole, the rest at {rest}")
+            hp = pool_bench(args, st, host_served=True, capacities=caps)
+            hp["plan"] = {"whole_of_48": whole, "rest_capacity": rest}
+            pool["host_served_plan"] = hp
     lay = None
     if "layered" not in skip and "pool" not in skip:
         log("layer-major prefill, experts streamed from host")
@@ -687,8 +711,10 @@ def main():
     if report is not None:
         rec["report"] = report
     if pool is not None:
-        rec["bounded_pool"] = {k2: (round(v, 4) if isinstance(v, float) else v)
-                               for k2, v in pool.items()}
+        def rnd(d):
+            return {k2: (rnd(v) if isinstance(v, dict) else round(v, 4) if isinstance(v, float)
+                         else v) for k2, v in d.items()}
+        rec["bounded_pool"] = rnd(pool)
     if lay is not None:
         rec["layer_major_prefill"] = lay
     print(json.dumps(rec), flush=True)

@@ -112,6 +112,8 @@ struct brx_pool {
     hipEvent_t last_read;
     hipEvent_t refill_done;
     hipEvent_t g2s_uploaded;
+    const uint8_t* host;        // host backing (device-visible pinned memory) or null
+    int64_t host_stride;
     bool read_recorded;
     bool refill_recorded;
     bool refill_pending;
@@ -246,10 +248,103 @@ int brx_pool_set_g2s(brx_pool* p, const int32_t* g2s_host, int n, void* stream) 
     hipStream_t s = (hipStream_t)stream;
     // the staging copy of the previous upload must have been consumed before it is rewritten
     if (p->g2s_recorded) HIP_TRY(hipEventSynchronize(p->g2s_uploaded));
-    for (int e = 0; e < n; ++e) p->g2s_pinned[e] = g2s_host[e] > 0 ? g2s_host[e] : 0;
+    // -1 (absent) stays -1 when the kernels can serve the expert from host backing
+    for (int e = 0; e < n; ++e) p->g2s_pinned[e] = g2s_host[e] >= 0 ? g2s_host[e] : (p->host ? -1 : 0);
     HIP_TRY(hipMemcpyAsync(p->g2s_dev, p->g2s_pinned, sizeof(int32_t) * n, hipMemcpyHostToDevice, s));
     HIP_TRY(hipEventRecord(p->g2s_uploaded, s));
     p->g2s_recorded = true;
+    return BRX_OK;
+}
+
+int brx_pool_set_host_backing(brx_pool* p, const void* host_base, int64_t host_stride, size_t host_bytes) {
+    if (!p || !host_base) return fail(BRX_EINVAL, "pool or host_base is NULL");
+    if (p->host) return fail(BRX_EINVAL, "the pool already has host backing");
+    if (p->refill_recorded || p->g2s_recorded || p->read_recorded)
+        return fail(BRX_EINVAL, "host backing is set on a fresh pool, before any refill, table upload or forward");
+    const int E = p->d.n_experts;
+    if (host_stride < p->lay.bytes)
+        return fail(BRX_EINVAL, "host stride %lld is below the %lld bytes of an expert", (long long)host_stride,
+                    (long long)p->lay.bytes);
+    // the kernels read an expert with the alignment a slot gives it
+    if (((uintptr_t)host_base | (uintptr_t)host_stride) & 255)
+        return fail(BRX_EINVAL, "host_base and host_stride must be multiples of 256 bytes");
+    const size_t need = (size_t)(E - 1) * (size_t)host_stride + (size_t)p->lay.bytes;
+    if (host_bytes < need)
+        return fail(BRX_EINVAL, "%d experts at stride %lld need %zu bytes, the region has %zu", E,
+                    (long long)host_stride, need, host_bytes);
+    // both ends of the range must be pinned host memory the device sees at the same address
+    const uint8_t* ends[2] = {(const uint8_t*)host_base, (const uint8_t*)host_base + need - 1};
+    for (const uint8_t* q : ends) {
+        hipPointerAttribute_t at{};
+        hipError_t e = hipPointerGetAttributes(&at, q);
+        if (e != hipSuccess) {
+            (void)hipGetLastError();
+            return fail(BRX_EINVAL, "host backing %p is not memory the runtime knows (%s): allocate it pinned",
+                        (const void*)q, hipGetErrorString(e));
+        }
+        // the kernels are given host_base itself: the device must see it at that address
+        if (at.type != hipMemoryTypeHost || (q == ends[0] && at.devicePointer != (void*)q))
+            return fail(BRX_EINVAL, "host backing %p is not pinned host memory mapped at the same device "
+                        "address (type %d, device pointer %p)", (const void*)q, (int)at.type, at.devicePointer);
+    }
+    // nothing is resident yet: every entry starts as -1, "read from host"
+    p->host = (const uint8_t*)host_base;
+    p->host_stride = host_stride;
+    for (int e = 0; e < E; ++e) p->g2s_pinned[e] = -1;
+    HIP_TRY(hipMemcpy(p->g2s_dev, p->g2s_pinned, sizeof(int32_t) * E, hipMemcpyHostToDevice));
+    return BRX_OK;
+}
+
+int brx_pool_publish_async(brx_pool* p, int n, const int32_t* experts, const int32_t* slots, void* stream) {
+    if (!p || (n > 0 && (!experts || !slots))) return fail(BRX_EINVAL, "pool, experts or slots is NULL");
+    if (!p->host) return fail(BRX_EINVAL, "table entries are published only on a pool with host backing");
+    if (n < 0) return fail(BRX_EINVAL, "n %d < 0", n);
+    for (int i = 0; i < n; ++i) {
+        if (experts[i] < 0 || experts[i] >= p->d.n_experts)
+            return fail(BRX_ERANGE, "expert %d outside [0, %d)", experts[i], p->d.n_experts);
+        if (slots[i] < -1 || slots[i] >= p->capacity)
+            return fail(BRX_ERANGE, "slot %d outside [-1, %d)", slots[i], p->capacity);
+        for (int j = 0; j < i; ++j)
+            if (experts[j] == experts[i]) return fail(BRX_EINVAL, "expert %d appears twice", experts[i]);
+    }
+    for (int i0 = 0; i0 < n; i0 += kMaxTableEdits) {
+        TableEdits ed{};
+        ed.n = n - i0 < kMaxTableEdits ? n - i0 : kMaxTableEdits;
+        for (int i = 0; i < ed.n; ++i) {
+            ed.e[i] = experts[i0 + i];
+            ed.v[i] = slots[i0 + i];
+        }
+        hipError_t e = launch_table_set(p->g2s_dev, ed, (hipStream_t)stream);
+        if (e != hipSuccess) return hip_fail(e, "table update");
+    }
+    return BRX_OK;
+}
+
+int brx_pool_admit_async(brx_pool* p, int expert, int slot, const void* host_src, size_t nbytes,
+                         void* copy_stream) {
+    if (!p) return fail(BRX_EINVAL, "pool is NULL");
+    if (!p->host) return fail(BRX_EINVAL, "brx_pool_admit_async needs a pool with host backing");
+    if (expert < 0 || expert >= p->d.n_experts)
+        return fail(BRX_ERANGE, "expert %d outside [0, %d)", expert, p->d.n_experts);
+    if (slot < 0 || slot >= p->capacity) return fail(BRX_ERANGE, "slot %d outside [0, %d)", slot, p->capacity);
+    if (!host_src) return fail(BRX_EINVAL, "source is NULL");
+    if ((int64_t)nbytes != p->lay.bytes)
+        return fail(BRX_EINVAL, "the layout accounts for %lld bytes but the region supplied %zu. "
+                    "Refusing to write a partially-filled slot.", (long long)p->lay.bytes, nbytes);
+    hipStream_t cs = (hipStream_t)copy_stream;
+    // write-after-read: every forward issued so far may still read the slot's old expert
+    if (p->read_recorded) HIP_TRY(hipStreamWaitEvent(cs, p->last_read, 0));
+    HIP_TRY(hipMemcpyAsync(p->slots + (int64_t)slot * p->stride, host_src, nbytes, hipMemcpyHostToDevice, cs));
+    TableEdits ed{};
+    ed.n = 1;
+    ed.e[0] = expert;
+    ed.v[0] = slot;
+    hipError_t e = launch_table_set(p->g2s_dev, ed, cs);
+    if (e != hipSuccess) return hip_fail(e, "table update");
+    // forwards do not wait for this copy: until the table entry lands they read the expert
+    // from host backing, after it from the slot (the same bytes)
+    HIP_TRY(hipEventRecord(p->refill_done, cs));
+    p->refill_recorded = true;
     return BRX_OK;
 }
 
@@ -299,6 +394,8 @@ static FwdArgs make_args(const brx_layer_desc* d, brx_pool* p, const void* x, in
     a.slot_stride = p->stride;
     a.g2s = p->g2s_dev;
     a.capacity = p->capacity;
+    a.host = p->host;
+    a.host_stride = p->host_stride;
     a.shared = (const uint8_t*)shared_expert;
     a.auto_shared = (token_mode && shared_expert) ? 1 : 0;
     a.lay = p->lay;

@@ -9,6 +9,7 @@
 namespace brx {
 
 constexpr int kWave = 64;
+constexpr int kMaxTableEdits = 32;   // table entries one brx_pool_publish_async launch sets
 
 // ------------------------------------------------------------------ layout (host + device)
 struct Proj {
@@ -61,6 +62,8 @@ struct FwdArgs {
     int64_t slot_stride;        // bytes between slots
     const int32_t* g2s;         // [E]
     int32_t capacity;
+    const uint8_t* host;        // host backing: expert e at host + e * host_stride, or null
+    int64_t host_stride;
     const uint8_t* shared;      // shared expert bytes or null (expert id E)
     int32_t auto_shared;        // token mode: every token also runs the shared expert
     Layout lay;                 // routed expert layout
@@ -88,6 +91,26 @@ __device__ __forceinline__ int pair_tok(const FwdArgs& a, int p) {
 }
 __device__ __forceinline__ int pair_row(const FwdArgs& a, int p) {
     return a.prow ? min(max(a.prow[p], 0), a.yrows - 1) : p;
+}
+
+// Where an expert's bytes are read from, as one int "slot code": c >= 0 pool slot c; c == -1
+// the shared expert; c <= -2 routed expert -2 - c read straight from the pool's host backing
+// (pinned host memory the GPU reads over the bus), which a table entry < 0 selects when the
+// pool has one. Without host backing a negative entry is clamped to slot 0, so a bad table
+// computes wrong rows rather than reading out of bounds.
+__device__ __forceinline__ int slot_code(const FwdArgs& a, int e, int v) {
+    return (v < 0 && a.host) ? -2 - e : min(max(v, 0), a.capacity - 1);
+}
+// A code read back from the library's own tables, clamped into what the arguments allow.
+__device__ __forceinline__ int clamp_code(const FwdArgs& a, int c) {
+    if (c == -1) return a.shared ? -1 : 0;
+    if (c < -1) return a.host ? max(c, -1 - a.E) : 0;
+    return min(c, a.capacity - 1);
+}
+__device__ __forceinline__ const uint8_t* code_base(const FwdArgs& a, int c) {
+    if (c >= 0) return a.slots + (int64_t)c * a.slot_stride;
+    if (c == -1) return a.shared;
+    return a.host + (int64_t)(-2 - c) * a.host_stride;
 }
 
 // ------------------------------------------------------------------ device helpers
@@ -282,6 +305,12 @@ hipError_t launch_router_logits(const brx_layer_desc& d, const void* x, const vo
                                 const float* bias, const void* sgw, int T, float* logits,
                                 hipStream_t s);
 // phases: bit 0 = first half (gate/up), bit 1 = second half (down + combine)
+struct TableEdits {
+    int32_t n;
+    int32_t e[kMaxTableEdits];
+    int32_t v[kMaxTableEdits];
+};
+hipError_t launch_table_set(int32_t* g2s, const TableEdits& ed, hipStream_t s);
 hipError_t launch_decode(const FwdArgs& a, void* ws, int phases, hipStream_t s);
 hipError_t launch_prefill(const FwdArgs& a, void* ws, size_t ws_bytes, int phases, hipStream_t s);
 size_t prefill_workspace_bytes(const FwdArgs& a);

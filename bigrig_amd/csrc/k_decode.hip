@@ -92,7 +92,7 @@ __device__ __forceinline__ bool plan_entry(const FwdArgs& a, int u, int e_raw, c
         en.nt = __popcll(en.mm);
         en.shared = false;
         int s = -1;
-        if (eu < a.E) s = min(max(s_g2s[eu], 0), a.capacity - 1);
+        if (eu < a.E) s = slot_code(a, eu, s_g2s[eu]);
         en.slot = s;
     } else {
         en.e = a.E;
@@ -174,9 +174,6 @@ struct PairIter {
     }
 };
 
-__device__ __forceinline__ const uint8_t* slot_base(const FwdArgs& a, int slot) {
-    return slot >= 0 ? a.slots + (int64_t)slot * a.slot_stride : a.shared;
-}
 
 
 // ------------------------------------------------------------------ weight units
@@ -482,7 +479,7 @@ __global__ __launch_bounds__(kThreads) void k_dec_gateup(FwdArgs a, uint16_t* __
         const int r0 = blockIdx.x * kWaves * RW;
         if (r0 >= inter) return;
         const Layout& L = sh ? a.lay_sh : a.lay;
-        const uint8_t* base = slot_base(a, en.slot);
+        const uint8_t* base = code_base(a, en.slot);
         const int g = lane >> lsp, sl = lane & (SP - 1);
         const int rr = (tid >> 6) * RW + g;
         const int row = min(r0 + rr, inter - 1);
@@ -550,7 +547,7 @@ __global__ __launch_bounds__(kThreads) void k_dec_gateup(FwdArgs a, uint16_t* __
             const int r0 = blockIdx.x * kWaves * RW;
             if (r0 >= inter) continue;   // uniform
             const Layout& L = sh ? a.lay_sh : a.lay;
-            const uint8_t* base = slot_base(a, en.slot);
+            const uint8_t* base = code_base(a, en.slot);
             const int g = lane >> lsp, sl = lane & (SP - 1);
             const int rr = (tid >> 6) * RW + g;
             const int row = min(r0 + rr, inter - 1);
@@ -611,9 +608,9 @@ __device__ __forceinline__ void dec_down_epilogue(const FwdArgs& a, float* ys, i
         if (a.has_bias) {
             int e = p < P ? min(max(a.pexp[p], 0), a.shared ? a.E : a.E - 1) : a.E;
             int s = -1;
-            if (e < a.E) s = min(max(a.g2s[e], 0), a.capacity - 1);
-            const Layout& L = s < 0 ? a.lay_sh : a.lay;
-            y += bf2f(reinterpret_cast<const uint16_t*>(slot_base(a, s) + L.p[2].bias)[nn]);
+            if (e < a.E) s = slot_code(a, e, a.g2s[e]);
+            const Layout& L = s == -1 ? a.lay_sh : a.lay;
+            y += bf2f(reinterpret_cast<const uint16_t*>(code_base(a, s) + L.p[2].bias)[nn]);
         }
         uint32_t yb = f2bf(y);
         ys[it] = bf2f(yb);
@@ -691,9 +688,9 @@ __global__ __launch_bounds__(kThreads) void k_dec_down(FwdArgs a, const uint16_t
     if (have_first) {
         // an item past the last entry reads a stale table slot: point it at slot 0 instead
         int sf = (it_first >> lrbd) < n ? slot_first : 0;
-        sf = min(max(sf, a.shared ? -1 : 0), a.capacity - 1);
-        const Layout& L = sf < 0 ? a.lay_sh : a.lay;
-        units_load<MODE, UPL>(slot_base(a, sf), L.p[2], min(n0 + (it_first & (RBD - 1)), H - 1), sl, SP, ud);
+        sf = clamp_code(a, sf);
+        const Layout& L = sf == -1 ? a.lay_sh : a.lay;
+        units_load<MODE, UPL>(code_base(a, sf), L.p[2], min(n0 + (it_first & (RBD - 1)), H - 1), sl, SP, ud);
     }
     if (tid < kWave) {
         nt0 = tid < n ? nt0 : 0;
@@ -742,8 +739,8 @@ __global__ __launch_bounds__(kThreads) void k_dec_down(FwdArgs a, const uint16_t
         int r = valid ? it & (RBD - 1) : 0;
         if (!have_first) {
             const int slot = s_slot[u0 + iu];
-            const Layout& L = slot < 0 ? a.lay_sh : a.lay;
-            units_load<MODE, UPL>(slot_base(a, slot), L.p[2], min(n0 + r, H - 1), sl, SP, ud);
+            const Layout& L = slot == -1 ? a.lay_sh : a.lay;
+            units_load<MODE, UPL>(code_base(a, slot), L.p[2], min(n0 + r, H - 1), sl, SP, ud);
         }
         float* hsum = all_fit ? hsum_all : reinterpret_cast<float*>(hs + (size_t)rows * Umax * kXU);
         if (!all_fit) {
@@ -757,13 +754,13 @@ __global__ __launch_bounds__(kThreads) void k_dec_down(FwdArgs a, const uint16_t
                 iu = valid ? it >> lrbd : 0;
                 r = valid ? it & (RBD - 1) : 0;
                 const int slot = s_slot[u0 + iu];
-                const Layout& L = slot < 0 ? a.lay_sh : a.lay;
-                units_load<MODE, UPL>(slot_base(a, slot), L.p[2], min(n0 + r, H - 1), sl, SP, ud);
+                const Layout& L = slot == -1 ? a.lay_sh : a.lay;
+                units_load<MODE, UPL>(code_base(a, slot), L.p[2], min(n0 + r, H - 1), sl, SP, ud);
             }
             const int u = u0 + iu;
             const int slot = s_slot[u];
             const int nt = valid ? s_nt[u] : 0;
-            const int U = (slot < 0 ? a.lay_sh : a.lay).p[2].n_in / 64;
+            const int U = (slot == -1 ? a.lay_sh : a.lay).p[2].n_in / 64;
             const int srow = s_first[u] - row0;   // staged row of the item's first pair (batched)
             // the SP lanes of one item share nt; lanes past the items have nt = 0 and only take
             // part in the shuffles
@@ -832,11 +829,11 @@ __global__ __launch_bounds__(kThreads) void k_dec_down_fit(FwdArgs a, const uint
         }
         const int nt = in_range ? (int)hd.y : 0;
         int slot = nt > 0 ? (int)hd.x : 0;
-        slot = min(max(slot, a.shared ? -1 : 0), a.capacity - 1);
-        const Layout& L = slot < 0 ? a.lay_sh : a.lay;
+        slot = clamp_code(a, slot);
+        const Layout& L = slot == -1 ? a.lay_sh : a.lay;
         const int U = L.p[2].n_in / 64;
         Units<MODE, UPL> ud;
-        units_load<MODE, UPL>(slot_base(a, slot), L.p[2], min(n0 + r, H - 1), sl, SP, ud);
+        units_load<MODE, UPL>(code_base(a, slot), L.p[2], min(n0 + r, H - 1), sl, SP, ud);
         if (it0 == 0) __syncthreads();
         const int pr[kMaxTok] = {(int)p0.x, (int)p0.y, (int)p0.z, (int)p0.w,
                                  (int)p1.x, (int)p1.y, (int)p1.z, (int)p1.w};

@@ -28,7 +28,19 @@ __global__ __launch_bounds__(256) void k_dequant(const uint8_t* __restrict__ bas
     }
 }
 
+// A batch of expert-table entries set in stream order (the values travel as kernel arguments,
+// so nothing on the host has to outlive the call). Entries are distinct.
+__global__ __launch_bounds__(64) void k_table_set(int32_t* __restrict__ g2s, TableEdits ed) {
+    const int i = threadIdx.x;
+    if (i < ed.n) g2s[ed.e[i]] = ed.v[i];
+}
+
 }  // namespace
+
+hipError_t launch_table_set(int32_t* g2s, const TableEdits& ed, hipStream_t s) {
+    hipLaunchKernelGGL(k_table_set, dim3(1), dim3(64), 0, s, g2s, ed);
+    return hipGetLastError();
+}
 
 hipError_t launch_dequant(const brx_layer_desc& d, const Layout& L, const uint8_t* expert,
                           int proj, float* out, hipStream_t s) {

@@ -58,6 +58,7 @@ __device__ __forceinline__ int bucket_expert(const int32_t* __restrict__ pexp, i
 __global__ __launch_bounds__(kBucketThreads) void k_bucket(const int32_t* __restrict__ pexp, int P, int E,
                                                            int E_ext, int T_sh, int BM,
                                                            const int32_t* __restrict__ g2s, int capacity,
+                                                           int host,
                                                            int32_t* __restrict__ order,
                                                            int32_t* __restrict__ offsets,
                                                            int32_t* __restrict__ tile_start,
@@ -120,7 +121,10 @@ __global__ __launch_bounds__(kBucketThreads) void k_bucket(const int32_t* __rest
     if (tinfo) {
         const int n = hist[e], off = base_s[0], big = base_s[1], small = base_s[2];
         int slot = 0;
-        if (e < E && g2s) slot = min(max(g2s[e], 0), capacity - 1);
+        if (e < E && g2s) {   // the slot code: a slot, or -2 - e for an expert read from host backing
+            const int v = g2s[e];
+            slot = (v < 0 && host) ? -2 - e : min(max(v, 0), capacity - 1);
+        }
         for (int j = tid; j * BM < n; j += kBucketThreads) {
             const int rows = min(BM, n - j * BM);
             tinfo[rows > BM / 2 ? big + j : small] = make_int4(e, off + j * BM, rows, slot);
@@ -301,7 +305,7 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
     const int K = KIND == 0 ? H : inter;
     const int nsteps = K / kBK;
     const Layout& L = sh ? a.lay_sh : a.lay;
-    const uint8_t* base = sh ? a.shared : a.slots + (int64_t)slot * a.slot_stride;
+    const uint8_t* base = sh ? a.shared : code_base(a, clamp_code(a, slot));
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int kh = lane >> 5, l32 = lane & 31;
@@ -685,10 +689,10 @@ hipError_t launch_gemm(const FwdArgs& a, const PfWs& w, int E_ext, int Imax, uin
 }
 
 hipError_t launch_bucket(const int32_t* pexp, int P, int E, int E_ext, int T_sh, int BM,
-                         const int32_t* g2s, int capacity, int32_t* order, int32_t* offsets,
+                         const int32_t* g2s, int capacity, int host, int32_t* order, int32_t* offsets,
                          int32_t* tile_start, int4* tinfo, hipStream_t s) {
     hipLaunchKernelGGL(k_bucket, dim3(E_ext), dim3(kBucketThreads), sizeof(int32_t) * E_ext, s, pexp, P, E,
-                       E_ext, T_sh, BM, g2s, capacity, order, offsets, tile_start, tinfo);
+                       E_ext, T_sh, BM, g2s, capacity, host, order, offsets, tile_start, tinfo);
     return hipGetLastError();
 }
 
@@ -698,7 +702,7 @@ size_t prefill_workspace_bytes(const FwdArgs& a) { return carve(a, nullptr).byte
 
 hipError_t launch_sort_pairs(const int32_t* pexp, int P, int E, int E_ext, int T_sh, int BM,
                              int32_t* order, int32_t* offsets, int32_t* tile_start, hipStream_t s) {
-    return launch_bucket(pexp, P, E, E_ext, T_sh, BM, nullptr, 1, order, offsets, tile_start, nullptr, s);
+    return launch_bucket(pexp, P, E, E_ext, T_sh, BM, nullptr, 1, 0, order, offsets, tile_start, nullptr, s);
 }
 
 hipError_t launch_combine(const uint16_t* y_routed, const uint16_t* y_shared, const float* w,
@@ -721,7 +725,7 @@ hipError_t launch_prefill(const FwdArgs& a, void* ws, size_t ws_bytes, int phase
     uint16_t* y_routed = a.yun ? a.yun : w.y_routed;
     hipError_t err = hipSuccess;
     if (phases & 1) {
-        err = launch_bucket(a.pexp, P, a.E, E_ext, T_sh, kBM, a.g2s, a.capacity, w.order, w.offsets,
+        err = launch_bucket(a.pexp, P, a.E, E_ext, T_sh, kBM, a.g2s, a.capacity, a.host != nullptr, w.order, w.offsets,
                             w.tile_start, w.tinfo, s);
         if (err != hipSuccess) return err;
     }

@@ -11,7 +11,11 @@ by the caller (stream.py:1523-1525). Its paths are the reference's:
   (stream.py:1447-1449, 1508);
 * a chunk that routes to more experts than the pool holds: pairs sorted by expert (stable),
   cut into spans of at most C experts (`_pair_chunks`), each span made resident and computed,
-  rows written straight back to their (token, k) positions (stream.py:1521-1561).
+  rows written straight back to their (token, k) positions (stream.py:1521-1561);
+* host-served (`host_served=True`, no counterpart in the reference): a bounded pool whose
+  misses the kernels read from pinned host memory, so it too stays on the sync-free path, its
+  residency updated behind the forwards from routing copied back asynchronously
+  (`hostserve.py`).
 
 Whatever the path and the capacity, a row's arithmetic is the same kernel in the same order:
 the kernel family is chosen by the call's token count only (decode for <= 8 tokens, the
@@ -134,7 +138,10 @@ def sort_pairs(spec: LayerSpec, idx, stream=None):
 class StreamingSwitchGLU:
     """Drop-in semantics of the reference's StreamingSwitchGLU over an HBM ExpertPool."""
 
-    def __init__(self, pool: ExpertPool, fetcher, shared=None):
+    def __init__(self, pool: ExpertPool, fetcher, shared=None, host_served: bool = False):
+        """host_served: give the (fresh) pool host backing so misses are served by the kernels
+        from the fetcher's pinned host store and residency is kept behind the forwards
+        (`hostserve.HostServedPool`); the operator is then always on the sync-free path."""
         self._pool = pool
         self._fetcher = fetcher
         self.spec = pool.spec
@@ -144,6 +151,15 @@ class StreamingSwitchGLU:
         self.sync_seconds = 0.0
         self.chunked_calls = 0
         self._sync_free = False
+        self._serve = None
+        if host_served:
+            store = getattr(fetcher, "store", None)
+            if store is None:
+                raise ValueError("host-served misses read the experts from a pinned host store: "
+                                 "pass a PinnedFetcher")
+            from .hostserve import HostServedPool
+            self._serve = HostServedPool(pool, store)
+            self._sync_free = True
 
     # -- residency (stream.py:922-978) -------------------------------------------------------
     def ensure(self, indices, ranks=None) -> np.ndarray:
@@ -182,9 +198,22 @@ class StreamingSwitchGLU:
         return self._pool.g2s[gi]
 
     def refresh(self) -> bool:
-        """Take the sync-free path iff every expert is resident (stream.py:1579-1603)."""
-        self._sync_free = self._pool.full
+        """Take the sync-free path iff every expert is resident (stream.py:1579-1603), or the
+        pool serves its misses from host memory."""
+        self._sync_free = self._pool.full or self._serve is not None
         return self._sync_free
+
+    def _before(self, stream=None) -> None:
+        """Ahead of a sync-free forward: the table as residency left it (uploaded if it changed),
+        or, host-served, the admissions decided from the routing that has come back since."""
+        if self._serve is not None:
+            self._serve.service(stream)
+        else:
+            self._pool.g2s_device(_stream(stream))
+
+    def _after(self, idx, stream=None) -> None:
+        if self._serve is not None:
+            self._serve.record(idx, stream)
 
     @staticmethod
     def _pair_chunks(sorted_experts: np.ndarray, C: int):
@@ -231,8 +260,9 @@ class StreamingSwitchGLU:
         idx = indices.reshape(-1, k).to(torch.int32).contiguous()
         y = torch.empty((T, k, H), dtype=torch.bfloat16, device=x2.device)
         if self._sync_free:
-            self._pool.g2s_device(_stream(stream))   # uploads only if residency changed
+            self._before(stream)
             moe_forward(self.spec, self._pool, x2, idx, y_unreduced=y, flags=flags, stream=stream)
+            self._after(idx, stream)
             return y.reshape(*indices.shape[:-1], k, H)
         gi = self._host_routing(idx)
         if k > self._pool.capacity:
@@ -258,9 +288,10 @@ class StreamingSwitchGLU:
         out = torch.empty((T, H), dtype=torch.bfloat16, device=x2.device)
         shared = self.shared
         if self._sync_free:
-            self._pool.g2s_device(_stream(stream))   # uploads only if residency changed
+            self._before(stream)
             moe_forward(self.spec, self._pool, x2, idx, w, shared, sgate, out=out, flags=flags,
                         stream=stream)
+            self._after(idx, stream)
             return out
         gi = self._host_routing(idx)
         if k > self._pool.capacity:
@@ -307,12 +338,19 @@ class MoELayer:
         x2 = x.reshape(-1, self.spec.hidden).contiguous()
         sw = self.switch
         if sw._sync_free:
-            # every expert resident: routing, experts and combine in one library call, the
-            # routing never read by the host (stream.py:1377-1394)
-            sw._pool.g2s_device(_stream(stream))   # uploads only if residency changed
+            # every expert resident (or served from host memory): routing, experts and combine
+            # in one library call, the routing never waited for by the host (stream.py:1377-1394)
+            sw._before(stream)
             sgw = self.shared_gate_w if sw.shared is not None else None
+            idx = None
+            if sw._serve is not None:
+                import torch
+                idx = torch.empty((x2.shape[0], self.spec.top_k), dtype=torch.int32,
+                                  device=x2.device)
             out = moe_block(self.spec, sw._pool, x2, self.router_w, self.router_bias, sgw,
-                            sw.shared, flags=path_flag(x2.shape[0]), stream=stream)
+                            sw.shared, out_idx=idx, flags=path_flag(x2.shape[0]), stream=stream)
+            if idx is not None:
+                sw._after(idx, stream)
             return out.reshape(x.shape)
         idx, w, sg = self.route(x2, stream)
         out = sw.forward_combined(x2, idx, w, sg, stream)

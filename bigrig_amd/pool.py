@@ -268,6 +268,8 @@ class ExpertPool:
         self._slots = slots
         self._device = device
         self._built = False
+        self.last_evicted = -1      # expert the latest _victim() call evicted (-1: a free slot)
+        self.host_served = False    # set by HostServedPool: table entries are then set one by one
 
     # -- construction -------------------------------------------------------
     @property
@@ -312,6 +314,7 @@ class ExpertPool:
     def _victim(self, protect=()) -> int:
         """Free a slot (stream.py:644-690): the free list first, then the policy's victim
         outside `protect`, else the least recently admitted unprotected slot."""
+        self.last_evicted = -1
         if self._free:
             return self._free.pop()
         protect = {int(x) for x in protect}
@@ -334,6 +337,7 @@ class ExpertPool:
                 f"layer {self.layer}: every one of {self.capacity} slots holds an expert this "
                 f"step still needs. Capacity must be at least top-k.")
         slot = int(self.g2s[ev])
+        self.last_evicted = ev
         self.policy.evicted(ev)
         self.g2s[ev] = -1
         self.s2g[slot] = -1
@@ -389,7 +393,7 @@ class ExpertPool:
 
     def g2s_device(self, stream) -> None:
         """Upload the table when residency changed (stream.py:791-797); stream-ordered."""
-        if self._g2s_dirty:
+        if self._g2s_dirty and not self.host_served:
             self._slots.set_table(self.g2s, stream)
             self._g2s_dirty = False
 

@@ -131,6 +131,38 @@ int brx_pool_set_g2s(brx_pool* p, const int32_t* g2s_host, int n, void* stream);
 /* Block until every copy and forward issued against the pool has finished. */
 int brx_pool_sync(brx_pool* p);
 
+/* ---- host-served misses (no per-layer host round trip)
+ * The reference keeps a bounded layer off the sync-free path because it must read the routing
+ * back to find its misses (stream.py:1440-1450, 1579-1603; SURVEY's "device-side miss
+ * detection", autoconfig.py:52-73 for the trade it forces). With host backing the kernels
+ * detect a miss themselves: a table entry of -1 makes them read that expert's bytes from the
+ * layer's pinned host store over the bus instead of from a slot, so every layer can take the
+ * sync-free path and the host updates residency behind the forwards, from routing it copies
+ * back asynchronously.
+ *
+ * Give the pool host backing: the layer's routed experts in pinned host memory, expert e at
+ * host_base + e * host_stride (host_bytes in all), mapped at the same address on the device
+ * (checked). Only on a fresh pool (no refill, table upload or forward yet); every table entry
+ * starts at -1; the memory must outlive the pool's last forward. host_base and host_stride
+ * must be multiples of 256. */
+int brx_pool_set_host_backing(brx_pool* p, const void* host_base, int64_t host_stride,
+                              size_t host_bytes);
+/* Set n table entries experts[i] -> slots[i] (slot -1: read from host backing) on `stream`, in
+ * stream order; the values are kernel arguments, nothing is read from the host later. Used on
+ * the compute stream to retire a victim (-1) before its slot is rewritten. Host backing
+ * required; experts distinct. */
+int brx_pool_publish_async(brx_pool* p, int n, const int32_t* experts, const int32_t* slots,
+                           void* stream);
+/* Admit expert `expert` into `slot` behind the forwards: on copy_stream, wait for every forward
+ * already issued against the pool, copy the expert's bytes from pinned host memory into the
+ * slot, then set table[expert] = slot. Forwards do not wait for it; until the entry lands they
+ * read the expert from host backing. The caller retires the slot's previous expert with
+ * brx_pool_publish_async(-1) on the compute stream first, and does not retire `expert` again
+ * before this copy has finished (the copy stream's table write would land after it). Host
+ * backing required. Replaces the slot write of admit_arrays (stream.py:765-769) on this path. */
+int brx_pool_admit_async(brx_pool* p, int expert, int slot, const void* host_src, size_t nbytes,
+                         void* copy_stream);
+
 /* ---------------------------------------------------------------- compute */
 
 /* Router top-k for T tokens: logits = x . W_r^T (+ bias), then the layer's routing rule.
