@@ -133,8 +133,8 @@ int brx_pool_sync(brx_pool* p);
 
 /* ---- host-served misses (no per-layer host round trip)
  * The reference keeps a bounded layer off the sync-free path because it must read the routing
- * back to find its misses (stream.py:1440-1450, 1579-1603; SURVEY's "device-side miss
- * detection", autoconfig.py:52-73 for the trade it forces). With host backing the kernels
+ * back to find its misses (stream.py:1440-1450, 1579-1603; autoconfig.py:52-109 for the
+ * whole-layer trade it forces). With host backing the kernels
  * detect a miss themselves: a table entry of -1 makes them read that expert's bytes from the
  * layer's pinned host store over the bus instead of from a slot, so every layer can take the
  * sync-free path and the host updates residency behind the forwards, from routing it copies
