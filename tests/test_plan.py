@@ -41,3 +41,38 @@ def _search(L, E, k, cap, over=1):
 def test_matches_brute_force():
     for L, E, k, cap in itertools.product(range(1, 7), range(2, 13), range(1, 4), range(1, 14)):
         assert plan_full_layers(L, E, k, cap) == _search(L, E, k, cap), (L, E, k, cap)
+
+
+def _spend(whole, rest, n_layers, n_experts):
+    return n_experts * whole + rest * (n_layers - whole)
+
+
+def test_sweep_never_overspends_or_starves():
+    """The properties the reference's planner tests hold it to (tests/test_fulllayers.py:33-131):
+    no plan spends more slots than the uniform one, none leaves a layer at or below top-k, none
+    holds every layer whole, more memory never means fewer whole layers, re-planning from the
+    streamed capacity does not ratchet up."""
+    for n_layers in (2, 4, 12, 24, 48, 64):
+        for n_experts in (8, 16, 60, 64, 128, 256):
+            for top_k in (1, 2, 4, 8, 16):
+                if top_k >= n_experts:
+                    continue
+                prev = -1
+                for cap in range(top_k, n_experts + 1):
+                    whole, rest = plan_full_layers(n_layers, n_experts, top_k, cap)
+                    assert _spend(whole, rest, n_layers, n_experts) <= cap * n_layers
+                    assert whole < n_layers
+                    if whole:
+                        assert top_k < rest <= n_experts
+                        w2, _ = plan_full_layers(n_layers, n_experts, top_k, rest)
+                        assert w2 <= whole
+                    if cap < n_experts:
+                        assert whole >= prev, (n_layers, n_experts, top_k, cap)
+                        prev = whole
+
+
+def test_nonsense_in_a_safe_plan_out():
+    for args in ((0, 128, 8, 36), (48, 0, 8, 36), (48, 128, 0, 36), (48, 128, 8, 0),
+                 (-4, 128, 8, 36), (48, 128, 200, 36), (48, 8, 8, 8)):
+        whole, rest = plan_full_layers(*args)
+        assert whole >= 0 and rest >= 0 and whole < max(1, args[0]), (args, whole, rest)
