@@ -25,6 +25,8 @@ Also reported on the same line:
   layer_major_prefill  a 32768-token prompt through 8 layers layer by layer, each layer's
                 experts streamed from pinned host memory into a two-layer HBM ring while the
                 previous layer computes (PCIe-inclusive)
+  policy_replay the eviction-policy trace replay (host C++, libbrx_replay.so) against the
+                Python restatement, requests/s on the shipped Qwen3 routing trace
   cpu_baseline  the C restatement (oracle/) on the host cores, on a bounded sample
 """
 from __future__ import annotations
@@ -62,7 +64,7 @@ def parse():
     ap.add_argument("--pool-capacity", type=int, default=32)
     ap.add_argument("--pool-tokens", type=int, default=64)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--skip", default="", help="comma list of: prefill,pool,layered,cpu,graph,report")
+    ap.add_argument("--skip", default="", help="comma list of: prefill,pool,layered,replay,cpu,graph,report")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB (--steps times): the "
                          "known-size reference for scaling HBM byte counters")
@@ -548,6 +550,35 @@ def pool_bench(args, st: "Stack", host_served: bool = False, capacities=None):
     return res
 
 
+def replay_bench() -> dict:
+    """Trace-replay throughput (host CPU): the Python restatement of LFUDA on two layers of the
+    shipped Qwen3 routing trace against the native sweep over all 48 layers at three
+    capacities, LFUDA and the Belady bound, on 16 threads; miss rates as evaluate() gives them."""
+    import numpy as np
+
+    from bigrig_amd import policy as P
+    from bigrig_amd import replay as R
+    idx = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "tests", "golden",
+                               "qwen3_full.npz"))["idx"].astype(np.int32)
+    L, T, k = idx.shape
+    caps = [16, 32, 64]
+    t0 = time.perf_counter()
+    for l in range(2):
+        seq, ranks = P.layer_sequence(idx, l)
+        P.simulate(seq, 32, 128, P.LFUDA, ranks)
+    py = 2 * T * k / (time.perf_counter() - t0)
+    out = {"trace": f"qwen3 routing, {L} layers x {T} tokens x top-{k}", "capacities": caps,
+           "python_lfuda_req_s": round(py)}
+    for name in ("lfuda", "belady"):
+        t0 = time.perf_counter()
+        m = R.trace_misses(name, idx, caps, 128, threads=16)
+        dt = time.perf_counter() - t0
+        out[f"native_{name}_req_s"] = round(len(caps) * L * T * k / dt)
+        out[f"{name}_miss_rate"] = [round(float(v), 4) for v in m.sum(1) / (L * T * k)]
+    out["threads"] = 16
+    return out
+
+
 def cpu_bench(args, st: "Stack"):
     """The oracle's C restatement (OpenMP) on a bounded sample: decode tokens through two
     layers until cpu_seconds of work, scaled to the 48-layer stack."""
@@ -635,6 +666,10 @@ def main():
     if "layered" not in skip and "pool" not in skip:
         log("layer-major prefill, experts streamed from host")
         lay = layered_bench(st)
+    rep = None
+    if "replay" not in skip:
+        log("policy replay (host)")
+        rep = replay_bench()
     cpu = None
     if "cpu" not in skip:
         log("cpu baseline")
@@ -717,6 +752,8 @@ def main():
         rec["bounded_pool"] = rnd(pool)
     if lay is not None:
         rec["layer_major_prefill"] = lay
+    if rep is not None:
+        rec["policy_replay"] = rep
     print(json.dumps(rec), flush=True)
 
 

@@ -1,6 +1,7 @@
-"""Build libbrx.so (the HIP kernels and C-ABI) for gfx950, in-tree, with hipcc.
+"""Build libbrx.so (the HIP kernels and C-ABI) for gfx950, in-tree, with hipcc, and the
+host-only trace-replay library libbrx_replay.so with g++.
 
-    python -m bigrig_amd.build            # compile bigrig_amd/libbrx.so
+    python -m bigrig_amd.build            # compile bigrig_amd/libbrx.so and libbrx_replay.so
 
 The library is one hipcc invocation over every `csrc/*.hip` file. Packed FP32 instructions are
 disabled for device code (`-Xclang -target-feature -Xclang -packed-fp32-ops`); the host pass
@@ -22,6 +23,7 @@ ROOT = os.path.dirname(PKG)
 CSRC = os.path.join(PKG, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 LIB = os.path.join(PKG, "libbrx.so")
+REPLAY_LIB = os.path.join(PKG, "libbrx_replay.so")
 ARCH = "gfx950"
 
 
@@ -52,7 +54,22 @@ def build(verbose: bool = False) -> str:
     if verbose and out.strip():
         print(out)
     os.replace(tmp, LIB)
+    build_replay(verbose)
     return LIB
+
+
+def build_replay(verbose: bool = False) -> str:
+    """libbrx_replay.so: csrc/replay.cpp, plain C++ for the host (no GPU code)."""
+    tmp = REPLAY_LIB + ".tmp"
+    cmd = [shutil.which("g++") or "g++", "-O3", "-std=c++17", "-fPIC", "-shared", "-pthread",
+           "-I", INCLUDE, os.path.join(CSRC, "replay.cpp"), "-o", tmp]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"g++ failed ({r.returncode}):\n{r.stdout}{r.stderr}")
+    os.replace(tmp, REPLAY_LIB)
+    return REPLAY_LIB
 
 
 if __name__ == "__main__":
