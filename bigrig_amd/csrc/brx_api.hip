@@ -112,8 +112,7 @@ struct brx_pool {
     hipEvent_t last_read;
     hipEvent_t refill_done;
     hipEvent_t g2s_uploaded;
-    const uint8_t* host;        // host backing (device-visible pinned memory) or null
-    int64_t host_stride;
+    const uint8_t* host;        // host backing (device-visible pinned memory), slot stride apart, or null
     bool read_recorded;
     bool refill_recorded;
     bool refill_pending;
@@ -262,12 +261,11 @@ int brx_pool_set_host_backing(brx_pool* p, const void* host_base, int64_t host_s
     if (p->refill_recorded || p->g2s_recorded || p->read_recorded)
         return fail(BRX_EINVAL, "host backing is set on a fresh pool, before any refill, table upload or forward");
     const int E = p->d.n_experts;
-    if (host_stride < p->lay.bytes)
-        return fail(BRX_EINVAL, "host stride %lld is below the %lld bytes of an expert", (long long)host_stride,
-                    (long long)p->lay.bytes);
-    // the kernels read an expert with the alignment a slot gives it
-    if (((uintptr_t)host_base | (uintptr_t)host_stride) & 255)
-        return fail(BRX_EINVAL, "host_base and host_stride must be multiples of 256 bytes");
+    // the kernels address a host expert exactly as a slot: same stride, same alignment
+    if (host_stride != p->stride)
+        return fail(BRX_EINVAL, "host stride %lld must equal the slot stride %lld (bytes per expert rounded "
+                    "up to 256)", (long long)host_stride, (long long)p->stride);
+    if ((uintptr_t)host_base & 255) return fail(BRX_EINVAL, "host_base must be a multiple of 256 bytes");
     const size_t need = (size_t)(E - 1) * (size_t)host_stride + (size_t)p->lay.bytes;
     if (host_bytes < need)
         return fail(BRX_EINVAL, "%d experts at stride %lld need %zu bytes, the region has %zu", E,
@@ -289,7 +287,6 @@ int brx_pool_set_host_backing(brx_pool* p, const void* host_base, int64_t host_s
     }
     // nothing is resident yet: every entry starts as -1, "read from host"
     p->host = (const uint8_t*)host_base;
-    p->host_stride = host_stride;
     for (int e = 0; e < E; ++e) p->g2s_pinned[e] = -1;
     HIP_TRY(hipMemcpy(p->g2s_dev, p->g2s_pinned, sizeof(int32_t) * E, hipMemcpyHostToDevice));
     return BRX_OK;
@@ -395,7 +392,6 @@ static FwdArgs make_args(const brx_layer_desc* d, brx_pool* p, const void* x, in
     a.g2s = p->g2s_dev;
     a.capacity = p->capacity;
     a.host = p->host;
-    a.host_stride = p->host_stride;
     a.shared = (const uint8_t*)shared_expert;
     a.auto_shared = (token_mode && shared_expert) ? 1 : 0;
     a.lay = p->lay;

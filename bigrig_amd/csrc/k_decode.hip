@@ -414,7 +414,7 @@ __device__ __forceinline__ void stage_rows(const uint16_t* __restrict__ src, int
 template <int MODE, int UPL, int KP, bool MULTI>
 __global__ __launch_bounds__(kThreads) void k_dec_gateup(FwdArgs a, uint16_t* __restrict__ hbuf,
                                                          int hstride, DecTable* __restrict__ table,
-                                                         int lsp, int nu) {
+                                                         int lsp, int nu, int nby) {
     prefetch_args(a);
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     __shared__ int32_t s_e[kWave];   // P <= 64 pairs
@@ -516,8 +516,10 @@ __global__ __launch_bounds__(kThreads) void k_dec_gateup(FwdArgs a, uint16_t* __
         }
     } else {
         const int e_raw = lane < a.P ? s_e[lane] : 0;
-        // entries by, by + NB, ... (NB = gridDim.y); x is staged once, with the first entry
-        const int NB = gridDim.y;
+        // entries by, by + NB, ... (NB = the grid's rows, passed in so the kernel reads no
+        // hidden argument and its argument block stays under 512 bytes); x is staged once,
+        // with the first entry
+        const int NB = nby;
         bool staged = false;
         for (int u = blockIdx.y; u < nu; u += NB) {
             Entry en;
@@ -890,9 +892,9 @@ hipError_t launch_gateup(const FwdArgs& a, uint16_t* hbuf, DecTable* table, int 
 #define BRX_GU(KP)                                                                                     \
     do {                                                                                               \
         if (a.T > 1)                                                                                   \
-            hipLaunchKernelGGL((k_dec_gateup<MODE, UPL, KP, true>), grid, block, lds, s, a, hbuf, Imax, table, lsp, nu); \
+            hipLaunchKernelGGL((k_dec_gateup<MODE, UPL, KP, true>), grid, block, lds, s, a, hbuf, Imax, table, lsp, nu, (int)grid.y); \
         else                                                                                           \
-            hipLaunchKernelGGL((k_dec_gateup<MODE, UPL, KP, false>), grid, block, lds, s, a, hbuf, Imax, table, lsp, nu); \
+            hipLaunchKernelGGL((k_dec_gateup<MODE, UPL, KP, false>), grid, block, lds, s, a, hbuf, Imax, table, lsp, nu, (int)grid.y); \
     } while (0)
     if (!a.logits) BRX_GU(0);
     else if (a.E <= 64) BRX_GU(1);

@@ -142,9 +142,10 @@ int brx_pool_sync(brx_pool* p);
  *
  * Give the pool host backing: the layer's routed experts in pinned host memory, expert e at
  * host_base + e * host_stride (host_bytes in all), mapped at the same address on the device
- * (checked). Only on a fresh pool (no refill, table upload or forward yet); every table entry
- * starts at -1; the memory must outlive the pool's last forward. host_base and host_stride
- * must be multiples of 256. */
+ * (checked). host_stride must equal the pool's slot stride (bytes per expert rounded up to
+ * 256) and host_base be 256-byte aligned: a host expert is addressed exactly as a slot. Only on
+ * a fresh pool (no refill, table upload or forward yet); every table entry starts at -1; the
+ * memory must outlive the pool's last forward. */
 int brx_pool_set_host_backing(brx_pool* p, const void* host_base, int64_t host_stride,
                               size_t host_bytes);
 /* Set n table entries experts[i] -> slots[i] (slot -1: read from host backing) on `stream`, in
