@@ -609,27 +609,51 @@ void k_pf_gemm(FwdArgs a, const int32_t* __restrict__ order, const int32_t* __re
 }
 
 // ------------------------------------------------------------------ combine
+// V consecutive outputs of one token per thread (V = 8: 16-byte loads and stores, every
+// expert row's load issued before the sums; V = 2 when a pointer is not 16-byte aligned). Each
+// output is fma(w[t, j], y[t, j], acc) over j = 0 .. k - 1 in order, then the shared term,
+// whatever V is.
+template <int V>
 __global__ __launch_bounds__(kThreads) void k_combine(const uint16_t* __restrict__ y_routed,
                                                       const uint16_t* __restrict__ y_shared,
                                                       const float* __restrict__ w,
                                                       const float* __restrict__ sg, int T, int k,
                                                       int H, uint16_t* __restrict__ out) {
+    using VT = typename std::conditional<V == 8, uint4, uint32_t>::type;
+    constexpr int NW = V / 2;                      // 32-bit words per thread
+    constexpr int KB = 8;                          // expert rows in flight per thread
     const int t = blockIdx.y;
-    const int n = (blockIdx.x * kThreads + threadIdx.x) * 2;
+    const int n = (blockIdx.x * kThreads + threadIdx.x) * V;
     if (n >= H) return;
-    float a0 = 0.f, a1 = 0.f;
-    for (int j = 0; j < k; ++j) {
-        float wj = w[t * k + j];
-        uint32_t yv = *reinterpret_cast<const uint32_t*>(y_routed + ((int64_t)t * k + j) * H + n);
-        a0 = fmaf(wj, bf2f(yv & 0xFFFFu), a0);
-        a1 = fmaf(wj, bf2f(yv >> 16), a1);
+    float acc[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) acc[i] = 0.f;
+    auto add = [&](float wj, const VT& v) __attribute__((always_inline)) {
+        const uint32_t* q = reinterpret_cast<const uint32_t*>(&v);
+#pragma unroll
+        for (int i = 0; i < NW; ++i) {
+            acc[2 * i] = fmaf(wj, bf2f(q[i] & 0xFFFFu), acc[2 * i]);
+            acc[2 * i + 1] = fmaf(wj, bf2f(q[i] >> 16), acc[2 * i + 1]);
+        }
+    };
+    for (int j0 = 0; j0 < k; j0 += KB) {
+        VT v[KB];
+        float wj[KB];
+#pragma unroll
+        for (int u = 0; u < KB; ++u) {
+            const int j = min(j0 + u, k - 1);
+            v[u] = *reinterpret_cast<const VT*>(y_routed + ((int64_t)t * k + j) * H + n);
+            wj[u] = w[t * k + j];
+        }
+#pragma unroll
+        for (int u = 0; u < KB; ++u)
+            if (j0 + u < k) add(wj[u], v[u]);
     }
-    if (y_shared && sg) {
-        uint32_t yv = *reinterpret_cast<const uint32_t*>(y_shared + (int64_t)t * H + n);
-        a0 = fmaf(sg[t], bf2f(yv & 0xFFFFu), a0);
-        a1 = fmaf(sg[t], bf2f(yv >> 16), a1);
-    }
-    *reinterpret_cast<uint32_t*>(out + (int64_t)t * H + n) = f2bf(a0) | (f2bf(a1) << 16);
+    if (y_shared && sg) add(sg[t], *reinterpret_cast<const VT*>(y_shared + (int64_t)t * H + n));
+    uint32_t o[NW];
+#pragma unroll
+    for (int i = 0; i < NW; ++i) o[i] = f2bf(acc[2 * i]) | (f2bf(acc[2 * i + 1]) << 16);
+    *reinterpret_cast<VT*>(out + (int64_t)t * H + n) = *reinterpret_cast<const VT*>(o);
 }
 
 struct PfWs {
@@ -707,8 +731,13 @@ hipError_t launch_sort_pairs(const int32_t* pexp, int P, int E, int E_ext, int T
 
 hipError_t launch_combine(const uint16_t* y_routed, const uint16_t* y_shared, const float* w,
                           const float* sg, int T, int k, int H, uint16_t* out, hipStream_t s) {
-    hipLaunchKernelGGL(k_combine, dim3((H / 2 + kThreads - 1) / kThreads, T), dim3(kThreads), 0, s,
-                       y_routed, y_shared, w, sg, T, k, H, out);
+    // H is a multiple of 64, so 8 outputs a thread tile every row
+    if ((((uintptr_t)y_routed | (uintptr_t)y_shared | (uintptr_t)out) & 15) == 0)
+        hipLaunchKernelGGL(k_combine<8>, dim3((H / 8 + kThreads - 1) / kThreads, T), dim3(kThreads), 0, s,
+                           y_routed, y_shared, w, sg, T, k, H, out);
+    else
+        hipLaunchKernelGGL(k_combine<2>, dim3((H / 2 + kThreads - 1) / kThreads, T), dim3(kThreads), 0, s,
+                           y_routed, y_shared, w, sg, T, k, H, out);
     return hipGetLastError();
 }
 
