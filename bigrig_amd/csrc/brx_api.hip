@@ -233,6 +233,34 @@ int brx_pool_refill_async(brx_pool* p, int slot, const void* host_src, size_t nb
     return refill(p, slot, host_src, nbytes, copy_stream, hipMemcpyHostToDevice);
 }
 
+int brx_pool_refill_range_async(brx_pool* p, int slot0, int n, const void* host_src, int64_t host_stride,
+                                size_t nbytes, void* copy_stream) {
+    if (!p || !host_src) return fail(BRX_EINVAL, "pool or source is NULL");
+    if (n < 1 || slot0 < 0 || slot0 + n > p->capacity)
+        return fail(BRX_ERANGE, "slots [%d, %d) outside [0, %d)", slot0, slot0 + n, p->capacity);
+    if ((int64_t)nbytes != p->lay.bytes)
+        return fail(BRX_EINVAL, "the layout accounts for %lld bytes but the region supplied %zu. "
+                    "Refusing to write a partially-filled slot.", (long long)p->lay.bytes, nbytes);
+    if (host_stride < (int64_t)nbytes) return fail(BRX_EINVAL, "host stride %lld is below the expert size", (long long)host_stride);
+    hipStream_t cs = (hipStream_t)copy_stream;
+    if (p->read_recorded) HIP_TRY(hipStreamWaitEvent(cs, p->last_read, 0));
+    uint8_t* dst = p->slots + (int64_t)slot0 * p->stride;
+    const uint8_t* src = (const uint8_t*)host_src;
+    if (host_stride == p->stride && p->stride == p->lay.bytes) {
+        // the experts are back to back on both sides: one transfer (a single DMA stream moves
+        // ~40% more per second than one copy per expert)
+        HIP_TRY(hipMemcpyAsync(dst, src, (size_t)n * nbytes, hipMemcpyHostToDevice, cs));
+    } else {
+        for (int i = 0; i < n; ++i)
+            HIP_TRY(hipMemcpyAsync(dst + (int64_t)i * p->stride, src + (int64_t)i * host_stride, nbytes,
+                                   hipMemcpyHostToDevice, cs));
+    }
+    HIP_TRY(hipEventRecord(p->refill_done, cs));
+    p->refill_pending = true;
+    p->refill_recorded = true;
+    return BRX_OK;
+}
+
 int brx_pool_refill_from_device_async(brx_pool* p, int slot, const void* dev_src, size_t nbytes,
                                       void* copy_stream) {
     return refill(p, slot, dev_src, nbytes, copy_stream, hipMemcpyDeviceToDevice);

@@ -73,8 +73,10 @@ class LayerRing:
         if store.tensor(layer).shape[0] != E:
             raise ValueError(f"layer {layer} has {store.tensor(layer).shape[0]} experts in the "
                              f"store, the ring holds {E}")
-        for e in range(E):
-            self.bytes_loaded += s.device.write(e, store.region(layer, e))
+        t = store.tensor(layer)
+        per = int(t.shape[1])
+        # expert e into slot e: the whole layer in one transfer
+        self.bytes_loaded += s.device.write_range(0, t.data_ptr(), E, per, per)
         s.layer = layer
         return s
 

@@ -190,6 +190,15 @@ class DeviceSlots:
         self._stage_ev.record(self.copy_stream)
         return raw.nbytes
 
+    def write_range(self, slot0: int, host_ptr: int, n: int, host_stride: int, nbytes: int) -> int:
+        """Queue the copies of n experts in pinned host memory (expert i at host_ptr + i *
+        host_stride) into slots slot0 .. slot0 + n - 1, one transfer when they are back to back
+        on both sides; returns the bytes copied."""
+        L = self._L
+        L.check(L.load().brx_pool_refill_range_async(self.handle, slot0, n, host_ptr, host_stride,
+                                                     nbytes, self.copy_stream.cuda_stream))
+        return n * nbytes
+
     def write_device(self, slot: int, dev_ptr: int, nbytes: int, src_stream=None) -> int:
         """Queue the copy of an expert staged in device memory into `slot`. The source is
         written by work on `src_stream` (default: the current stream), so the copy stream

@@ -122,6 +122,13 @@ int brx_pool_g2s_ptr(brx_pool* p, int32_t** out);
  * Replaces the slot write of admit_arrays (stream.py:765-769). */
 int brx_pool_refill_async(brx_pool* p, int slot, const void* host_src, size_t nbytes,
                           void* copy_stream);
+/* n experts into slots slot0 .. slot0 + n - 1 from pinned host memory, expert i at
+ * host_src + i * host_stride (nbytes = bytes_per_expert each), ordered as brx_pool_refill_async.
+ * When both sides hold the experts back to back (host_stride = slot stride = nbytes) it is one
+ * transfer. The reference reads a layer's experts ahead one by one (StreamHandle.read_ahead,
+ * stream.py:2009-2034); a whole layer arriving at once is this call. */
+int brx_pool_refill_range_async(brx_pool* p, int slot0, int n, const void* host_src,
+                                int64_t host_stride, size_t nbytes, void* copy_stream);
 /* Same, from device memory (a staged expert, stream.py:957-961). */
 int brx_pool_refill_from_device_async(brx_pool* p, int slot, const void* dev_src, size_t nbytes,
                                       void* copy_stream);

@@ -124,3 +124,40 @@ def test_pool_slots_hold_the_admitted_bytes(gpu):
             got = out.cpu().numpy()
             assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (slot, e, p)
     pool.close()
+
+
+def test_refill_range_lands_every_expert(gpu):
+    """brx_pool_refill_range_async: one transfer when the experts are back to back on both
+    sides, one copy per expert otherwise (a padded host stride); every slot then holds its
+    expert's bytes, and a bad range is refused before anything is copied."""
+    import ctypes as C
+
+    import torch
+
+    from bigrig_amd import lib as L
+    from bigrig_amd.pool import ExpertPool
+    spec = F16
+    per = spec.bytes_per_expert
+    E = spec.n_experts
+    rng = np.random.default_rng(5)
+    src = rng.integers(0, 256, (E, per), dtype=np.uint8)
+    hip = C.CDLL("libamdhip64.so")
+    hip.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+    for pad in (0, 512):
+        host = torch.empty((E, per + pad), dtype=torch.uint8, pin_memory=True)
+        host.numpy()[:, :per] = src
+        pool = ExpertPool(0, spec, E).build()
+        n = pool.device.write_range(0, host.data_ptr(), E, per + pad, per)
+        assert n == E * per
+        pool.device.sync()
+        for e in (0, 1, E // 2, E - 1):
+            out = (C.c_uint8 * per)()
+            assert hip.hipMemcpy(out, C.c_void_p(pool.device.slot_ptr(e)), per, 2) == 0
+            assert bytes(out) == src[e].tobytes(), (pad, e)
+        lib = L.load()
+        s = torch.cuda.current_stream().cuda_stream
+        assert lib.brx_pool_refill_range_async(pool.device.handle, 1, E, host.data_ptr(),
+                                               per + pad, per, s) != 0       # past the pool
+        assert lib.brx_pool_refill_range_async(pool.device.handle, 0, 2, host.data_ptr(),
+                                               per + pad, per - 1, s) != 0   # wrong size
+        pool.close()
