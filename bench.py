@@ -619,7 +619,7 @@ def cpu_bench(args, st: "Stack"):
 def main():
     args = parse()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU: this build has no multi-GPU path (got --gpus "
+        print(f"bench.py measures one GPU: the library has no multi-GPU path (got --gpus "
               f"{args.gpus}). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
     import torch

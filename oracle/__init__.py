@@ -1,7 +1,8 @@
 """ORACLE -- test infrastructure only; the product never imports this package.
 
 Only tests/, the smoke check in __graft_entry__.py and bench.py's CPU-baseline leg use it, and
-only as the checker (or the timed CPU baseline), never as a code path of the product.
+only as the reference result to compare against (or the timed CPU baseline), never as a code
+path of the product.
 
 Two restatements of the reference's routed-expert layer (the reference computes it through MLX,
 which cannot run here; see moe_oracle.c for the file:line each function follows):
