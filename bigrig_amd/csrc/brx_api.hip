@@ -50,6 +50,11 @@ int check_desc(const brx_layer_desc* d) {
         return fail(BRX_EINVAL, "hidden %d must be a positive multiple of 64", d->hidden);
     if (d->inter <= 0 || d->inter % 64)
         return fail(BRX_EINVAL, "inter %d must be a positive multiple of 64", d->inter);
+    // the decode kernels stage 8 token rows of x (and h rows) in LDS and split a weight row over
+    // at most 256 lanes x 4 units; the router loops over any width
+    if (d->hidden > kMaxWidth || d->inter > kMaxWidth || d->shared_inter > kMaxWidth)
+        return fail(BRX_EINVAL, "hidden %d, inter %d and shared_inter %d must be at most %d", d->hidden,
+                    d->inter, d->shared_inter, kMaxWidth);
     if (d->n_experts < 1 || d->n_experts > 512)
         return fail(BRX_EINVAL, "n_experts %d outside [1, 512]", d->n_experts);
     if (d->top_k < 1 || d->top_k > d->n_experts || d->top_k > 64)
@@ -74,8 +79,6 @@ int check_desc(const brx_layer_desc* d) {
         return fail(BRX_EINVAL, "router_dtype %d unknown", d->router_dtype);
     if (d->shared_inter < 0 || d->shared_inter % 64)
         return fail(BRX_EINVAL, "shared_inter %d must be 0 or a multiple of 64", d->shared_inter);
-    if (d->shared_inter && d->shared_inter != d->inter)
-        return fail(BRX_EINVAL, "shared_inter %d must equal inter %d", d->shared_inter, d->inter);
     return BRX_OK;
 }
 
@@ -109,6 +112,8 @@ struct brx_pool {
     uint8_t* slots;
     int32_t* g2s_dev;
     int32_t* g2s_pinned;
+    int32_t* err_dev;           // {flag, expert}: a forward met an expert that was not resident
+    int resident;               // table entries >= 0 as last uploaded (pools without host backing)
     hipEvent_t last_read;
     hipEvent_t refill_done;
     hipEvent_t g2s_uploaded;
@@ -172,7 +177,10 @@ int brx_pool_create(const brx_layer_desc* d, int capacity, brx_pool** out) {
         return fail(BRX_ENOMEM, "%d slots of %lld bytes: %s", capacity, (long long)p->stride, hipGetErrorString(e));
     }
     e = hipMalloc(&p->g2s_dev, sizeof(int32_t) * d->n_experts);
-    if (e == hipSuccess) e = hipMemset(p->g2s_dev, 0, sizeof(int32_t) * d->n_experts);
+    // every expert starts absent (-1)
+    if (e == hipSuccess) e = hipMemset(p->g2s_dev, 0xFF, sizeof(int32_t) * d->n_experts);
+    if (e == hipSuccess) e = hipMalloc(&p->err_dev, 2 * sizeof(int32_t));
+    if (e == hipSuccess) e = hipMemset(p->err_dev, 0, 2 * sizeof(int32_t));
     if (e == hipSuccess) e = hipHostMalloc(&p->g2s_pinned, sizeof(int32_t) * d->n_experts, hipHostMallocDefault);
     if (e == hipSuccess) e = hipEventCreateWithFlags(&p->last_read, hipEventDisableTiming);
     if (e == hipSuccess) e = hipEventCreateWithFlags(&p->refill_done, hipEventDisableTiming);
@@ -190,6 +198,7 @@ int brx_pool_destroy(brx_pool* p) {
     (void)hipDeviceSynchronize();
     if (p->slots) (void)hipFree(p->slots);
     if (p->g2s_dev) (void)hipFree(p->g2s_dev);
+    if (p->err_dev) (void)hipFree(p->err_dev);
     if (p->g2s_pinned) (void)hipHostFree(p->g2s_pinned);
     if (p->last_read) (void)hipEventDestroy(p->last_read);
     if (p->refill_done) (void)hipEventDestroy(p->refill_done);
@@ -275,8 +284,14 @@ int brx_pool_set_g2s(brx_pool* p, const int32_t* g2s_host, int n, void* stream) 
     hipStream_t s = (hipStream_t)stream;
     // the staging copy of the previous upload must have been consumed before it is rewritten
     if (p->g2s_recorded) HIP_TRY(hipEventSynchronize(p->g2s_uploaded));
-    // -1 (absent) stays -1 when the kernels can serve the expert from host backing
-    for (int e = 0; e < n; ++e) p->g2s_pinned[e] = g2s_host[e] >= 0 ? g2s_host[e] : (p->host ? -1 : 0);
+    // -1 stays -1 (absent): with host backing the kernels read the expert from host memory,
+    // without it a forward that routes to it records the error and writes NaN rows
+    int resident = 0;
+    for (int e = 0; e < n; ++e) {
+        p->g2s_pinned[e] = g2s_host[e] >= 0 ? g2s_host[e] : -1;
+        resident += g2s_host[e] >= 0 ? 1 : 0;
+    }
+    p->resident = resident;
     HIP_TRY(hipMemcpyAsync(p->g2s_dev, p->g2s_pinned, sizeof(int32_t) * n, hipMemcpyHostToDevice, s));
     HIP_TRY(hipEventRecord(p->g2s_uploaded, s));
     p->g2s_recorded = true;
@@ -381,6 +396,20 @@ int brx_pool_sync(brx_pool* p) {
     return BRX_OK;
 }
 
+int brx_pool_check(brx_pool* p) {
+    if (!p) return fail(BRX_EINVAL, "pool is NULL");
+    int rc = brx_pool_sync(p);
+    if (rc) return rc;
+    int32_t h[2] = {0, 0};
+    HIP_TRY(hipMemcpy(h, p->err_dev, sizeof h, hipMemcpyDeviceToHost));
+    if (h[0]) {
+        HIP_TRY(hipMemset(p->err_dev, 0, sizeof h));
+        return fail(BRX_ERANGE, "a forward routed to expert %d, which is neither in a slot nor host-backed; "
+                    "the rows it touched were written as NaN", h[1]);
+    }
+    return BRX_OK;
+}
+
 int brx_router_topk(const brx_layer_desc* d, const void* x, const void* w_router, const float* bias,
                     const void* shared_gate_w, int T, int32_t* out_idx, float* out_w,
                     float* out_shared_gate, void* stream) {
@@ -432,6 +461,7 @@ static FwdArgs make_args(const brx_layer_desc* d, brx_pool* p, const void* x, in
     a.yun = (uint16_t*)y_rows;
     a.yrows = yrows;
     a.route_mode = d->route_mode;
+    a.err = p->err_dev;
     return a;
 }
 
@@ -460,7 +490,8 @@ static int forward_impl(const brx_layer_desc* d, brx_pool* p, const void* x, int
     const bool force_dec = flags & BRX_FWD_FORCE_DECODE, force_pf = flags & BRX_FWD_FORCE_PREFILL;
     if (force_dec && force_pf) return fail(BRX_EINVAL, "FORCE_DECODE and FORCE_PREFILL are exclusive");
     const bool token_mode = ptok == nullptr;
-    bool decode = force_dec || (!force_pf && (token_mode ? T <= 8 : P <= 8));
+    // the decode kernels stage every token row of x and plan at most 64 pairs
+    bool decode = force_dec || (!force_pf && T <= 8 && P <= (token_mode ? 64 : 8));
     if (decode && (T > 8 || P > 64))
         return fail(BRX_EINVAL, "the decode path takes at most 8 token rows and 64 pairs (T=%d, P=%d)", T, P);
     FwdArgs a = make_args(d, p, x, T, P, pexp, ptok, prow, yrows, w, shared_expert, shared_gate, out, y_rows);
@@ -544,9 +575,17 @@ int brx_moe_block_forward(const brx_layer_desc* d, brx_pool* p, const void* x, c
     const unsigned phase_bits = flags & (BRX_FWD_PHASE_R | BRX_FWD_PHASE_A | BRX_FWD_PHASE_B);
     const bool do_route = !phase_bits || (flags & BRX_FWD_PHASE_R);
     int phases = phase_bits ? (int)((flags & (BRX_FWD_PHASE_A | BRX_FWD_PHASE_B)) >> 2) : 3;
-    const bool decode = force_dec || (!force_pf && T <= 8);
-    if (decode && T > 8) return fail(BRX_EINVAL, "the decode path takes at most 8 tokens (T=%d)", T);
     const int k = d->top_k, P = T * k;
+    // the decode kernels rank and plan at most 64 (token, expert) pairs in one wave
+    const bool decode = force_dec || (!force_pf && T <= 8 && P <= 64);
+    if (decode && (T > 8 || P > 64))
+        return fail(BRX_EINVAL, "the decode path takes at most 8 tokens and 64 pairs (T=%d, top_k=%d)", T, k);
+    // the block reads the table for every expert the router may pick: all must be resident, or
+    // served from host backing (the reference raises KeyError for a non-resident expert,
+    // stream.py:608-615)
+    if (!p->host && p->resident < d->n_experts)
+        return fail(BRX_ESTATE, "brx_moe_block_forward needs every expert resident or a host-backed pool "
+                    "(%d of %d experts resident)", p->resident, d->n_experts);
     hipStream_t s = (hipStream_t)stream;
 
     // one workspace for the whole block: routing first, then the expert kernels' scratch
@@ -560,6 +599,7 @@ int brx_moe_block_forward(const brx_layer_desc* d, brx_pool* p, const void* x, c
     const size_t fwd_b = decode ? decode_workspace_bytes(a) : prefill_workspace_bytes(a);
     void* ws = nullptr;
     if ((rc = ws_reserve(route_b + fwd_b, s, &ws))) return rc;
+    const size_t ws_bytes = g_ws.bytes;
     char* base = (char*)ws;
     float* logits = (float*)base;
     int32_t* ridx = out_idx ? out_idx : (int32_t*)(base + logits_b);
@@ -581,7 +621,7 @@ int brx_moe_block_forward(const brx_layer_desc* d, brx_pool* p, const void* x, c
     }
     if (e != hipSuccess) return hip_fail(e, "router launch");
     if (!phases) return BRX_OK;
-    return run_forward(p, a, decode, phases, fws, g_ws.bytes - route_b, s);
+    return run_forward(p, a, decode, phases, fws, ws_bytes - route_b, s);
 }
 
 int brx_combine(const brx_layer_desc* d, const void* y_routed, const float* w, const void* y_shared,

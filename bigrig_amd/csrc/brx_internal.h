@@ -10,6 +10,7 @@ namespace brx {
 
 constexpr int kWave = 64;
 constexpr int kMaxTableEdits = 32;   // table entries one brx_pool_publish_async launch sets
+constexpr int kMaxWidth = 8192;      // largest hidden / intermediate width the kernels take
 
 // ------------------------------------------------------------------ layout (host + device)
 struct Proj {
@@ -73,6 +74,7 @@ struct FwdArgs {
     int32_t* route_idx;         // [T, k]
     float* route_w;             // [T, k]
     float* route_sg;            // [T] or null
+    int32_t* err;               // the pool's error word {flag, expert} (device), or null
     Layout lay;                 // routed expert layout
     Layout lay_sh;              // shared expert layout
     int32_t P;                  // routed (token, expert) pairs
@@ -95,25 +97,38 @@ __device__ __forceinline__ int pair_row(const FwdArgs& a, int p) {
     return a.prow ? min(max(a.prow[p], 0), a.yrows - 1) : p;
 }
 
-// Where an expert's bytes are read from, as one int "slot code": c >= 0 pool slot c; c == -1
-// the shared expert; c <= -2 routed expert -2 - c read straight from the pool's host backing
-// (pinned host memory the GPU reads over the bus), which a table entry < 0 selects when the
-// pool has one. Without host backing a negative entry is clamped to slot 0, so a bad table
-// computes wrong rows rather than reading out of bounds.
-__device__ __forceinline__ int slot_code(const FwdArgs& a, int e, int v) {
-    return (v < 0 && a.host) ? -2 - e : min(max(v, 0), a.capacity - 1);
+// Where an expert's bytes are read from, as one int "slot code": 0 <= c < capacity pool slot
+// c; c == -1 the shared expert; c <= -2 routed expert -2 - c read straight from the pool's host
+// backing (pinned host memory the GPU reads over the bus), which a table entry < 0 selects when
+// the pool has one; kAbsentCode an expert that is neither in a slot nor host-backed. An absent
+// expert is never computed as if it were another: the pool's error word records it (the host
+// reports it as BRX_ERANGE), its bytes are read from the last slot only so every address stays
+// in bounds, and the activations of its rows are written as NaN, so every output it touches
+// is NaN rather than a plausible wrong value.
+constexpr int kAbsentCode = 0x40000000;
+__device__ __forceinline__ void note_absent(const FwdArgs& a, int e) {
+    if (a.err) {
+        a.err[1] = e;
+        a.err[0] = 1;
+    }
 }
-// A code read back from the library's own tables, clamped into what the arguments allow.
+__device__ __forceinline__ int slot_code(const FwdArgs& a, int e, int v) {
+    if (v >= 0) return min(v, a.capacity - 1);
+    return a.host ? -2 - e : kAbsentCode;
+}
+// A code read back from the library's own tables, clamped into what the arguments allow
+// (kAbsentCode stays as it is: code_base keeps its reads in bounds).
 __device__ __forceinline__ int clamp_code(const FwdArgs& a, int c) {
     if (c == -1) return a.shared ? -1 : 0;
     if (c < -1) return a.host ? max(c, -1 - a.E) : 0;
-    return min(c, a.capacity - 1);
+    return c == kAbsentCode ? c : min(c, a.capacity - 1);
 }
 __device__ __forceinline__ const uint8_t* code_base(const FwdArgs& a, int c) {
-    if (c >= 0) return a.slots + (int64_t)c * a.slot_stride;
+    if (c >= 0) return a.slots + (int64_t)min(c, a.capacity - 1) * a.slot_stride;
     if (c == -1) return a.shared;
     return a.host + (int64_t)(-2 - c) * a.slot_stride;
 }
+__device__ __forceinline__ float absent_nan() { return __uint_as_float(0x7fc00000u); }
 
 // ------------------------------------------------------------------ device helpers
 __device__ __forceinline__ float bf2f(uint32_t b16) { return __uint_as_float(b16 << 16); }

@@ -93,6 +93,7 @@ __device__ __forceinline__ bool plan_entry(const FwdArgs& a, int u, int e_raw, c
         en.shared = false;
         int s = -1;
         if (eu < a.E) s = slot_code(a, eu, s_g2s[eu]);
+        if (s == kAbsentCode && lane == 0) note_absent(a, eu);
         en.slot = s;
     } else {
         en.e = a.E;
@@ -510,7 +511,7 @@ __global__ __launch_bounds__(kThreads) void k_dec_gateup(FwdArgs a, uint16_t* __
             pg = group_sum(pg, SP);
             pu = group_sum(pu, SP);
             if (sl == 0 && r0 + rr < inter) {
-                const float h = act_apply(a.act, pg + bg, pu + bu, a.alpha, a.limit);
+                const float h = en.slot == kAbsentCode ? absent_nan() : act_apply(a.act, pg + bg, pu + bu, a.alpha, a.limit);
                 hbuf[(int64_t)pair * hstride + r0 + rr] = (uint16_t)f2bf(h);
             }
         }
@@ -585,7 +586,8 @@ __global__ __launch_bounds__(kThreads) void k_dec_gateup(FwdArgs a, uint16_t* __
                 pg = group_sum(pg, SP);
                 pu = group_sum(pu, SP);
                 if (sl == 0 && r0 + rr < inter) {
-                    const float h = act_apply(a.act, pg + bg, pu + bu, a.alpha, a.limit);
+                    const float h = en.slot == kAbsentCode ? absent_nan()
+                                                           : act_apply(a.act, pg + bg, pu + bu, a.alpha, a.limit);
                     hbuf[(int64_t)pair * hstride + r0 + rr] = (uint16_t)f2bf(h);
                 }
             }

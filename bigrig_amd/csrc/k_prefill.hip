@@ -58,7 +58,7 @@ __device__ __forceinline__ int bucket_expert(const int32_t* __restrict__ pexp, i
 __global__ __launch_bounds__(kBucketThreads) void k_bucket(const int32_t* __restrict__ pexp, int P, int E,
                                                            int E_ext, int T_sh, int BM,
                                                            const int32_t* __restrict__ g2s, int capacity,
-                                                           int host,
+                                                           int host, int32_t* __restrict__ err,
                                                            int32_t* __restrict__ order,
                                                            int32_t* __restrict__ offsets,
                                                            int32_t* __restrict__ tile_start,
@@ -121,9 +121,13 @@ __global__ __launch_bounds__(kBucketThreads) void k_bucket(const int32_t* __rest
     if (tinfo) {
         const int n = hist[e], off = base_s[0], big = base_s[1], small = base_s[2];
         int slot = 0;
-        if (e < E && g2s) {   // the slot code: a slot, or -2 - e for an expert read from host backing
+        if (e < E && g2s) {   // the slot code: a slot, -2 - e for an expert read from host backing
             const int v = g2s[e];
-            slot = (v < 0 && host) ? -2 - e : min(max(v, 0), capacity - 1);
+            slot = v >= 0 ? min(v, capacity - 1) : (host ? -2 - e : kAbsentCode);
+            if (slot == kAbsentCode && n > 0 && tid == 0 && err) {
+                err[1] = e;
+                err[0] = 1;
+            }
         }
         for (int j = tid; j * BM < n; j += kBucketThreads) {
             const int rows = min(BM, n - j * BM);
@@ -538,7 +542,8 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
             for (int mi = 0; mi < MR; ++mi) {
 #pragma unroll
                 for (int i = 0; i < 16; ++i) {
-                    const float h = act_apply(a.act, acc[mi][0][i] + bg, acc[mi][1][i] + bu, a.alpha, a.limit);
+                    const float h = slot == kAbsentCode
+                        ? absent_nan() : act_apply(a.act, acc[mi][0][i] + bg, acc[mi][1][i] + bu, a.alpha, a.limit);
                     T[(mi * 32 + 8 * (i >> 2) + 4 * kh + (i & 3)) * TS + fl] = __builtin_bit_cast(uint16_t, (__bf16)h);
                 }
             }
@@ -713,10 +718,10 @@ hipError_t launch_gemm(const FwdArgs& a, const PfWs& w, int E_ext, int Imax, uin
 }
 
 hipError_t launch_bucket(const int32_t* pexp, int P, int E, int E_ext, int T_sh, int BM,
-                         const int32_t* g2s, int capacity, int host, int32_t* order, int32_t* offsets,
-                         int32_t* tile_start, int4* tinfo, hipStream_t s) {
+                         const int32_t* g2s, int capacity, int host, int32_t* err, int32_t* order,
+                         int32_t* offsets, int32_t* tile_start, int4* tinfo, hipStream_t s) {
     hipLaunchKernelGGL(k_bucket, dim3(E_ext), dim3(kBucketThreads), sizeof(int32_t) * E_ext, s, pexp, P, E,
-                       E_ext, T_sh, BM, g2s, capacity, host, order, offsets, tile_start, tinfo);
+                       E_ext, T_sh, BM, g2s, capacity, host, err, order, offsets, tile_start, tinfo);
     return hipGetLastError();
 }
 
@@ -726,7 +731,8 @@ size_t prefill_workspace_bytes(const FwdArgs& a) { return carve(a, nullptr).byte
 
 hipError_t launch_sort_pairs(const int32_t* pexp, int P, int E, int E_ext, int T_sh, int BM,
                              int32_t* order, int32_t* offsets, int32_t* tile_start, hipStream_t s) {
-    return launch_bucket(pexp, P, E, E_ext, T_sh, BM, nullptr, 1, 0, order, offsets, tile_start, nullptr, s);
+    return launch_bucket(pexp, P, E, E_ext, T_sh, BM, nullptr, 1, 0, nullptr, order, offsets, tile_start, nullptr,
+                         s);
 }
 
 hipError_t launch_combine(const uint16_t* y_routed, const uint16_t* y_shared, const float* w,
@@ -754,7 +760,7 @@ hipError_t launch_prefill(const FwdArgs& a, void* ws, size_t ws_bytes, int phase
     uint16_t* y_routed = a.yun ? a.yun : w.y_routed;
     hipError_t err = hipSuccess;
     if (phases & 1) {
-        err = launch_bucket(a.pexp, P, a.E, E_ext, T_sh, kBM, a.g2s, a.capacity, a.host != nullptr, w.order, w.offsets,
+        err = launch_bucket(a.pexp, P, a.E, E_ext, T_sh, kBM, a.g2s, a.capacity, a.host != nullptr, a.err, w.order, w.offsets,
                             w.tile_start, w.tinfo, s);
         if (err != hipSuccess) return err;
     }

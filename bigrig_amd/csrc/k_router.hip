@@ -38,7 +38,7 @@ __global__ __launch_bounds__(kRouterThreads) void k_router_tiled(
     const uint16_t* __restrict__ x, const void* __restrict__ w, const float* __restrict__ bias,
     const uint16_t* __restrict__ sgw, int T, int H, int E, int rows_per_block, float* __restrict__ logits) {
     static_assert(TT == 16, "the exchange pattern below is written for 16 tokens");
-    constexpr int kNJ = 6;                      // chunks per lane: H <= 64 * 8 * 6 = 3072
+    constexpr int kNJ = 6;                      // chunks per lane per pass (one pass: H <= 3072)
     constexpr int RW = WF32 ? 2 : 4;            // rows a wave works on at once (sharing x)
     extern __shared__ uint4 xs4[];              // [TT][H / 8] chunks of 8 bf16
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -57,67 +57,71 @@ __global__ __launch_bounds__(kRouterThreads) void k_router_tiled(
     for (int r0 = blockIdx.y * rows_per_block + wv * RW; r0 < r_end; r0 += kWaves * RW) {
         // the wave's rows r0, r0 + 1 (a row past the block's range repeats the last one and is
         // not stored)
-        uint4 wv4[RW][kNJ][2];
-        bool wf32[RW];
-#pragma unroll
-        for (int rr = 0; rr < RW; ++rr) {
-            const int r = min(r0 + rr, r_end - 1);
-            wf32[rr] = WF32 && r < E;
-#pragma unroll
-            for (int j = 0; j < kNJ; ++j) {
-                const int c = min(lane + kWave * j, nch - 1);
-                if (wf32[rr]) {
-                    const uint4* p = reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(w) + (int64_t)r * H + 8 * c);
-                    wv4[rr][j][0] = p[0];
-                    wv4[rr][j][1] = p[1];
-                } else {
-                    const uint16_t* src = r < E ? reinterpret_cast<const uint16_t*>(w) + (int64_t)r * H : sgw;
-                    wv4[rr][j][0] = *reinterpret_cast<const uint4*>(src + 8 * c);
-                    wv4[rr][j][1] = make_uint4(0, 0, 0, 0);
-                }
-            }
-        }
         float acc[RW][TT];
 #pragma unroll
         for (int rr = 0; rr < RW; ++rr)
 #pragma unroll
             for (int t = 0; t < TT; ++t) acc[rr][t] = 0.0f;
+        bool wf32[RW];
 #pragma unroll
-        for (int j = 0; j < kNJ; ++j) {
-            const int c = lane + kWave * j;
-            if (c >= nch) continue;
-            float wf[RW][8];
+        for (int rr = 0; rr < RW; ++rr) wf32[rr] = WF32 && min(r0 + rr, r_end - 1) < E;
+        // passes of kNJ chunks per lane continue each lane's chain in chunk order
+        for (int jb = 0; jb < nch; jb += kWave * kNJ) {
+            uint4 wv4[RW][kNJ][2];
 #pragma unroll
             for (int rr = 0; rr < RW; ++rr) {
-                if (wf32[rr]) {
-                    wf[rr][0] = __uint_as_float(wv4[rr][j][0].x); wf[rr][1] = __uint_as_float(wv4[rr][j][0].y);
-                    wf[rr][2] = __uint_as_float(wv4[rr][j][0].z); wf[rr][3] = __uint_as_float(wv4[rr][j][0].w);
-                    wf[rr][4] = __uint_as_float(wv4[rr][j][1].x); wf[rr][5] = __uint_as_float(wv4[rr][j][1].y);
-                    wf[rr][6] = __uint_as_float(wv4[rr][j][1].z); wf[rr][7] = __uint_as_float(wv4[rr][j][1].w);
-                } else {
-                    const uint32_t ww[4] = {wv4[rr][j][0].x, wv4[rr][j][0].y, wv4[rr][j][0].z, wv4[rr][j][0].w};
+                const int r = min(r0 + rr, r_end - 1);
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        wf[rr][2 * i] = bf2f(ww[i] & 0xFFFFu);
-                        wf[rr][2 * i + 1] = bf2f(ww[i] >> 16);
+                for (int j = 0; j < kNJ; ++j) {
+                    const int c = min(jb + lane + kWave * j, nch - 1);
+                    if (wf32[rr]) {
+                        const uint4* p = reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(w) + (int64_t)r * H + 8 * c);
+                        wv4[rr][j][0] = p[0];
+                        wv4[rr][j][1] = p[1];
+                    } else {
+                        const uint16_t* src = r < E ? reinterpret_cast<const uint16_t*>(w) + (int64_t)r * H : sgw;
+                        wv4[rr][j][0] = *reinterpret_cast<const uint4*>(src + 8 * c);
+                        wv4[rr][j][1] = make_uint4(0, 0, 0, 0);
                     }
                 }
             }
-            // one conversion of the token's 8 activations serves every row of the wave
 #pragma unroll
-            for (int t = 0; t < TT; ++t) {
-                const uint4 xv = xs4[t * nch + c];
-                const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
-                float xf[8];
+            for (int j = 0; j < kNJ; ++j) {
+                const int c = jb + lane + kWave * j;
+                if (c >= nch) continue;
+                float wf[RW][8];
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    xf[2 * i] = bf2f(xw[i] & 0xFFFFu);
-                    xf[2 * i + 1] = bf2f(xw[i] >> 16);
+                for (int rr = 0; rr < RW; ++rr) {
+                    if (wf32[rr]) {
+                        wf[rr][0] = __uint_as_float(wv4[rr][j][0].x); wf[rr][1] = __uint_as_float(wv4[rr][j][0].y);
+                        wf[rr][2] = __uint_as_float(wv4[rr][j][0].z); wf[rr][3] = __uint_as_float(wv4[rr][j][0].w);
+                        wf[rr][4] = __uint_as_float(wv4[rr][j][1].x); wf[rr][5] = __uint_as_float(wv4[rr][j][1].y);
+                        wf[rr][6] = __uint_as_float(wv4[rr][j][1].z); wf[rr][7] = __uint_as_float(wv4[rr][j][1].w);
+                    } else {
+                        const uint32_t ww[4] = {wv4[rr][j][0].x, wv4[rr][j][0].y, wv4[rr][j][0].z, wv4[rr][j][0].w};
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            wf[rr][2 * i] = bf2f(ww[i] & 0xFFFFu);
+                            wf[rr][2 * i + 1] = bf2f(ww[i] >> 16);
+                        }
+                    }
                 }
+                // one conversion of the token's 8 activations serves every row of the wave
 #pragma unroll
-                for (int rr = 0; rr < RW; ++rr)
+                for (int t = 0; t < TT; ++t) {
+                    const uint4 xv = xs4[t * nch + c];
+                    const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
+                    float xf[8];
 #pragma unroll
-                    for (int i = 0; i < 8; ++i) acc[rr][t] = fmaf(xf[i], wf[rr][i], acc[rr][t]);
+                    for (int i = 0; i < 4; ++i) {
+                        xf[2 * i] = bf2f(xw[i] & 0xFFFFu);
+                        xf[2 * i + 1] = bf2f(xw[i] >> 16);
+                    }
+#pragma unroll
+                    for (int rr = 0; rr < RW; ++rr)
+#pragma unroll
+                        for (int i = 0; i < 8; ++i) acc[rr][t] = fmaf(xf[i], wf[rr][i], acc[rr][t]);
+                }
             }
         }
 #pragma unroll
@@ -163,7 +167,7 @@ template <bool WF32, int TT, int WPB>
 __global__ __launch_bounds__(WPB * kWave) void k_router_logits(
     const uint16_t* __restrict__ x, const void* __restrict__ w, const float* __restrict__ bias,
     const uint16_t* __restrict__ sgw, int T, int H, int E, float* __restrict__ logits) {
-    constexpr int kNJ = 6;                      // chunks per lane: H <= 64 * 8 * 6 = 3072
+    constexpr int kNJ = 6;                      // chunks per lane per pass (one pass: H <= 3072)
     const int lane = threadIdx.x & 63;
     const int r = blockIdx.x * WPB + (threadIdx.x >> 6);
     const int rows = E + (sgw ? 1 : 0);
@@ -172,56 +176,65 @@ __global__ __launch_bounds__(WPB * kWave) void k_router_logits(
     const int nch = H / 8;
     if (r >= rows) return;
     const bool wf32 = WF32 && r < E;
-    uint4 wv[kNJ][2];
-    uint4 xv[TT][kNJ];
+    float acc[TT];
 #pragma unroll
-    for (int j = 0; j < kNJ; ++j) {
-        const int c = lane + kWave * j;
-        if (c < nch) {
-            if (wf32) {
-                const uint4* p = reinterpret_cast<const uint4*>(
-                    reinterpret_cast<const float*>(w) + (int64_t)r * H + 8 * c);
-                wv[j][0] = p[0];
-                wv[j][1] = p[1];
-            } else {
-                const uint16_t* src = r < E ? reinterpret_cast<const uint16_t*>(w) + (int64_t)r * H : sgw;
-                wv[j][0] = *reinterpret_cast<const uint4*>(src + 8 * c);
+    for (int t = 0; t < TT; ++t) acc[t] = 0.0f;
+    // passes of kNJ chunks per lane continue each lane's chain in chunk order; every load of a
+    // pass is issued before its first FMA
+    for (int jb = 0; jb < nch; jb += kWave * kNJ) {
+        uint4 wv[kNJ][2];
+        uint4 xv[TT][kNJ];
+#pragma unroll
+        for (int j = 0; j < kNJ; ++j) {
+            const int c = jb + lane + kWave * j;
+            if (c < nch) {
+                if (wf32) {
+                    const uint4* p = reinterpret_cast<const uint4*>(
+                        reinterpret_cast<const float*>(w) + (int64_t)r * H + 8 * c);
+                    wv[j][0] = p[0];
+                    wv[j][1] = p[1];
+                } else {
+                    const uint16_t* src = r < E ? reinterpret_cast<const uint16_t*>(w) + (int64_t)r * H : sgw;
+                    wv[j][0] = *reinterpret_cast<const uint4*>(src + 8 * c);
+                }
+#pragma unroll
+                for (int t = 0; t < TT; ++t)
+                    if (t < nt) xv[t][j] = *reinterpret_cast<const uint4*>(x + (int64_t)(t0 + t) * H + 8 * c);
             }
+        }
 #pragma unroll
-            for (int t = 0; t < TT; ++t)
-                if (t < nt) xv[t][j] = *reinterpret_cast<const uint4*>(x + (int64_t)(t0 + t) * H + 8 * c);
+        for (int t = 0; t < TT; ++t) {
+#pragma unroll
+            for (int j = 0; j < kNJ; ++j) {
+                const int c = jb + lane + kWave * j;
+                if (c < nch && t < nt) {
+                    uint32_t xw[4] = {xv[t][j].x, xv[t][j].y, xv[t][j].z, xv[t][j].w};
+                    float wf[8];
+                    if (wf32) {
+                        wf[0] = __uint_as_float(wv[j][0].x); wf[1] = __uint_as_float(wv[j][0].y);
+                        wf[2] = __uint_as_float(wv[j][0].z); wf[3] = __uint_as_float(wv[j][0].w);
+                        wf[4] = __uint_as_float(wv[j][1].x); wf[5] = __uint_as_float(wv[j][1].y);
+                        wf[6] = __uint_as_float(wv[j][1].z); wf[7] = __uint_as_float(wv[j][1].w);
+                    } else {
+                        uint32_t ww[4] = {wv[j][0].x, wv[j][0].y, wv[j][0].z, wv[j][0].w};
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            wf[2 * i] = bf2f(ww[i] & 0xFFFFu);
+                            wf[2 * i + 1] = bf2f(ww[i] >> 16);
+                        }
+                    }
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        acc[t] = fmaf(bf2f(xw[i] & 0xFFFFu), wf[2 * i], acc[t]);
+                        acc[t] = fmaf(bf2f(xw[i] >> 16), wf[2 * i + 1], acc[t]);
+                    }
+                }
+            }
         }
     }
 #pragma unroll
     for (int t = 0; t < TT; ++t) {
-        float acc = 0.0f;
-#pragma unroll
-        for (int j = 0; j < kNJ; ++j) {
-            const int c = lane + kWave * j;
-            if (c < nch && t < nt) {
-                uint32_t xw[4] = {xv[t][j].x, xv[t][j].y, xv[t][j].z, xv[t][j].w};
-                float wf[8];
-                if (wf32) {
-                    wf[0] = __uint_as_float(wv[j][0].x); wf[1] = __uint_as_float(wv[j][0].y);
-                    wf[2] = __uint_as_float(wv[j][0].z); wf[3] = __uint_as_float(wv[j][0].w);
-                    wf[4] = __uint_as_float(wv[j][1].x); wf[5] = __uint_as_float(wv[j][1].y);
-                    wf[6] = __uint_as_float(wv[j][1].z); wf[7] = __uint_as_float(wv[j][1].w);
-                } else {
-                    uint32_t ww[4] = {wv[j][0].x, wv[j][0].y, wv[j][0].z, wv[j][0].w};
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        wf[2 * i] = bf2f(ww[i] & 0xFFFFu);
-                        wf[2 * i + 1] = bf2f(ww[i] >> 16);
-                    }
-                }
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    acc = fmaf(bf2f(xw[i] & 0xFFFFu), wf[2 * i], acc);
-                    acc = fmaf(bf2f(xw[i] >> 16), wf[2 * i + 1], acc);
-                }
-            }
-        }
-        float s = wave_sum_xor(acc);
+        float s = wave_sum_xor(acc[t]);
         if (lane == 0 && t < nt) logits[(int64_t)(t0 + t) * (E + 1) + r] = (r < E && bias) ? s + bias[r] : s;
     }
 }

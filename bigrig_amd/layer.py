@@ -36,6 +36,7 @@ from .pool import ExpertPool
 from .spec import LayerSpec
 
 DECODE_MAX_TOKENS = 8
+DECODE_MAX_PAIRS = 64
 
 
 def _stream(stream=None):
@@ -65,9 +66,11 @@ def router_topk(spec: LayerSpec, x, w_router, bias=None, shared_gate_w=None, str
     return idx, w, sg
 
 
-def path_flag(n_tokens: int) -> int:
-    """The kernel family for a call of n_tokens rows: decode GEMV or grouped GEMM."""
-    return L.FWD_FORCE_DECODE if n_tokens <= DECODE_MAX_TOKENS else L.FWD_FORCE_PREFILL
+def path_flag(n_tokens: int, top_k: int) -> int:
+    """The kernel family for a call of n_tokens rows routed to top_k experts each: the decode
+    GEMV for at most 8 tokens and 64 (token, expert) pairs, the grouped GEMM otherwise."""
+    decode = n_tokens <= DECODE_MAX_TOKENS and n_tokens * top_k <= DECODE_MAX_PAIRS
+    return L.FWD_FORCE_DECODE if decode else L.FWD_FORCE_PREFILL
 
 
 def moe_forward(spec: LayerSpec, pool: ExpertPool, x2, idx, w=None, shared=None, sgate=None,
@@ -77,7 +80,7 @@ def moe_forward(spec: LayerSpec, pool: ExpertPool, x2, idx, w=None, shared=None,
     L.check(L.load().brx_moe_forward(
         C.byref(d), pool.device.handle, _dptr(x2), _dptr(idx), _dptr(w), _dptr(shared),
         _dptr(sgate), T, _dptr(out), _dptr(y_unreduced),
-        path_flag(T) if flags is None else flags, _stream(stream)))
+        path_flag(T, spec.top_k) if flags is None else flags, _stream(stream)))
 
 
 def moe_block(spec: LayerSpec, pool: ExpertPool, x2, router_w, router_bias=None,
@@ -256,7 +259,7 @@ class StreamingSwitchGLU:
         H, k = self.spec.hidden, self.spec.top_k
         x2 = x.reshape(-1, H).contiguous()
         T = x2.shape[0]
-        flags = path_flag(T)
+        flags = path_flag(T, k)
         idx = indices.reshape(-1, k).to(torch.int32).contiguous()
         y = torch.empty((T, k, H), dtype=torch.bfloat16, device=x2.device)
         if self._sync_free:
@@ -284,7 +287,7 @@ class StreamingSwitchGLU:
         import torch
         H, k = self.spec.hidden, self.spec.top_k
         T = x2.shape[0]
-        flags = path_flag(T)
+        flags = path_flag(T, k)
         out = torch.empty((T, H), dtype=torch.bfloat16, device=x2.device)
         shared = self.shared
         if self._sync_free:
@@ -348,7 +351,7 @@ class MoELayer:
                 idx = torch.empty((x2.shape[0], self.spec.top_k), dtype=torch.int32,
                                   device=x2.device)
             out = moe_block(self.spec, sw._pool, x2, self.router_w, self.router_bias, sgw,
-                            sw.shared, out_idx=idx, flags=path_flag(x2.shape[0]), stream=stream)
+                            sw.shared, out_idx=idx, flags=path_flag(x2.shape[0], self.spec.top_k), stream=stream)
             if idx is not None:
                 sw._after(idx, stream)
             return out.reshape(x.shape)

@@ -118,7 +118,7 @@ def prefill(spec: LayerSpec, layers: list, store: HostStore, chunks: list, ring:
             ring.load(i + 1, store, layers[i + 1].layer)
         for j, x in enumerate(h):
             out = ops.moe_block(spec, s, x, lw.router, lw.router_bias, lw.shared_gate_w, lw.shared,
-                                flags=ops.path_flag(x.shape[0]))
+                                flags=ops.path_flag(x.shape[0], spec.top_k))
             h[j] = out + x if residual else out
         if progress is not None:
             progress(i + 1, n)

@@ -27,7 +27,7 @@ EXPORTS = (
     "brx_pool_set_g2s", "brx_pool_sync", "brx_router_topk", "brx_moe_forward",
     "brx_moe_forward_pairs", "brx_moe_block_forward", "brx_combine", "brx_dequant",
     "brx_sort_pairs", "brx_pool_set_host_backing", "brx_pool_publish_async",
-    "brx_pool_admit_async", "brx_pool_refill_range_async",
+    "brx_pool_admit_async", "brx_pool_refill_range_async", "brx_pool_check",
 )
 
 
@@ -72,6 +72,7 @@ _SIGS = {
     "brx_pool_refill_from_device_async": ([_vp, C.c_int, _vp, C.c_size_t, _vp], C.c_int),
     "brx_pool_set_g2s": ([_vp, _i32p, C.c_int, _vp], C.c_int),
     "brx_pool_sync": ([_vp], C.c_int),
+    "brx_pool_check": ([_vp], C.c_int),
     "brx_pool_set_host_backing": ([_vp, _vp, C.c_int64, C.c_size_t], C.c_int),
     "brx_pool_publish_async": ([_vp, C.c_int, _i32p, _i32p, _vp], C.c_int),
     "brx_pool_admit_async": ([_vp, C.c_int, C.c_int, _vp, C.c_size_t, _vp], C.c_int),

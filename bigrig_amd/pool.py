@@ -178,11 +178,12 @@ class DeviceSlots:
             L.check(L.load().brx_pool_refill_async(self.handle, slot, blob.ptr, blob.nbytes, cs))
             return blob.nbytes
         raw = np.frombuffer(blob, dtype=np.uint8)
+        if self._stage_ev is not None:
+            # the previous copy out of the staging buffer must have finished before the buffer
+            # is rewritten or handed back to torch's pinned-memory cache
+            self._stage_ev.synchronize()
         if self._stage is None or self._stage.numel() < raw.nbytes:
             self._stage = torch.empty(raw.nbytes, dtype=torch.uint8, pin_memory=True)
-            self._stage_ev = None
-        if self._stage_ev is not None:
-            self._stage_ev.synchronize()      # the previous copy out of the staging buffer
         self._stage.numpy()[:raw.nbytes] = raw
         L.check(L.load().brx_pool_refill_async(self.handle, slot, self._stage.data_ptr(),
                                                raw.nbytes, cs))
@@ -230,6 +231,11 @@ class DeviceSlots:
 
     def sync(self) -> None:
         self._L.check(self._L.load().brx_pool_sync(self.handle))
+
+    def check(self) -> None:
+        """Wait for the pool's work, then raise (BrxError, code BRX_ERANGE) if a forward routed to
+        an expert that was neither resident nor host-backed (its rows were written as NaN)."""
+        self._L.check(self._L.load().brx_pool_check(self.handle))
 
     def close(self) -> None:
         if self.handle is not None:

@@ -8,6 +8,7 @@ from . import formats as F
 _ROUTES = {"softmax_topk": 0, "softmax_topk_renorm": 1, "topk_softmax": 2}
 _ACTS = {"swiglu": 0, "swiglu_clamped": 1}
 _RDT = {"float32": 0, "bfloat16": 1}
+MAX_WIDTH = 8192   # largest hidden / intermediate width libbrx takes
 
 
 @dataclass(frozen=True)
@@ -43,6 +44,11 @@ class LayerSpec:
             raise ValueError(f"router_dtype {self.router_dtype!r} not in {sorted(_RDT)}")
         if not 1 <= self.top_k <= self.n_experts:
             raise ValueError(f"top_k {self.top_k} outside [1, {self.n_experts}]")
+        for name in ("hidden", "inter", "shared_inter"):
+            v = getattr(self, name)
+            if v % 64 or v > MAX_WIDTH or (v <= 0 and name != "shared_inter") or v < 0:
+                raise ValueError(f"{name} {v} must be a multiple of 64 in "
+                                 f"[{0 if name == 'shared_inter' else 64}, {MAX_WIDTH}]")
 
     @property
     def route_mode(self) -> int:

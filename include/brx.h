@@ -56,8 +56,8 @@ enum { BRX_DT_F32 = 0, BRX_DT_BF16 = 1 };
 /* One MoE layer's shape and quantization: the manifest's per-layer
  * {n_experts, spec, quant} record (stream.py:133-151) plus the block's routing rule. */
 typedef struct brx_layer_desc {
-    int32_t hidden;        /* H: model width, input of gate/up, output of down            */
-    int32_t inter;         /* I: expert intermediate width                                  */
+    int32_t hidden;        /* H: model width, input of gate/up, output of down (<= 8192)  */
+    int32_t inter;         /* I: expert intermediate width (<= 8192)                        */
     int32_t n_experts;     /* E                                                             */
     int32_t top_k;         /* k                                                             */
     int32_t quant_mode;    /* BRX_QUANT_*                                                   */
@@ -70,7 +70,8 @@ typedef struct brx_layer_desc {
     float   limit;         /* clamped SwiGLU limit (7.0)                                    */
     int32_t route_mode;    /* BRX_ROUTE_*                                                   */
     int32_t router_dtype;  /* BRX_DT_*: dtype of the router weight [E, H]                   */
-    int32_t shared_inter;  /* intermediate width of an always-on shared expert, 0 = none    */
+    int32_t shared_inter;  /* intermediate width of an always-on shared expert, 0 = none
+                              (any multiple of 64 up to 8192, independent of inter)          */
     int32_t reserved;
 } brx_layer_desc;
 
@@ -105,7 +106,8 @@ int brx_expert_layout_get(const brx_layer_desc* d, int shared, brx_expert_layout
  * holds bytes and the table kernels read. */
 
 /* Allocate `capacity` slots of bytes_per_expert each (ExpertPool.build, stream.py:570-597).
- * 1 <= capacity <= n_experts (stream.py:503-506). The table starts all zero. */
+ * 1 <= capacity <= n_experts (stream.py:503-506). The table starts with every expert absent
+ * (-1). */
 int brx_pool_create(const brx_layer_desc* d, int capacity, brx_pool** out);
 /* Free the slots (StreamHandle.close, stream.py:2160-2191). Synchronizes the pool's streams. */
 int brx_pool_destroy(brx_pool* p);
@@ -132,11 +134,19 @@ int brx_pool_refill_range_async(brx_pool* p, int slot0, int n, const void* host_
 /* Same, from device memory (a staged expert, stream.py:957-961). */
 int brx_pool_refill_from_device_async(brx_pool* p, int slot, const void* dev_src, size_t nbytes,
                                       void* copy_stream);
-/* Upload the host expert->slot table (int32 [n_experts], -1 = absent, uploaded as max(g2s,0)
- * like ExpertPool.g2s_device, stream.py:791-797), ordered on `stream` and after any refill. */
+/* Upload the host expert->slot table (int32 [n_experts], -1 = absent; ExpertPool.g2s_device,
+ * stream.py:791-797), ordered on `stream` and after any refill. An absent expert stays -1 on
+ * the device: a forward that routes to it on a pool without host backing does not compute it
+ * from another expert's slot (the reference raises KeyError, stream.py:608-615) -- the rows it
+ * touches are written as NaN and the pool records the error, which brx_pool_check reports. */
 int brx_pool_set_g2s(brx_pool* p, const int32_t* g2s_host, int n, void* stream);
 /* Block until every copy and forward issued against the pool has finished. */
 int brx_pool_sync(brx_pool* p);
+/* brx_pool_sync, then BRX_ERANGE (naming the expert) if a forward since the last check routed
+ * to an expert that was neither in a slot nor host-backed; the error is cleared by the report.
+ * The device-side counterpart of ExpertPool.expert_arrays' KeyError (stream.py:608-615) for
+ * routing the host never sees. */
+int brx_pool_check(brx_pool* p);
 
 /* ---- host-served misses (no per-layer host round trip)
  * The reference keeps a bounded layer off the sync-free path because it must read the routing
@@ -189,7 +199,8 @@ int brx_router_topk(const brx_layer_desc* d, const void* x, const void* w_router
                     int32_t* out_idx, float* out_w, float* out_shared_gate, void* stream);
 
 /* flags for brx_moe_forward */
-#define BRX_FWD_FORCE_DECODE  1u  /* take the gather-GEMV path (at most 8 token rows, 64 pairs) */
+#define BRX_FWD_FORCE_DECODE  1u  /* take the gather-GEMV path (at most 8 token rows, 64 pairs;
+                                     BRX_EINVAL above)                                       */
 #define BRX_FWD_FORCE_PREFILL 2u  /* take the grouped-GEMM path whatever T is              */
 /* Split launch: run only the first half (gate/up + act; for the grouped GEMM also the
  * bucketing) or only the second half (down + combine) of a forward. The halves share the
@@ -210,9 +221,11 @@ int brx_router_topk(const brx_layer_desc* d, const void* x, const void* w_router
  * y_unreduced [T, k, H] bf16 or NULL (the unreduced rows StreamingSwitchGLU returns,
  * stream.py:1377-1577); shared_expert: device pointer to the shared expert's packed bytes
  * (layout brx_expert_layout_get(shared=1)) or NULL; shared_gate [T] fp32 or NULL.
- * T <= 8 (or FORCE_DECODE) runs the decode gather-GEMV kernels, larger T the prefill
- * grouped GEMM on MFMA (the reference's per-row `gather_qmm` vs sorted `gather_qmm`,
- * stream.py:1128-1172, 1320-1336). The library keeps a grown-on-demand workspace. */
+ * Without a FORCE flag, T <= 8 with T * k <= 64 runs the decode gather-GEMV kernels, anything
+ * larger the prefill grouped GEMM on MFMA (the reference's per-row `gather_qmm` vs sorted
+ * `gather_qmm`, stream.py:1128-1172, 1320-1336). The library keeps a grown-on-demand
+ * workspace. An expert in idx that is absent from a pool without host backing yields NaN rows
+ * and an error brx_pool_check reports (see brx_pool_set_g2s). */
 int brx_moe_forward(const brx_layer_desc* d, brx_pool* p, const void* x, const int32_t* idx,
                     const float* w, const void* shared_expert, const float* shared_gate, int T,
                     void* out, void* y_unreduced, unsigned flags, void* stream);
@@ -228,7 +241,8 @@ int brx_moe_forward(const brx_layer_desc* d, brx_pool* p, const void* x, const i
  * at most `capacity` experts (_pair_chunks, stream.py:1098-1126), makes each span resident and
  * calls this once per span, writing straight to the unsorted positions (stream.py:1558-1561).
  * x [T, H] bf16. Pass the same FORCE flag for every span of one chunk so a row's arithmetic
- * does not depend on how the chunk was cut (without a flag: decode kernels for n_pairs <= 8). */
+ * does not depend on how the chunk was cut (without a flag: decode kernels when n_pairs <= 8
+ * and T <= 8, since the decode kernels stage every row of x). */
 int brx_moe_forward_pairs(const brx_layer_desc* d, brx_pool* p, const void* x, int T,
                           const int32_t* pair_token, const int32_t* pair_expert,
                           const int32_t* pair_row, int n_pairs, int n_rows,
@@ -241,10 +255,11 @@ int brx_moe_forward_pairs(const brx_layer_desc* d, brx_pool* p, const void* x, i
  * (mlx_lm's MoE block around SwitchGLU; stream.py:1523-1525, adapter.py:61-64).
  *   out [T, H] bf16; out_idx [T, k] int32 and out_w [T, k] fp32 optional (device): the routing
  *   the block used, the same values brx_router_topk returns.
- * For T <= 8 (or FORCE_DECODE) the routing is ranked inside the expert kernel, so the block is
- * three launches; larger T routes first and runs the grouped GEMM. Every expert of the layer
- * must be resident: the pool's table is read for all E experts. PHASE_R / PHASE_A / PHASE_B
- * split the block into its routing, first-half and second-half launches (timing). */
+ * For T <= 8 with T * k <= 64 (or FORCE_DECODE) the routing is ranked inside the expert kernel,
+ * so the block is three launches; anything larger routes first and runs the grouped GEMM. Every
+ * expert of the layer must be resident (as last uploaded by brx_pool_set_g2s) unless the pool
+ * has host backing: BRX_ESTATE otherwise, before anything is launched. PHASE_R / PHASE_A /
+ * PHASE_B split the block into its routing, first-half and second-half launches (timing). */
 int brx_moe_block_forward(const brx_layer_desc* d, brx_pool* p, const void* x, const void* w_router,
                           const float* router_bias, const void* shared_gate_w,
                           const void* shared_expert, int T, void* out, int32_t* out_idx,

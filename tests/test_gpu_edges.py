@@ -73,7 +73,7 @@ def test_router_ties_go_to_the_lower_id(gpu):
         gi = torch.full((T, spec.top_k), -1, dtype=torch.int32, device=gpu)
         gw = torch.zeros((T, spec.top_k), dtype=torch.float32, device=gpu)
         ops.moe_block(spec, pool, to_dev_bits(x, gpu), router, out_idx=gi, out_w=gw,
-                      flags=ops.path_flag(T))
+                      flags=ops.path_flag(T, spec.top_k))
         i2, w2, _ = ops.router_topk(spec, to_dev_bits(x, gpu), router)
         torch.cuda.synchronize()
         assert np.array_equal(gi.cpu().numpy(), idx)
@@ -100,7 +100,7 @@ def test_512_experts(gpu, T):
     gi = torch.full((T, spec.top_k), -1, dtype=torch.int32, device=gpu)
     gw = torch.zeros((T, spec.top_k), dtype=torch.float32, device=gpu)
     out = ops.moe_block(spec, pool, to_dev_bits(x, gpu), router, out_idx=gi, out_w=gw,
-                        flags=ops.path_flag(T))
+                        flags=ops.path_flag(T, spec.top_k))
     torch.cuda.synchronize()
     _, idx, w, _ = oracle.router(x, lay.router, False, None, spec.top_k, spec.route_mode)
     assert np.array_equal(gi.cpu().numpy(), idx)

@@ -68,7 +68,7 @@ def test_full_size_layer(gpu, spec, T):
     idx = torch.empty((T, k), dtype=torch.int32, device=gpu)
     w = torch.empty((T, k), dtype=torch.float32, device=gpu)
     out = ops.moe_block(spec, pool, x, wr, bias, sgw, shared, out_idx=idx, out_w=w,
-                        flags=ops.path_flag(T))
+                        flags=ops.path_flag(T, spec.top_k))
     torch.cuda.synchronize()
     assert bool(torch.isfinite(out.float()).all()), "non-finite layer outputs"
 

@@ -152,7 +152,7 @@ def test_block_forward(gpu, spec, T):
     gw = torch.zeros((T, spec.top_k), dtype=torch.float32, device=gpu)
     pool.g2s_device(torch.cuda.current_stream().cuda_stream)
     out = ops.moe_block(spec, pool, xd, router, bias, sgw, sw.shared, out_idx=gi, out_w=gw,
-                        flags=ops.path_flag(T))
+                        flags=ops.path_flag(T, spec.top_k))
     torch.cuda.synchronize()
     _, idx, w, sg = oracle.router(x, lay.router, spec.router_dtype == "float32", lay.bias,
                                   spec.top_k, spec.route_mode, lay.sgate_w)

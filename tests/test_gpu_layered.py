@@ -52,7 +52,7 @@ def test_layer_major_prefill_matches_token_major(gpu):
         h = x.clone()
         for l in range(nl):
             out = ops.moe_block(spec, pools[l], h, ws[l].router, ws[l].router_bias,
-                                flags=ops.path_flag(h.shape[0]))
+                                flags=ops.path_flag(h.shape[0], spec.top_k))
             if l == 0:
                 xb = bits(h)
                 _, idx, w, _ = oracle.router(xb, lays[0].router, False, lays[0].bias, spec.top_k,

@@ -77,10 +77,12 @@ def test_expert_layout_matches_formats(spec):
 BAD = [("hidden", 100, "hidden"), ("inter", 0, "inter"), ("n_experts", 513, "n_experts"),
        ("top_k", 0, "top_k"), ("bits", 3, "affine"), ("group_size", 128, "affine"),
        ("quant_mode", 7, "quant_mode"), ("act", 5, "act"), ("route_mode", 3, "route_mode"),
-       ("router_dtype", 9, "router_dtype"), ("shared_inter", 96, "shared_inter")]
+       ("router_dtype", 9, "router_dtype"), ("shared_inter", 96, "shared_inter"),
+       ("hidden", 8256, "at most 8192"), ("inter", 8256, "at most 8192"),
+       ("shared_inter", 8256, "at most 8192")]
 
 
-@pytest.mark.parametrize("field,value,msg", BAD, ids=[b[0] for b in BAD])
+@pytest.mark.parametrize("field,value,msg", BAD, ids=[f"{b[0]}={b[1]}" for b in BAD])
 def test_descriptor_validation(field, value, msg):
     """Every entry point validates the descriptor before anything touches the device."""
     lib = L.load()
@@ -111,3 +113,26 @@ def test_calls_before_init_fail_cleanly():
 def test_missing_library_fails_loudly(tmp_path):
     with pytest.raises(RuntimeError, match="no CPU fallback"):
         L.load(str(tmp_path / "nope.so"))
+
+
+def test_shared_expert_width_is_independent_of_the_routed_width():
+    """A shared expert wider than the routed ones (a different shared intermediate) is a layout
+    of its own, equal to what formats packs."""
+    from dataclasses import replace
+    lib = L.load()
+    for sh in (256, 1024, 1536):
+        spec = replace(E256_SHARED, shared_inter=sh)
+        d = spec.desc()
+        out = L.ExpertLayout()
+        L.check(lib.brx_expert_layout_get(C.byref(d), 1, C.byref(out)))
+        assert out.bytes_per_expert == F.spec_bytes(spec.expert_spec(True))
+        L.check(lib.brx_expert_layout_get(C.byref(d), 0, C.byref(out)))
+        assert out.bytes_per_expert == spec.bytes_per_expert
+
+
+def test_layer_spec_refuses_widths_the_kernels_do_not_take():
+    from dataclasses import replace
+    for kw in ({"hidden": 8256}, {"inter": 100}, {"shared_inter": 96}, {"hidden": 0}):
+        with pytest.raises(ValueError):
+            replace(QWEN3_30B_A3B, **kw)
+    assert replace(QWEN3_30B_A3B, hidden=8192).hidden == 8192
