@@ -24,6 +24,13 @@ struct Workspace {
 Workspace g_ws;
 std::mutex g_ws_mu;
 
+// Scratch of brx_moe_block_forward_noalloc: a file-scope device array (one copy per GPU, held
+// until the process ends). Host code never uses the array's name as an address: brx_init looks
+// up each device's copy with hipGetSymbolAddress and keeps that pointer.
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) uint8_t scratch[BRX_NOALLOC_SCRATCH_BYTES];
+void* g_scratch_ptr[kMaxDevices] = {};
+
 int fail(int code, const char* fmt, ...) {
     char buf[512];
     va_list ap;
@@ -139,6 +146,14 @@ int brx_init(int device) {
     HIP_TRY(hipGetDeviceProperties(&prop, device));
     if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
         return fail(BRX_EINVAL, "device %d is %s; libbrx is built for gfx950 only", device, prop.gcnArchName);
+    if (device >= kMaxDevices) return fail(BRX_EINVAL, "device %d outside [0, %d)", device, kMaxDevices);
+    if (!g_scratch_ptr[device]) {
+        // this device's copy of the no-alloc scratch, looked up with the device current
+        void* sp = nullptr;
+        HIP_TRY(hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch)));
+        if (!sp || ((uintptr_t)sp & 255)) return fail(BRX_EHIP, "no-alloc scratch resolved to %p", sp);
+        g_scratch_ptr[device] = sp;
+    }
     g_device = device;
     return BRX_OK;
 }
@@ -555,9 +570,12 @@ int brx_moe_forward_pairs(const brx_layer_desc* d, brx_pool* p, const void* x, i
                         nullptr, y_rows, flags, stream);
 }
 
-int brx_moe_block_forward(const brx_layer_desc* d, brx_pool* p, const void* x, const void* w_router,
-                          const float* router_bias, const void* shared_gate_w, const void* shared_expert,
-                          int T, void* out, int32_t* out_idx, float* out_w, unsigned flags, void* stream) {
+// The whole block over either the library workspace (scratch == nullptr: grown on demand) or
+// the caller-free static scratch of `scratch_bytes` (nothing allocated; too small -> EINVAL).
+static int block_forward_impl(const brx_layer_desc* d, brx_pool* p, const void* x, const void* w_router,
+                              const float* router_bias, const void* shared_gate_w, const void* shared_expert,
+                              int T, void* out, int32_t* out_idx, float* out_w, unsigned flags, void* stream,
+                              void* scratch_ws, size_t scratch_bytes) {
     int rc = check_forward_common(d, p, x);
     if (rc) return rc;
     if (T < 0) return fail(BRX_EINVAL, "T %d < 0", T);
@@ -598,8 +616,17 @@ int brx_moe_block_forward(const brx_layer_desc* d, brx_pool* p, const void* x, c
                           nullptr);
     const size_t fwd_b = decode ? decode_workspace_bytes(a) : prefill_workspace_bytes(a);
     void* ws = nullptr;
-    if ((rc = ws_reserve(route_b + fwd_b, s, &ws))) return rc;
-    const size_t ws_bytes = g_ws.bytes;
+    size_t ws_bytes = 0;
+    if (scratch_ws) {
+        if (route_b + fwd_b > scratch_bytes)
+            return fail(BRX_EINVAL, "this call needs %zu bytes of scratch, the no-alloc scratch holds %zu "
+                        "(T=%d); use brx_moe_block_forward", route_b + fwd_b, scratch_bytes, T);
+        ws = scratch_ws;
+        ws_bytes = scratch_bytes;
+    } else {
+        if ((rc = ws_reserve(route_b + fwd_b, s, &ws))) return rc;
+        ws_bytes = g_ws.bytes;
+    }
     char* base = (char*)ws;
     float* logits = (float*)base;
     int32_t* ridx = out_idx ? out_idx : (int32_t*)(base + logits_b);
@@ -622,6 +649,25 @@ int brx_moe_block_forward(const brx_layer_desc* d, brx_pool* p, const void* x, c
     if (e != hipSuccess) return hip_fail(e, "router launch");
     if (!phases) return BRX_OK;
     return run_forward(p, a, decode, phases, fws, ws_bytes - route_b, s);
+}
+
+int brx_moe_block_forward(const brx_layer_desc* d, brx_pool* p, const void* x, const void* w_router,
+                          const float* router_bias, const void* shared_gate_w, const void* shared_expert,
+                          int T, void* out, int32_t* out_idx, float* out_w, unsigned flags, void* stream) {
+    return block_forward_impl(d, p, x, w_router, router_bias, shared_gate_w, shared_expert, T, out, out_idx,
+                              out_w, flags, stream, nullptr, 0);
+}
+
+int brx_moe_block_forward_noalloc(const brx_layer_desc* d, brx_pool* p, const void* x, const void* w_router,
+                                  const float* router_bias, const void* shared_gate_w,
+                                  const void* shared_expert, int T, void* out, int32_t* out_idx, float* out_w,
+                                  unsigned flags, void* stream) {
+    int rc = ensure_device();
+    if (rc) return rc;
+    void* sp = g_scratch_ptr[g_device];
+    if (!sp) return fail(BRX_ESTATE, "no-alloc scratch of device %d is not set up", g_device);
+    return block_forward_impl(d, p, x, w_router, router_bias, shared_gate_w, shared_expert, T, out, out_idx,
+                              out_w, flags, stream, sp, BRX_NOALLOC_SCRATCH_BYTES);
 }
 
 int brx_combine(const brx_layer_desc* d, const void* y_routed, const float* w, const void* y_shared,

@@ -19,6 +19,7 @@ ACT_SWIGLU, ACT_SWIGLU_CLAMPED = 0, 1
 ROUTE_SOFTMAX_TOPK, ROUTE_SOFTMAX_TOPK_RENORM, ROUTE_TOPK_SOFTMAX = 0, 1, 2
 DT_F32, DT_BF16 = 0, 1
 FWD_FORCE_DECODE, FWD_FORCE_PREFILL, FWD_PHASE_A, FWD_PHASE_B, FWD_PHASE_R = 1, 2, 4, 8, 16
+NOALLOC_SCRATCH_BYTES = 16 << 20
 
 EXPORTS = (
     "brx_abi_version", "brx_last_error", "brx_init", "brx_expert_layout_get",
@@ -28,6 +29,7 @@ EXPORTS = (
     "brx_moe_forward_pairs", "brx_moe_block_forward", "brx_combine", "brx_dequant",
     "brx_sort_pairs", "brx_pool_set_host_backing", "brx_pool_publish_async",
     "brx_pool_admit_async", "brx_pool_refill_range_async", "brx_pool_check",
+    "brx_moe_block_forward_noalloc",
 )
 
 
@@ -86,6 +88,8 @@ _SIGS = {
                                C.c_int, _vp, _vp, C.c_uint, _vp], C.c_int),
     "brx_moe_block_forward": ([C.POINTER(LayerDesc), _vp, _vp, _vp, _vp, _vp, _vp, C.c_int, _vp,
                                _vp, _vp, C.c_uint, _vp], C.c_int),
+    "brx_moe_block_forward_noalloc": ([C.POINTER(LayerDesc), _vp, _vp, _vp, _vp, _vp, _vp, C.c_int,
+                                       _vp, _vp, _vp, C.c_uint, _vp], C.c_int),
     "brx_combine": ([C.POINTER(LayerDesc), _vp, _vp, _vp, _vp, C.c_int, _vp, _vp], C.c_int),
     "brx_dequant": ([C.POINTER(LayerDesc), _vp, C.c_int, C.c_int, _vp, _vp], C.c_int),
     "brx_sort_pairs": ([C.POINTER(LayerDesc), _vp, C.c_int, _vp, _vp, _vp], C.c_int),

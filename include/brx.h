@@ -265,6 +265,24 @@ int brx_moe_block_forward(const brx_layer_desc* d, brx_pool* p, const void* x, c
                           const void* shared_expert, int T, void* out, int32_t* out_idx,
                           float* out_w, unsigned flags, void* stream);
 
+/* brx_moe_block_forward that allocates nothing. It has no counterpart in the reference: it is
+ * for callers that cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). Same arguments, results and errors; the scratch the
+ * call needs (routing logits and weights, the decode entry table and activations, or the
+ * prefill bucketing and GEMM intermediates) lives in a library-owned static device array of
+ * BRX_NOALLOC_SCRATCH_BYTES per GPU, resolved at brx_init, instead of the grown-on-demand
+ * workspace, and no hipMalloc, hipFree or device synchronization is made. A call whose scratch
+ * exceeds it fails with BRX_EINVAL before anything is launched (every decode step fits; a
+ * Qwen3-30B-shaped prefill chunk fits up to ~350 tokens). Every call on one GPU shares that
+ * GPU's array and nothing in it has to start at zero: calls that overlap on one GPU (other
+ * streams or host threads) race and must be ordered by the caller. */
+#define BRX_NOALLOC_SCRATCH_BYTES (16u << 20)
+int brx_moe_block_forward_noalloc(const brx_layer_desc* d, brx_pool* p, const void* x,
+                                  const void* w_router, const float* router_bias,
+                                  const void* shared_gate_w, const void* shared_expert, int T,
+                                  void* out, int32_t* out_idx, float* out_w, unsigned flags,
+                                  void* stream);
+
 /* The caller's router-weighted combine of unreduced rows (stream.py:1523-1525):
  *   out[t] = bf16( sum_j w[t, j] * y_routed[t, j]  (+ shared_gate[t] * y_shared[t]) )
  * in fp32, j in order. y_routed [T, k, H] bf16, w [T, k] fp32, y_shared [T, H] bf16 or NULL. */
