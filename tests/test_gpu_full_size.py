@@ -9,7 +9,9 @@ sizes).
 The sizes: Qwen3-30B-A3B shape (hidden 2048, 128 experts, top-8, inter 768, 4-bit affine) for a
 2048-token prefill chunk and a 1-token decode step; gpt-oss-120b shape (hidden 2880, 128
 experts, top-4, inter 2880, MXFP4 + biases, clamped SwiGLU) for a 512-token chunk and one
-decode token; 256 experts + shared expert (inter 512) at batch 8.
+decode token; 256 experts + shared expert (inter 512) at batch 8 and batch 1; the OLMoE-1B-7B
+layer (hidden 2048, 64 experts, inter 1024, fp32 router, softmax top-8 without renormalisation)
+at batch 1 and 8. The Qwen3 and 256-expert routers carry the Zipf(1.1) bias, the others none.
 """
 import numpy as np
 import pytest
@@ -17,7 +19,7 @@ import pytest
 import oracle
 from bigrig_amd import formats as F
 from bigrig_amd import layer as ops
-from bigrig_amd.spec import E256_SHARED, GPT_OSS_120B, QWEN3_30B_A3B
+from bigrig_amd.spec import E256_SHARED, GPT_OSS_120B, OLMOE_1B_7B, QWEN3_30B_A3B
 
 pytestmark = pytest.mark.gpu
 
@@ -29,8 +31,14 @@ def _bits(t):
     return t.detach().contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
 
 
+# the configurations with a Zipf-biased router (Qwen3-30B-A3B shape and the 256-expert layer);
+# the OLMoE and gpt-oss layers route on the plain logits
+ZIPF = {QWEN3_30B_A3B: 1.1, E256_SHARED: 1.1}
+
+
 def _layer(spec, seed):
-    """(pool, experts uint8 [E, bytes] on the GPU, router w, Zipf bias, shared, shared gate w)."""
+    """(pool, experts uint8 [E, bytes] on the GPU, router w, Zipf bias or None, shared, shared
+    gate w)."""
     import torch
 
     from bigrig_amd import synth
@@ -43,7 +51,8 @@ def _layer(spec, seed):
     pool.g2s_device(torch.cuda.current_stream().cuda_stream)
     pool.device.sync()
     wr = synth.router_weights(spec, seed=seed + 1)
-    bias = synth.zipf_bias_torch(spec.n_experts, 1.1, seed=seed + 2)
+    bias = (synth.zipf_bias_torch(spec.n_experts, ZIPF[spec], seed=seed + 2) if spec in ZIPF
+            else None)
     shared = sgw = None
     if spec.shared_inter:
         shared = synth.make_layer_experts(spec, seed=seed + 3, shared=True)[0].contiguous()
@@ -54,9 +63,11 @@ def _layer(spec, seed):
 
 
 @pytest.mark.parametrize("spec,T", [(QWEN3_30B_A3B, 2048), (QWEN3_30B_A3B, 1), (GPT_OSS_120B, 512),
-                                    (GPT_OSS_120B, 1), (E256_SHARED, 8)],
+                                    (GPT_OSS_120B, 1), (E256_SHARED, 8), (E256_SHARED, 1),
+                                    (OLMOE_1B_7B, 1), (OLMOE_1B_7B, 8)],
                          ids=["qwen3-prefill2048", "qwen3-decode1", "gptoss-prefill512",
-                              "gptoss-decode1", "e256shared-decode8"])
+                              "gptoss-decode1", "e256shared-decode8", "e256shared-decode1",
+                              "olmoe-decode1", "olmoe-decode8"])
 def test_full_size_layer(gpu, spec, T):
     import torch
 
@@ -76,8 +87,9 @@ def test_full_size_layer(gpu, spec, T):
     xb = _bits(x)[toks]
     wr_h = wr.cpu().numpy() if spec.router_dtype == "float32" else _bits(wr)
     sgw_h = None if sgw is None else _bits(sgw)
-    _, oidx, ow, osg = oracle.router(xb, wr_h, spec.router_dtype == "float32", bias.cpu().numpy(),
-                                     k, spec.route_mode, sgw_h)
+    _, oidx, ow, osg = oracle.router(xb, wr_h, spec.router_dtype == "float32",
+                                     None if bias is None else bias.cpu().numpy(), k,
+                                     spec.route_mode, sgw_h)
     gidx = idx.cpu().numpy()[toks]
     assert np.array_equal(gidx, oidx), "routing indices differ from the oracle"
     np.testing.assert_allclose(w.cpu().numpy()[toks], ow, rtol=1e-5, atol=1e-7)
