@@ -87,9 +87,11 @@ def copy_probe(args) -> None:
 
 
 class Stack:
-    """48 layers of pools, router weights, Zipf biases and input banks on the GPU."""
+    """A stack of layers on the GPU: fully resident pools, router weights, the router's Zipf
+    bias (None for the configurations that route on plain logits) and input banks."""
 
-    def __init__(self, spec, layers: int, bank: int, keep_host_layers: int = 0):
+    def __init__(self, spec, layers: int, bank: int, keep_host_layers: int = 0,
+                 zipf: float | None = 1.1):
         import torch
 
         from bigrig_amd import synth
@@ -114,7 +116,8 @@ class Stack:
             del experts
             self.pools.append(pool)
             self.routers.append(synth.router_weights(spec, seed=2000 + l))
-            self.biases.append(synth.zipf_bias_torch(spec.n_experts, 1.1, seed=3000 + l))
+            self.biases.append(synth.zipf_bias_torch(spec.n_experts, zipf, seed=3000 + l)
+                               if zipf else None)
             self.xbank.append(synth.activations(bank, spec.hidden, seed=4000 + l))
             if spec.shared_inter:
                 self.shared.append(synth.make_layer_experts(spec, seed=5000 + l, shared=True)[0].contiguous())
@@ -318,9 +321,16 @@ def prefill_bench(args, st: "Stack"):
     }
 
 
-def decode_report(st: "Stack", T: int, graphs: int = 4, reps: int = 25):
+def _p(t):
+    return None if t is None else t.data_ptr()
+
+
+def decode_report(st: "Stack", T: int, steps: int, per_graph: int = 16, reps: int = 3):
     """Kernel-level decode of T tokens through every layer of `st` (one brx_moe_block_forward
-    per layer, all experts resident), replayed as HIP graphs over `graphs` input rows."""
+    per layer, all experts resident) for `steps` steps, each with its own input rows (a fresh
+    input per step: repeating a few inputs would let a biased router settle on experts the
+    last-level cache then holds). Steps are captured `per_graph` at a time as HIP graphs and the
+    graphs replayed in order."""
     import ctypes as C
 
     import torch
@@ -331,26 +341,32 @@ def decode_report(st: "Stack", T: int, graphs: int = 4, reps: int = 25):
     d = spec.desc()
     dref = C.byref(d)
     H, k = spec.hidden, spec.top_k
+    assert st.xbank[0].shape[0] >= steps * T, "input bank smaller than steps x T"
     outs = [torch.empty((T, H), dtype=torch.bfloat16, device="cuda") for _ in range(Ln)]
-    idx = [[torch.empty((T, k), dtype=torch.int32, device="cuda") for _ in range(Ln)] for _ in range(graphs)]
+    idx = [[torch.empty((T, k), dtype=torch.int32, device="cuda") for _ in range(Ln)]
+           for _ in range(steps)]
+    sh = bool(spec.shared_inter)
 
-    def step(g, stream):
+    def step(i, stream):
         for l in range(Ln):
-            x = st.xbank[l][g * T:(g + 1) * T]
-            sh = bool(spec.shared_inter)
+            x = st.xbank[l][i * T:(i + 1) * T]
             L.check(lib.brx_moe_block_forward(dref, st.pools[l].device.handle, x.data_ptr(),
-                                              st.routers[l].data_ptr(), st.biases[l].data_ptr(),
+                                              st.routers[l].data_ptr(), _p(st.biases[l]),
                                               st.shared_gate[l].data_ptr() if sh else None,
                                               st.shared[l].data_ptr() if sh else None, T,
-                                              outs[l].data_ptr(), idx[g][l].data_ptr(), None,
+                                              outs[l].data_ptr(), idx[i][l].data_ptr(), None,
                                               L.FWD_FORCE_DECODE, stream))
 
+    # one eager step first: a pool's first forward orders itself after the pool's refills,
+    # which a graph capture cannot wait on
+    step(0, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
     gs = []
-    for g in range(graphs):
-        step(g, torch.cuda.current_stream().cuda_stream)
+    for g0 in range(0, steps, per_graph):
         cg = torch.cuda.CUDAGraph()
         with torch.cuda.graph(cg):
-            step(g, torch.cuda.current_stream().cuda_stream)
+            for i in range(g0, min(g0 + per_graph, steps)):
+                step(i, torch.cuda.current_stream().cuda_stream)
         gs.append(cg)
     torch.cuda.synchronize()
     for cg in gs:
@@ -360,18 +376,19 @@ def decode_report(st: "Stack", T: int, graphs: int = 4, reps: int = 25):
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(s)
     for r in range(reps):
-        gs[r % graphs].replay()
+        for cg in gs:
+            cg.replay()
     e1.record(s)
     torch.cuda.synchronize()
-    us_layer = e0.elapsed_time(e1) * 1e3 / (reps * Ln)
-    distinct = sum(len(torch.unique(i)) for row in idx for i in row) / (graphs * Ln)
+    us_layer = e0.elapsed_time(e1) * 1e3 / (reps * steps * Ln)
+    distinct = sum(len(torch.unique(i)) for row in idx for i in row) / (steps * Ln)
     router_b = spec.n_experts * H * (4 if spec.router_dtype == "float32" else 2)
     nbytes = distinct * spec.bytes_per_expert + router_b + 2 * T * H * 2
     if spec.shared_inter:
         from bigrig_amd import formats as F
         nbytes += F.spec_bytes(spec.expert_spec(True)) + 2 * H
     del gs
-    return {"tokens": T, "layers": Ln, "us_per_layer": round(us_layer, 3),
+    return {"tokens": T, "layers": Ln, "steps": steps, "us_per_layer": round(us_layer, 3),
             "layer_tokens_per_s": round(T * 1e6 / us_layer, 1),
             "distinct_experts": round(distinct, 2), "bytes_per_layer_step": int(nbytes),
             "hbm_gbs": round(nbytes / (us_layer * 1e-6) / 1e9, 1),
@@ -400,7 +417,7 @@ def prefill_report(st: "Stack", T: int, reps: int = 3):
         for l in range(Ln):
             sh = bool(spec.shared_inter)
             L.check(lib.brx_moe_block_forward(dref, st.pools[l].device.handle, xs[l].data_ptr(),
-                                              st.routers[l].data_ptr(), st.biases[l].data_ptr(),
+                                              st.routers[l].data_ptr(), _p(st.biases[l]),
                                               st.shared_gate[l].data_ptr() if sh else None,
                                               st.shared[l].data_ptr() if sh else None, T,
                                               out.data_ptr(), idx[l].data_ptr(), None,
@@ -469,25 +486,40 @@ def layered_bench(st: "Stack", n_layers: int = 8, prompt: int = 32768, chunk: in
             "hidden_frac": round((t_ser - t_ra) / max(min(t_copy, t_cmp), 1e-9), 3)}
 
 
-def config_report():
-    """The other shapes of the workload list, kernel level, all experts resident: OLMoE decode,
-    256 experts + shared expert decode at batch 1 and 8, gpt-oss MXFP4 decode and a 512-token
-    prefill. Fewer layers than the full stacks (distinct layers, 1.8-6.8 GB of weights, far
-    beyond the 256 MB last-level cache, so every step reads its experts from HBM)."""
+def config_report(args):
+    """The other configurations, each as specified, all experts resident unless stated:
+      OLMoE-1B-7B layer, decode batch 1: 256 seeded steps, each with a fresh input, cycled over
+        16 distinct weight replicas (3.6 GB, far beyond the 256 MB last-level cache); fp32
+        router, softmax top-8 without renormalisation, no router bias;
+      256 experts + shared expert, the 40-layer stack (18 GB), Zipf(1.1) router bias: decode at
+        batch 1 and batch 8 (64 steps, fresh inputs), and end to end through 38 of 256 slots per
+        layer (15% residency), synchronous and host-served (PCIe-inclusive);
+      gpt-oss-120b MXFP4, the 36-layer stack (61 GB), plain logits: decode at batch 1 (64 steps,
+        fresh inputs) and one 512-token prefill chunk through every layer."""
     import torch
 
     from bigrig_amd.spec import E256_SHARED, GPT_OSS_120B, OLMOE_1B_7B
     rep = {}
-    st = Stack(OLMOE_1B_7B, 8, bank=32)
-    rep["olmoe_1b_7b_decode_b1"] = decode_report(st, 1)
+    st = Stack(OLMOE_1B_7B, 16, bank=256, zipf=None)
+    rep["olmoe_1b_7b_decode_b1"] = decode_report(st, 1, steps=256)
     del st
-    st = Stack(E256_SHARED, 8, bank=32)
-    rep["e256_shared_decode_b1"] = decode_report(st, 1)
-    rep["e256_shared_decode_b8"] = decode_report(st, 8)
+    torch.cuda.empty_cache()
+    keep = 0 if "pool" in args.skip else 40
+    st = Stack(E256_SHARED, 40, bank=64 * 8, keep_host_layers=keep)
+    rep["e256_shared_decode_b1"] = decode_report(st, 1, steps=64)
+    rep["e256_shared_decode_b8"] = decode_report(st, 8, steps=64, per_graph=8)
+    if keep:
+        log("256-expert + shared through 38 slots")
+        pool = {"synchronous": pool_bench(args, st, capacities=[38] * keep),
+                "host_served": pool_bench(args, st, host_served=True, capacities=[38] * keep)}
+        rep["e256_shared_pool_c38"] = {
+            k2: {k3: (round(v, 4) if isinstance(v, float) else v) for k3, v in d.items()}
+            for k2, d in pool.items()}
     del st
-    st = Stack(GPT_OSS_120B, 4, bank=32)
-    rep["gpt_oss_120b_decode_b1"] = decode_report(st, 1)
-    rep["gpt_oss_120b_prefill_512"] = prefill_report(st, 512)
+    torch.cuda.empty_cache()
+    st = Stack(GPT_OSS_120B, 36, bank=64, zipf=None)
+    rep["gpt_oss_120b_decode_b1"] = decode_report(st, 1, steps=64)
+    rep["gpt_oss_120b_prefill_512"] = prefill_report(st, 512, reps=1)
     del st
     torch.cuda.empty_cache()
     return rep
@@ -510,9 +542,11 @@ def pool_bench(args, st: "Stack", host_served: bool = False, capacities=None):
     for i, l in enumerate(layers):
         cap = args.pool_capacity if capacities is None else capacities[i]
         pool = ExpertPool(l, spec, cap).build()
-        sw = StreamingSwitchGLU(pool, fetcher, host_served=host_served)
+        shared = st.shared[l] if spec.shared_inter else None
+        sw = StreamingSwitchGLU(pool, fetcher, shared=shared, host_served=host_served)
         sw.refresh()
-        mods.append(MoELayer(spec, st.routers[l], sw, router_bias=st.biases[l]))
+        mods.append(MoELayer(spec, st.routers[l], sw, router_bias=st.biases[l],
+                             shared_gate_w=st.shared_gate[l] if spec.shared_inter else None))
     from bigrig_amd import synth
     n = args.pool_tokens
     # a fresh activation per (layer, token): repeating a small input bank would let the pool
@@ -536,10 +570,10 @@ def pool_bench(args, st: "Stack", host_served: bool = False, capacities=None):
     dt = time.perf_counter() - t0
     hits = sum(m.switch._pool.hits for m in mods)
     miss = sum(m.switch._pool.misses for m in mods)
-    res = {"capacity": args.pool_capacity if capacities is None else "per layer",
+    caps = sorted(set(capacities)) if capacities is not None else [args.pool_capacity]
+    res = {"capacity": caps[0] if len(caps) == 1 else "per layer",
            "layers": len(layers),
-           "tok_s_layers": n / dt,
-           "tok_s_48": n / dt * len(layers) / 48.0,
+           "tok_s": n / dt,
            "miss_rate": miss / max(1, hits + miss),
            "pcie_inclusive": True}
     if host_served:
@@ -597,19 +631,20 @@ def cpu_bench(args, st: "Stack"):
         biases.append(st.biases[l].cpu().numpy())
     xs = [st.xbank[l].view(torch.int16).cpu().numpy().view(np.uint16) for l in range(nlay)]
     G = xs[0].shape[0]
+    cores = len(os.sched_getaffinity(0))
     n, t0 = 0, time.perf_counter()
     while True:
         for l in range(nlay):
             x = xs[l][n % G:n % G + 1]
             _, idx, w, _ = oracle.router(x, routers[l], False, biases[l], spec.top_k,
                                          spec.route_mode)
-            oracle.moe_forward(spec, experts[l], x, idx, w)
+            oracle.moe_forward(spec, experts[l], x, idx, w, nthreads=cores)
         n += 1
         el = time.perf_counter() - t0
         if el >= args.cpu_seconds:
             break
     per_layer_tok = el / (n * nlay)
-    return {"value": 1.0 / (per_layer_tok * 48), "unit": "tokens/s", "cores": oracle.num_threads(),
+    return {"value": 1.0 / (per_layer_tok * 48), "unit": "tokens/s", "cores": cores,
             "kind": "port",
             "sample": f"{n} decode tokens x {nlay} layers of the same stack (router + 8 experts + "
                       f"combine per layer-token, OpenMP over (token, expert) rows), "
@@ -679,7 +714,7 @@ def main():
         log("other shapes")
         del st
         torch.cuda.empty_cache()
-        report = config_report()
+        report = config_report(args)
     traffic = None
     tp = os.path.join(ROOT, "profiles", "traffic_decode_gateup.json")
     if os.path.exists(tp):

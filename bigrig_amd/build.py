@@ -77,7 +77,10 @@ def build(verbose: bool = False) -> str:
 def build_replay(verbose: bool = False) -> str:
     """libbrx_replay.so: csrc/replay.cpp, plain C++ for the host (no GPU code)."""
     tmp = REPLAY_LIB + ".tmp"
-    cmd = [shutil.which("g++") or "g++", "-O3", "-std=c++17", "-fPIC", "-shared", "-pthread",
+    # -ffp-contract=off: the floating-point policies (LFUDA, gaterank, coact) must round each
+    # step as the Python restatement does, so their victims agree request for request
+    cmd = [shutil.which("g++") or "g++", "-O3", "-std=c++17", "-ffp-contract=off", "-fPIC",
+           "-shared", "-pthread",
            "-I", INCLUDE, os.path.join(CSRC, "replay.cpp"), "-o", tmp]
     if verbose:
         print(" ".join(cmd), flush=True)

@@ -18,8 +18,11 @@ from __future__ import annotations
 import glob
 import json
 import os
+import re
 import struct
 from dataclasses import dataclass, field
+
+import numpy as np
 
 from . import formats as F
 
@@ -40,6 +43,11 @@ ST_DTYPES = {"F64": ("float64", 8), "F32": ("float32", 4), "F16": ("float16", 2)
 
 _MAX_HEADER = 1 << 30
 
+# <anything>.<layer index><one of the infixes><projection>.<component>
+_EXPERT_NAME = re.compile(
+    r"^.*\.(?P<layer>\d+)(?P<infix>" + "|".join(re.escape(i) for i in EXPERT_INFIXES) +
+    r")(?P<proj>[A-Za-z0-9_]+)\.(?P<comp>[A-Za-z0-9_]+)$")
+
 
 @dataclass(frozen=True)
 class Tensor:
@@ -52,63 +60,68 @@ class Tensor:
 
 
 def read_header(path: str) -> tuple:
-    """(header dict, absolute offset of the data section) of one safetensors file."""
+    """(header dict, absolute offset of the data section) of one safetensors file: a
+    little-endian u64 header length, then that many bytes of JSON object."""
     with open(path, "rb") as f:
-        raw = f.read(8)
-        if len(raw) != 8:
-            raise ValueError(f"{path} is too short to be a safetensors file")
-        n = struct.unpack("<Q", raw)[0]
-        if not 0 < n < _MAX_HEADER:
-            raise ValueError(f"{path}: implausible safetensors header length {n}")
-        body = f.read(n)
-    if len(body) != n:
-        raise ValueError(f"{path}: header of {n} bytes is cut short at {len(body)}")
-    hdr = json.loads(body)
-    if not isinstance(hdr, dict):
-        raise ValueError(f"{path}: safetensors header is not an object")
-    return hdr, 8 + n
+        prefix = f.read(8)
+        if len(prefix) < 8:
+            raise ValueError(f"{path} is too short to be a safetensors file ({len(prefix)} bytes)")
+        (hlen,) = struct.unpack("<Q", prefix)
+        if hlen == 0 or hlen >= _MAX_HEADER:
+            raise ValueError(f"{path}: implausible safetensors header length {hlen}")
+        text = f.read(hlen)
+    if len(text) < hlen:
+        raise ValueError(f"{path}: the {hlen}-byte header is cut short at {len(text)} bytes")
+    header = json.loads(text)
+    if type(header) is not dict:
+        raise ValueError(f"{path}: the safetensors header is not an object")
+    return header, 8 + hlen
+
+
+def _shard_tensors(path: str) -> dict:
+    """{name: Tensor} of one shard, every entry's dtype and byte range checked against the
+    file before it is trusted."""
+    header, start = read_header(path)
+    end = os.path.getsize(path)
+    found = {}
+    for name, meta in header.items():
+        if name == "__metadata__":
+            continue
+        lo, hi = (int(v) for v in meta["data_offsets"])
+        if not 0 <= lo <= hi or start + hi > end:
+            raise ValueError(f"{path}: tensor {name} claims bytes {lo}..{hi}, which runs past the "
+                             f"file ({end} bytes); nothing is read past the end")
+        dt = meta["dtype"]
+        if dt not in ST_DTYPES:
+            raise ValueError(f"{path}: tensor {name} has unknown dtype {dt}")
+        found[name] = Tensor(path, start + lo, hi - lo, dt, tuple(int(x) for x in meta["shape"]))
+    return found
 
 
 def scan(model_dir: str) -> dict:
     """{tensor name: Tensor} over every `*.safetensors` shard of a model directory."""
-    d = os.path.expanduser(model_dir)
-    files = sorted(glob.glob(os.path.join(d, "*.safetensors")))
-    if not files:
-        raise FileNotFoundError(f"no safetensors in {d}")
-    out = {}
-    for p in files:
-        hdr, base = read_header(p)
-        size = os.path.getsize(p)
-        for name, ent in hdr.items():
-            if name == "__metadata__":
-                continue
-            a, b = (int(v) for v in ent["data_offsets"])
-            if b < a or base + b > size:
-                raise ValueError(f"{p}: tensor {name} claims bytes {a}..{b}, which runs past the "
-                                 f"file ({size} bytes). Refusing to read past the end.")
-            if ent["dtype"] not in ST_DTYPES:
-                raise ValueError(f"{p}: tensor {name} has unknown dtype {ent['dtype']}")
-            out[name] = Tensor(p, base + a, b - a, ent["dtype"], tuple(int(x) for x in ent["shape"]))
-    return out
+    root = os.path.expanduser(model_dir)
+    shards = sorted(glob.glob(os.path.join(root, "*.safetensors")))
+    if not shards:
+        raise FileNotFoundError(f"no safetensors in {root}")
+    index = {}
+    for path in shards:
+        index.update(_shard_tensors(path))
+    return index
 
 
 def quant_for(cfg: dict, module_path: str, spec: dict | None = None) -> dict:
-    """A layer's {bits, group_size, mode}, or {} for unquantized weights.
-
-    The tensors decide first: a layer with no `scales` component is not quantized whatever
-    config.json says. Then a per-module entry of the config's quantization block, then its
-    global bits / group size (direct.py:110-142)."""
-    if spec is not None and not any("scales" in comps for comps in spec.values()):
+    """A layer's {bits, group_size, mode}, or {} for unquantized weights (direct.py:110-142):
+    weights without `scales` are unquantized whatever config.json says; otherwise the entry for
+    the module in the config's quantization block, else the block's global bits / group size."""
+    if spec is not None and all("scales" not in comps for comps in spec.values()):
         return {}
-    q = cfg.get("quantization") or cfg.get("quantization_config") or {}
-    if not q:
+    block = cfg.get("quantization") or cfg.get("quantization_config") or {}
+    if not block:
         return {}
-    v = q.get(module_path)
-    if isinstance(v, dict):
-        return {"bits": int(v["bits"]), "group_size": int(v["group_size"]),
-                "mode": v.get("mode", "affine")}
-    return {"bits": int(q.get("bits", 4)), "group_size": int(q.get("group_size", 64)),
-            "mode": q.get("mode", "affine")}
+    src = block[module_path] if isinstance(block.get(module_path), dict) else block
+    return {"bits": int(src.get("bits", 4)), "group_size": int(src.get("group_size", 64)),
+            "mode": src.get("mode", "affine")}
 
 
 @dataclass
@@ -135,79 +148,78 @@ class CheckpointManifest:
         return F.Manifest(layers=self.layers).quant(layer)
 
 
+def _expert_tensors(tensors: dict):
+    """{layer: {projection: {component: name}}} of the stacked routed-expert tensors, the infix
+    they were found under, and the projection names seen that are not SwiGLU's."""
+    by_layer, infix, other = {}, None, set()
+    for name in tensors:
+        m = _EXPERT_NAME.match(name)
+        if m is None:
+            continue
+        proj, comp = m.group("proj"), m.group("comp")
+        if proj not in F.PROJECTIONS:
+            other.add(proj)
+        elif comp in F.COMPONENTS:
+            by_layer.setdefault(int(m.group("layer")), {}).setdefault(proj, {})[comp] = name
+            infix = m.group("infix")
+    return by_layer, infix, other
+
+
+def _layer_layout(li: int, comps_of: dict, tensors: dict):
+    """(spec, expert count, [(path, offset of expert 0, bytes per expert)] in packing order) of
+    one layer: projections in F.PROJECTIONS order, components in F.COMPONENTS order."""
+    spec, segs, count = {}, [], None
+    for proj in F.PROJECTIONS:
+        if not comps_of.get(proj):
+            raise ValueError(f"layer {li} is missing {proj}; the checkpoint is incomplete")
+        spec[proj] = {}
+        for comp in (c for c in F.COMPONENTS if c in comps_of[proj]):
+            name = comps_of[proj][comp]
+            t = tensors[name]
+            if len(t.shape) < 2:
+                raise ValueError(f"{name} has shape {t.shape}; stacked expert tensors lead with E")
+            if count is None:
+                count = t.shape[0]
+            if t.shape[0] != count:
+                raise ValueError(f"layer {li}: {name} has {t.shape[0]} experts but a sibling "
+                                 f"has {count}; the layer is refused rather than guessed at")
+            dtype, isize = ST_DTYPES[t.dtype]
+            per = isize * int(np.prod(t.shape[1:], dtype=np.int64))
+            if per * count != t.nbytes:
+                raise ValueError(f"{name}: {count} x {per} != {t.nbytes} bytes on disk; "
+                                 f"the header and the data disagree")
+            spec[proj][comp] = {"shape": list(t.shape[1:]), "dtype": dtype, "nbytes": per}
+            segs.append((t.path, t.offset, per))
+    return spec, count, segs
+
+
 def expert_manifest(model_dir: str) -> CheckpointManifest:
     """Describe every routed expert of an MLX checkpoint by where its bytes already sit."""
-    d = os.path.expanduser(model_dir)
-    tensors = scan(d)
-    with open(os.path.join(d, "config.json")) as f:
+    root = os.path.expanduser(model_dir)
+    tensors = scan(root)
+    with open(os.path.join(root, "config.json")) as f:
         cfg = json.load(f)
-    layers, found_infix, foreign = {}, None, set()
-    for name in tensors:
-        for infix in EXPERT_INFIXES:
-            if infix in name:
-                break
-        else:
-            continue
-        head, tail = name.split(infix, 1)
-        li = int(head.rsplit(".", 1)[1])
-        proj, comp = tail.rsplit(".", 1)
-        if proj not in F.PROJECTIONS:
-            foreign.add(proj)
-            continue
-        if comp not in F.COMPONENTS:
-            continue
-        found_infix = infix
-        layers.setdefault(li, {}).setdefault(proj, {})[comp] = name
-    if not layers:
-        if foreign:
-            kind = "a two-layer MLP (fc1/fc2)" if foreign <= set(MLP_PROJECTIONS) else "a"
-            raise ValueError(f"{d} is a mixture-of-experts model, but its experts use {kind} "
-                             f"{'/'.join(sorted(foreign))} layout; these kernels compute "
+    by_layer, infix, other = _expert_tensors(tensors)
+    if not by_layer:
+        if other:
+            kind = "a two-layer MLP (fc1/fc2)" if other <= set(MLP_PROJECTIONS) else "a"
+            raise ValueError(f"{root} is a mixture-of-experts model, but its experts use {kind} "
+                             f"{'/'.join(sorted(other))} layout; these kernels compute "
                              f"gate/up/down (SwiGLU) experts")
-        raise ValueError(f"{d} has no MoE expert tensors (looked for "
+        raise ValueError(f"{root} has no MoE expert tensors (looked for "
                          f"{', '.join('*' + i + '*' for i in EXPERT_INFIXES)})")
-
-    man = CheckpointManifest(model_dir=d, config=cfg)
-    tk = cfg.get("num_experts_per_tok") or cfg.get("moe_topk")
-    if isinstance(tk, int) and tk > 0:
-        man.top_k = tk
-    total = 0
-    for li in sorted(layers):
-        spec, n_experts, per_expert, ordered = {}, None, 0, []
-        for proj in F.PROJECTIONS:          # projection outer, component inner: packing order
-            comps = layers[li].get(proj)
-            if not comps:
-                raise ValueError(f"layer {li} is missing {proj}; the checkpoint is incomplete")
-            spec[proj] = {}
-            for comp in F.COMPONENTS:
-                nm = comps.get(comp)
-                if nm is None:
-                    continue
-                t = tensors[nm]
-                if len(t.shape) < 2:
-                    raise ValueError(f"{nm} has shape {t.shape}; stacked expert tensors lead with E")
-                if n_experts is None:
-                    n_experts = t.shape[0]
-                elif t.shape[0] != n_experts:
-                    raise ValueError(f"layer {li}: {nm} has {t.shape[0]} experts but a sibling "
-                                     f"has {n_experts}. Refusing to guess which is right.")
-                dt, isize = ST_DTYPES[t.dtype]
-                stride = isize
-                for x in t.shape[1:]:
-                    stride *= x
-                if stride * n_experts != t.nbytes:
-                    raise ValueError(f"{nm}: {n_experts} x {stride} != {t.nbytes} bytes on disk. "
-                                     f"The header and the data disagree.")
-                spec[proj][comp] = {"shape": list(t.shape[1:]), "dtype": dt, "nbytes": stride}
-                ordered.append((t.path, t.offset, stride))
-                per_expert += stride
-        for e in range(n_experts):
-            man.segments[f"{li}:{e}"] = [(p, o + e * s, s) for p, o, s in ordered]
+    man = CheckpointManifest(model_dir=root, config=cfg)
+    top_k = cfg.get("num_experts_per_tok") or cfg.get("moe_topk")
+    man.top_k = top_k if isinstance(top_k, int) and top_k > 0 else None
+    for li in sorted(by_layer):
+        spec, count, segs = _layer_layout(li, by_layer[li], tensors)
+        per_expert = sum(n for _, _, n in segs)
+        man.segments.update({f"{li}:{e}": [(p, o + e * n, n) for p, o, n in segs]
+                             for e in range(count)})
         man.layers[str(li)] = {
-            "n_experts": n_experts, "spec": spec, "bytes_per_expert": per_expert,
-            "quant": quant_for(cfg, f"model.layers.{li}{found_infix}gate_proj", spec)}
-        total += per_expert * n_experts
-    man.total_bytes = total
+            "n_experts": count, "spec": spec, "bytes_per_expert": per_expert,
+            "quant": quant_for(cfg, f"model.layers.{li}{infix}{F.PROJECTIONS[0]}", spec)}
+        man.total_bytes += per_expert * count
     return man
 
 

@@ -32,7 +32,7 @@ import time
 import numpy as np
 
 from . import lib as L
-from .pool import ExpertPool, HostStore
+from .pool import ExpertPool, HostStore, step_requests
 
 
 def plan_full_layers(n_layers: int, n_experts: int, top_k: int, capacity: int,
@@ -65,9 +65,9 @@ class HostServedPool:
 
     def __init__(self, pool: ExpertPool, store: HostStore, copy_stream=None, depth: int = 16):
         import torch
-        if not pool._built:
+        if not pool.built:
             raise RuntimeError("build() the pool before giving it host backing")
-        if pool.admits or pool._resident:
+        if pool.admits or pool.resident:
             raise RuntimeError("host backing is given to a fresh pool, before any admission")
         t = store.tensor(pool.layer)
         E, per = pool.n_experts, pool.bytes_per_expert
@@ -150,14 +150,10 @@ class HostServedPool:
         outside the step's experts and the admissions still in flight (stream.py:957-969)."""
         torch = self._torch
         pool = self.pool
-        best = {}
-        for row in gi:
-            for r, e in enumerate(row):
-                e = int(e)
-                if 0 <= e < pool.n_experts and (e not in best or r < best[e]):
-                    best[e] = r
-        uniq = sorted(best)
-        need = pool.touch(uniq, [best[e] for e in uniq])
+        uniq, ranks = step_requests(gi)
+        keep = [i for i, e in enumerate(uniq) if 0 <= e < pool.n_experts]
+        uniq, ranks = [uniq[i] for i in keep], [ranks[i] for i in keep]
+        need = pool.touch(uniq, ranks)
         if not need:
             return
         for e, ev in list(self._pending.items()):
@@ -170,7 +166,7 @@ class HostServedPool:
         for e in need:
             t0 = time.perf_counter()
             try:
-                slot = pool._victim(protect=protect)
+                slot = pool.claim_slot(protect)
             except RuntimeError:
                 break                      # every slot holds a protected expert: serve from host
             v = pool.last_evicted
@@ -184,7 +180,7 @@ class HostServedPool:
             done.record(self.copy_stream)
             self._pending[e] = done
             protect.add(e)
-            pool._place(e, slot, t0)
+            pool.record_admission(e, slot, t0)
             pool.refill_bytes += region.nbytes
             self.admit_bytes += region.nbytes
 

@@ -32,7 +32,7 @@ import time
 import numpy as np
 
 from . import lib as L
-from .pool import ExpertPool
+from .pool import ExpertPool, step_requests
 from .spec import LayerSpec
 
 DECODE_MAX_TOKENS = 8
@@ -166,39 +166,34 @@ class StreamingSwitchGLU:
 
     # -- residency (stream.py:922-978) -------------------------------------------------------
     def ensure(self, indices, ranks=None) -> np.ndarray:
-        """Make every requested expert resident; return the slot-remapped indices."""
-        gi = np.asarray(indices).astype(np.int64)
-        best = {}
-        if ranks is not None:
-            for e, r in zip(gi.reshape(-1), np.asarray(ranks).reshape(-1)):
-                e, r = int(e), int(r)
-                if e not in best or r < best[e]:
-                    best[e] = r
-        else:
-            for row in gi.reshape(-1, gi.shape[-1]):
-                for r, e in enumerate(row):
-                    e = int(e)
-                    if e not in best or r < best[e]:
-                        best[e] = r
-        uniq = sorted(best)
-        for e in uniq:
-            if not 0 <= e < self._pool.n_experts:
-                raise KeyError(e)
-        need = self._pool.touch(uniq, [best[e] for e in uniq])
+        """Make every expert in `indices` resident and return `indices` mapped to slots.
+
+        The pool sees the step as its distinct experts in ascending id, each at the best rank
+        it was requested at (`step_requests`; ranks default to the top-k position), and admits
+        the misses in that order with the whole step protected -- the order that fixes slot
+        numbers (stream.py:922-978). A step that needs more experts than the pool holds, or names
+        an expert the layer does not have, is refused before anything is written."""
+        gi = np.asarray(indices, dtype=np.int64)
+        pool = self._pool
+        experts, best = step_requests(gi, ranks)
+        bad = [e for e in experts if not 0 <= e < pool.n_experts]
+        if bad:
+            raise KeyError(bad[0])
+        need = pool.touch(experts, best)
+        if len(need) > pool.capacity:
+            raise RuntimeError(
+                f"layer {pool.layer} needs {len(need)} experts for one step but the "
+                f"pool holds {pool.capacity}. Capacity must be at least top-k; below "
+                f"that a token evicts an expert it is still using.")
         if need:
-            if len(need) > self._pool.capacity:
-                raise RuntimeError(
-                    f"layer {self._pool.layer} needs {len(need)} experts for one step but the "
-                    f"pool holds {self._pool.capacity}. Capacity must be at least top-k; below "
-                    f"that a token evicts an expert it is still using.")
             t0 = time.perf_counter()
-            blobs = self._fetcher.fetch([(self._pool.layer, e) for e in need])
+            got = self._fetcher.fetch([(pool.layer, e) for e in need])
             self.fetch_seconds += time.perf_counter() - t0
             for e in need:
-                b = blobs[(self._pool.layer, e)]
-                self.fetch_bytes += len(b)
-                self._pool.admit(e, b, protect=uniq)
-        return self._pool.g2s[gi]
+                region = got[(pool.layer, e)]
+                self.fetch_bytes += len(region)
+                pool.admit(e, region, protect=experts)
+        return pool.g2s[gi]
 
     def refresh(self) -> bool:
         """Take the sync-free path iff every expert is resident (stream.py:1579-1603), or the

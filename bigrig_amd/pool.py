@@ -1,9 +1,8 @@
 """The bounded expert pool of one layer: HBM slots, expert<->slot tables, eviction policy.
 
-`ExpertPool` restates the residency bookkeeping of the reference's ExpertPool
-(bigrig_engine/stream.py:454-811) -- the same tables, the same free-list order, the same victim
-rules and the same errors, so the same requests produce the same slot numbers -- over slots
-that live in HBM (libbrx `brx_pool_*`). Where the reference wrote an MLX slot tensor
+`ExpertPool` keeps the residency of the reference's ExpertPool (bigrig_engine/stream.py:454-811)
+-- the same slot-assignment and victim rules and the same errors, so the same requests produce
+the same slot numbers -- over slots that live in HBM (libbrx `brx_pool_*`). Where the reference wrote an MLX slot tensor
 (`self._slots[...][slot] = arrays[i]`, stream.py:765-769) this issues an asynchronous copy of
 the expert's packed bytes from pinned host memory on a side stream; the library orders that
 copy after every forward that may still read the slot, and the next forward after the copy.
@@ -14,7 +13,6 @@ copy after every forward that may still read the slot, and the next forward afte
 """
 from __future__ import annotations
 
-import inspect
 import os
 import time
 from dataclasses import dataclass
@@ -243,13 +241,37 @@ class DeviceSlots:
             self.handle = None
 
 
-class ExpertPool:
-    """C slots of expert weights for ONE layer plus the tables saying which expert is where.
+def step_requests(indices, ranks=None):
+    """The distinct experts of one step in ascending id, each with the best (lowest) router rank
+    it was requested at: the order and the rank the pool is told about them (stream.py:933-950).
+    `ranks` defaults to the position along the last axis of `indices` (the router's top-k
+    order)."""
+    gi = np.asarray(indices, dtype=np.int64)
+    if ranks is None:
+        rk = np.broadcast_to(np.arange(gi.shape[-1], dtype=np.int64), gi.shape) if gi.ndim else gi * 0
+    else:
+        rk = np.asarray(ranks, dtype=np.int64)
+    ids, rs = gi.reshape(-1), rk.reshape(-1)
+    if ids.size == 0:
+        return [], []
+    order = np.lexsort((rs, ids))                     # by id, then rank
+    uniq, first = np.unique(ids[order], return_index=True)
+    return uniq.tolist(), rs[order][first].tolist()
 
-    Bookkeeping restated from stream.py:454-811: `g2s`/`s2g` int32 tables (-1 = absent), a free
-    list popped from the end (so the first admission takes slot C-1), victims from the policy
-    with the current step's experts excluded, else the least recently admitted unprotected
-    slot, and every error raised before a slot is touched.
+
+class ExpertPool:
+    """C slots of expert weights for ONE layer and the tables that say which expert is where.
+
+    The residency rules are the reference's (stream.py:454-811), since they decide every slot
+    number a forward looks up:
+      * g2s [E] and s2g [C] int32 tables, -1 for absent / free;
+      * slots never used are handed out from the top down (the first admission takes slot
+        C - 1), and a slot freed by an eviction goes straight to the admission that caused it;
+      * a victim is the policy's, unless it is protected (the step's own experts) or the policy
+        cannot exclude; then the unprotected slot admitted longest ago;
+      * every error is raised before a slot or a table is touched.
+    The tables here are plain arrays: `admitted_at[slot]` orders slots by admission for the
+    fallback, `_fresh` counts the never-used slots left.
     """
 
     def __init__(self, layer: int, spec: LayerSpec, capacity: int, policy: str = "lfuda",
@@ -259,32 +281,26 @@ class ExpertPool:
             raise ValueError(
                 f"capacity must be in [1, {n_experts}], got {capacity}. A pool larger than the "
                 f"expert count wastes memory; a pool of zero cannot serve any token.")
-        self.layer, self.spec, self.n_experts, self.capacity = layer, spec, n_experts, capacity
+        self.layer, self.spec = int(layer), spec
+        self.n_experts, self.capacity = int(n_experts), int(capacity)
         self.policy = make_policy(policy, capacity, n_experts)
-        try:
-            self._policy_excludes = "exclude" in inspect.signature(self.policy.victim).parameters
-        except (TypeError, ValueError):
-            self._policy_excludes = False
-        self._slot_tick = np.zeros(capacity, dtype=np.int64)
-        self._tick = 0
         self.g2s = np.full(n_experts, -1, dtype=np.int32)
         self.s2g = np.full(capacity, -1, dtype=np.int32)
-        self._g2s_dirty = True
-        self._free = list(range(capacity))
-        self._resident = 0
-        self._pending_rank = {}
-        self.hits = 0
-        self.misses = 0
+        self.admitted_at = np.zeros(capacity, dtype=np.int64)
+        self._fresh = self.capacity
+        self._admissions = 0
+        self.resident = 0               # experts in slots (counted: read per layer per token)
+        self._table_stale = True
+        self.miss_ranks = {}            # rank of each miss of the latest touch(), for admission
         self.uses = np.zeros(n_experts, dtype=np.int64)
-        self.admits = 0
-        self.evicts = 0
+        self.hits = self.misses = self.admits = self.evicts = 0
         self.admit_seconds = 0.0
         self.refill_bytes = 0
+        self.last_evicted = -1          # the expert the latest claim_slot() evicted, -1 if none
+        self.host_served = False        # set by HostServedPool: entries are then set one by one
         self._slots = slots
         self._device = device
-        self._built = False
-        self.last_evicted = -1      # expert the latest _victim() call evicted (-1: a free slot)
-        self.host_served = False    # set by HostServedPool: table entries are then set one by one
+        self.built = False
 
     # -- construction -------------------------------------------------------
     @property
@@ -295,7 +311,7 @@ class ExpertPool:
         """Allocate the C slots in HBM (ExpertPool.build, stream.py:570-597)."""
         if self._slots is None:
             self._slots = DeviceSlots(self.spec, self.capacity, self._device)
-        self._built = True
+        self.built = True
         return self
 
     @property
@@ -305,66 +321,62 @@ class ExpertPool:
     def nbytes(self) -> int:
         return self.capacity * self.bytes_per_expert
 
+
     # -- residency ----------------------------------------------------------
     def slot_of(self, e: int) -> int:
         return int(self.g2s[e])
 
     def touch(self, experts, ranks=None) -> list:
-        """Record a reference to each expert and return those NOT resident (stream.py:622-642)."""
-        need, nrank = [], []
-        ranks = list(ranks) if ranks is not None else [0] * len(experts)
-        for e, r in zip(experts, ranks):
-            e, r = int(e), int(r)
-            self.uses[e] += 1
-            if self.g2s[e] >= 0:
-                self.hits += 1
-                self.policy.touch(e, r)
-            else:
-                self.misses += 1
-                need.append(e)
-                nrank.append(r)
-        self._pending_rank = dict(zip(need, nrank))
+        """Count a request for each expert; tell the policy about the resident ones (in the
+        given order) and return the others, the misses (stream.py:622-642)."""
+        ex = np.asarray(experts, dtype=np.int64).reshape(-1)
+        rk = np.zeros_like(ex) if ranks is None else np.asarray(ranks, dtype=np.int64).reshape(-1)
+        np.add.at(self.uses, ex, 1)
+        present = self.g2s[ex] >= 0
+        self.hits += int(present.sum())
+        self.misses += int((~present).sum())
+        for e, r in zip(ex[present].tolist(), rk[present].tolist()):
+            self.policy.touch(e, r)
+        need = ex[~present].tolist()
+        self.miss_ranks = dict(zip(need, rk[~present].tolist()))
         return need
 
-    def _victim(self, protect=()) -> int:
-        """Free a slot (stream.py:644-690): the free list first, then the policy's victim
-        outside `protect`, else the least recently admitted unprotected slot."""
+    def claim_slot(self, protect=()) -> int:
+        """A slot for the next admission (stream.py:644-690): a never-used one while any is
+        left, else the slot of an evicted expert."""
         self.last_evicted = -1
-        if self._free:
-            return self._free.pop()
-        protect = {int(x) for x in protect}
-        ev = -1
-        v = (self.policy.victim(exclude=protect) if self._policy_excludes
-             else self.policy.victim())
-        if v is not None and v >= 0 and v not in protect and self.g2s[v] >= 0:
-            ev = int(v)
-        if ev < 0:
-            best, best_t = -1, None
-            for slot in range(self.capacity):
-                g = int(self.s2g[slot])
-                if g < 0 or g in protect:
-                    continue
-                if best_t is None or self._slot_tick[slot] < best_t:
-                    best, best_t = g, self._slot_tick[slot]
-            ev = best
-        if ev < 0:
-            raise RuntimeError(
-                f"layer {self.layer}: every one of {self.capacity} slots holds an expert this "
-                f"step still needs. Capacity must be at least top-k.")
-        slot = int(self.g2s[ev])
-        self.last_evicted = ev
-        self.policy.evicted(ev)
-        self.g2s[ev] = -1
+        if self._fresh:
+            self._fresh -= 1
+            return self._fresh
+        keep = {int(x) for x in protect}
+        pol = self.policy
+        v = pol.victim(exclude=keep) if pol.excludes else pol.victim()
+        ok = v is not None and 0 <= v < self.n_experts and v not in keep and self.g2s[v] >= 0
+        if not ok:
+            occupied = self.s2g >= 0
+            if keep:
+                occupied &= ~np.isin(self.s2g, np.fromiter(keep, dtype=np.int64))
+            cand = np.flatnonzero(occupied)
+            if cand.size == 0:
+                raise RuntimeError(
+                    f"layer {self.layer}: every one of {self.capacity} slots holds an expert this "
+                    f"step still needs. Capacity must be at least top-k.")
+            v = int(self.s2g[cand[np.argmin(self.admitted_at[cand])]])
+        v = int(v)
+        slot = int(self.g2s[v])
+        pol.evicted(v)
+        self.g2s[v] = -1
         self.s2g[slot] = -1
-        self._resident -= 1
-        self._g2s_dirty = True
+        self.resident -= 1
+        self._table_stale = True
         self.evicts += 1
+        self.last_evicted = v
         return slot
 
     def admit(self, e: int, blob, protect=()) -> int:
-        """Place expert e's packed bytes into a slot and return the slot (stream.py:692-705,
+        """Write expert e's packed bytes into a slot and return the slot (stream.py:692-705,
         757-780). `blob` is a PinnedRegion or any bytes-like object."""
-        if not self._built:
+        if not self.built:
             raise RuntimeError("build() must run before admit()")
         want = self.bytes_per_expert
         if len(blob) != want:
@@ -372,56 +384,56 @@ class ExpertPool:
                 f"layer {self.layer} expert {e}: the manifest accounts for {want} bytes but the "
                 f"region supplied {len(blob)}. Refusing to write a partially-filled slot.")
         t0 = time.perf_counter()
-        slot = self._victim(protect=protect)
+        slot = self.claim_slot(protect)
         self.refill_bytes += self._slots.write(slot, blob)
-        self._place(e, slot, t0)
+        self.record_admission(e, slot, t0)
         return slot
 
     def admit_device(self, e: int, dev_ptr: int, protect=(), src_stream=None) -> int:
-        """Admit from device memory (an expert staged on the GPU, stream.py:957-961). The copy
-        is ordered after the work queued on `src_stream` (default: the current stream), which
-        is where the staged bytes were written."""
-        if not self._built:
+        """Admit from device memory (an expert staged on the GPU, stream.py:957-961), ordered
+        after the work queued on `src_stream` (default: the current stream), which wrote it."""
+        if not self.built:
             raise RuntimeError("build() must run before admit()")
         t0 = time.perf_counter()
-        slot = self._victim(protect=protect)
+        slot = self.claim_slot(protect)
         self._slots.write_device(slot, dev_ptr, self.bytes_per_expert, src_stream)
-        self._place(e, slot, t0)
+        self.record_admission(e, slot, t0)
         return slot
 
-    def _place(self, e: int, slot: int, t0: float) -> None:
+    def record_admission(self, e: int, slot: int, t0: float) -> None:
+        """Tables, admission order and policy after expert e was placed in `slot`."""
+        e, slot = int(e), int(slot)
         if self.s2g[slot] < 0:
-            self._resident += 1
+            self.resident += 1
         self.g2s[e] = slot
         self.s2g[slot] = e
-        self._g2s_dirty = True
-        self._tick += 1
-        self._slot_tick[slot] = self._tick
-        self.policy.admit(e, int(self._pending_rank.get(e, 0)))
+        self._table_stale = True
+        self._admissions += 1
+        self.admitted_at[slot] = self._admissions
+        self.policy.admit(e, int(self.miss_ranks.get(e, 0)))
         self.admits += 1
         self.admit_seconds += time.perf_counter() - t0
 
     @property
     def full(self) -> bool:
-        """Every expert resident, so no request can miss (stream.py:782-789). Counted."""
-        return self.capacity == self.n_experts and self._resident == self.n_experts
+        """Every expert resident, so no request can miss (stream.py:782-789)."""
+        return self.capacity == self.n_experts and self.resident == self.n_experts
 
     def g2s_device(self, stream) -> None:
         """Upload the table when residency changed (stream.py:791-797); stream-ordered."""
-        if self._g2s_dirty and not self.host_served:
+        if self._table_stale and not self.host_served:
             self._slots.set_table(self.g2s, stream)
-            self._g2s_dirty = False
+            self._table_stale = False
 
     def stats(self) -> dict:
-        tot = self.hits + self.misses
+        n = self.hits + self.misses
         return {"layer": self.layer, "capacity": self.capacity, "n_experts": self.n_experts,
-                "hits": self.hits, "misses": self.misses,
-                "miss_rate": self.misses / tot if tot else 0.0,
+                "hits": self.hits, "misses": self.misses, "miss_rate": self.misses / n if n else 0.0,
                 "admits": self.admits, "evicts": self.evicts,
-                "resident_bytes": self._resident * self.bytes_per_expert,
+                "resident_bytes": self.resident * self.bytes_per_expert,
                 "refill_bytes": self.refill_bytes, "admit_seconds": self.admit_seconds}
 
     def close(self) -> None:
         if self._slots is not None and hasattr(self._slots, "close"):
             self._slots.close()
-        self._built = False
+        self.built = False

@@ -2,7 +2,8 @@
 
 The reference studies hit rates by replaying routing traces through its policies in Python
 (bigrig_engine/pool.py:219-358). `misses` / `trace_misses` / `evaluate` here run the same
-replay (simulate()'s contract; LRU, LFUDA, and the Belady bound) in C++, every (capacity,
+replay (simulate()'s contract; LRU, LFUDA, the rest of the reference's policy zoo -- windowed
+LFU, S3-FIFO, ARC, LIRS, gaterank, coact -- and the Belady bound) in C++, every (capacity,
 layer) cell of a sweep on its own thread, with results equal to `policy.simulate` /
 `policy.belady` to the request. The library is host-only; it fails loudly when unbuilt.
 """
@@ -14,7 +15,8 @@ import os
 import numpy as np
 
 LIB = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libbrx_replay.so")
-POLICY_IDS = {"lru": 0, "lfuda": 1, "belady": 2}
+POLICY_IDS = {"lru": 0, "lfuda": 1, "belady": 2, "wlfu": 3, "windowed_lfu": 3, "s3fifo": 4,
+              "arc": 5, "lirs": 6, "gaterank": 7, "coact": 8}
 
 
 class LfudaParams(C.Structure):

@@ -20,6 +20,12 @@ extern "C" {
 #define BRX_POLICY_LRU     0  /* least recently used (pool.py:53-72) */
 #define BRX_POLICY_LFUDA   1  /* LFU with dynamic aging (policies/lfuda.py:67-161) */
 #define BRX_POLICY_BELADY  2  /* optimal offline bound, furthest next use (pool.py:282-316) */
+#define BRX_POLICY_WLFU    3  /* fewest uses in the last 128 requests (pool.py:75-118)       */
+#define BRX_POLICY_S3FIFO  4  /* S3-FIFO, 10% probation, ghost ids (policies/s3fifo.py)      */
+#define BRX_POLICY_ARC     5  /* adaptive replacement cache (policies/arc.py)                */
+#define BRX_POLICY_LIRS    6  /* LIRS, 5% HIR, history 25% of capacity (policies/lirs.py)    */
+#define BRX_POLICY_GATERANK 7 /* recency + 16 x linear top-8 rank bonus (policies/gaterank.py) */
+#define BRX_POLICY_COACT   8  /* self-use + windowed co-activation (policies/coact.py)       */
 
 /* LFUDA knobs (policies/lfuda.py:75-101): credit(rank) = 1 + rank_weight / (1 + rank)
  * (1 when rank_weight is 0); count saturates at fcap (no cap when fcap <= 0); an evicted

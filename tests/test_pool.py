@@ -75,21 +75,21 @@ def test_lfuda_known_answers():
     """Hand-worked LFUDA: count+1 per use, key = L + count, victim = min (key, last tick),
     L rises to the evicted key, a ghost keeps half its count."""
     p = P.LFUDA(2, 8)
-    p.admit(1); p.admit(2); p.touch(1)          # cnt 1:2, 2:1; keys 2, 1
+    p.admit(1); p.admit(2); p.touch(1)          # credit 1:2, 2:1; priorities 2, 1
     assert p.victim() == 2
-    p.evicted(2)                                # L = 1; ghost cnt(2) = 0.5
-    assert p.L == 1.0 and p.cnt[2] == 0.5
-    p.admit(3)                                  # key(3) = 1 + 1 = 2, tick later than 1's
-    assert p.key[3] == 2.0 and p.victim() == 1  # tie on key 2: the older tick goes
+    p.evicted(2)                                # age = 1; ghost credit(2) = 0.5
+    assert p.age == 1.0 and p.credit[2] == 0.5
+    p.admit(3)                                  # prio(3) = 1 + 1 = 2, used later than 1
+    assert p.prio[3] == 2.0 and p.victim() == 1  # tie on priority 2: the older use goes
     assert p.victim(exclude={1}) == 3
     assert p.victim(exclude={1, 3}) == -1
     p.evicted(1)
-    p.admit(2)                                  # ghost: 0.5 + 1 = 1.5, key = L + 1.5 = 3.5
-    assert p.cnt[2] == 1.5 and p.key[2] == pytest.approx(3.5)
-    # the count saturates at 12
+    p.admit(2)                                  # ghost: 0.5 + 1 = 1.5, prio = age + 1.5 = 3.5
+    assert p.credit[2] == 1.5 and p.prio[2] == pytest.approx(3.5)
+    # the credit saturates at 12
     for _ in range(20):
         p.touch(3)
-    assert p.cnt[3] == 12.0
+    assert p.credit[3] == 12.0
 
 
 def _frontier():
@@ -198,7 +198,7 @@ def test_protected_experts_are_never_evicted_and_errors():
 def test_churn_pool_and_policy_agree():
     """200 steps of 8 experts out of 32 at C=12 (tests/test_stream.py:148-184)."""
     pd = fresh(12, 32)
-    assert pd._policy_excludes
+    assert pd.policy.excludes
     rng = np.random.default_rng(0)
     for _ in range(200):
         want = sorted(rng.choice(32, size=8, replace=False).tolist())
@@ -206,18 +206,18 @@ def test_churn_pool_and_policy_agree():
             pd.admit(e, BLOCK, protect=want)
         assert all(pd.g2s[e] >= 0 for e in want)
     pool_r = {int(e) for e in range(32) if pd.g2s[e] >= 0}
-    assert pool_r == set(pd.policy.resident)
+    assert pool_r == set(np.flatnonzero(pd.policy.held).tolist())
     assert pd.policy.victim() in pool_r
-    assert pd.policy.L <= pd.evicts * 1.2 + 1
+    assert pd.policy.age <= pd.evicts * 1.2 + 1
     assert all(pd.g2s[pd.s2g[s]] == s for s in range(12) if pd.s2g[s] >= 0)
     # a policy without exclude= (LRU): the pool chooses for itself, and the views still agree
     pl = fresh(12, 32, policy="lru")
-    assert not pl._policy_excludes
+    assert not pl.policy.excludes
     for _ in range(120):
         want = sorted(rng.choice(32, size=8, replace=False).tolist())
         for e in pl.touch(want, list(range(8))):
             pl.admit(e, BLOCK, protect=want)
-    assert {int(e) for e in range(32) if pl.g2s[e] >= 0} == set(pl.policy.od.keys())
+    assert {int(e) for e in range(32) if pl.g2s[e] >= 0} == set(np.flatnonzero(pl.policy.held).tolist())
 
 
 def test_residency_is_counted():
@@ -226,12 +226,12 @@ def test_residency_is_counted():
     for e in range(8):
         pc.touch([e], [0])
         pc.admit(e, BLOCK)
-    assert pc.full and pc._resident == int((pc.g2s >= 0).sum())
+    assert pc.full and pc.resident == int((pc.g2s >= 0).sum())
     pe = fresh(4, 8)
     for e in range(8):
         pe.touch([e], [0])
         pe.admit(e, BLOCK)
-    assert not pe.full and pe._resident == int((pe.g2s >= 0).sum()) == 4
+    assert not pe.full and pe.resident == int((pe.g2s >= 0).sum()) == 4
 
 
 def test_device_table_uploads_only_on_change():
@@ -284,7 +284,7 @@ def test_ensure_order_rules_fix_slot_numbers():
     assert slots.tolist() == [[3, 5, 4, 5]]
     assert [w[0] for w in pool.device.writes] == [5, 4, 3]
     # best rank: expert 3 appears at ranks 1 and 3, the policy sees rank 1
-    assert pool._pending_rank == {3: 1, 5: 2, 9: 0}
+    assert pool.miss_ranks == {3: 1, 5: 2, 9: 0}
     # a step that needs more experts than the pool holds is refused before any write
     n = len(pool.device.writes)
     with pytest.raises(RuntimeError, match="pool holds"):
