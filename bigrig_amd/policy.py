@@ -8,8 +8,8 @@ position in the router's top-k for the request. A policy whose `excludes` is Tru
 victim itself when the policy names a protected one (stream.py:644-690).
 
 Every policy here keeps its per-expert state in arrays indexed by expert id (E <= 512) and picks
-its victim as a lexicographic minimum over a mask of candidates; ordered lists (LRU lists,
-FIFO queues, the LIRS stack) are a membership code per expert plus the clock value at which it
+its victim as a lexicographic minimum over its candidates; ordered lists (LRU lists, FIFO
+queues, the LIRS stack) are a membership code per expert plus the clock value at which it
 entered its list, so "oldest of list X" is the smallest entry stamp among X's members. The
 rules -- which decide which expert leaves and therefore every slot number a pool hands out --
 are those of the reference's policies:
@@ -74,25 +74,33 @@ def _argmin2(mask: np.ndarray, primary, secondary: np.ndarray) -> int:
 
 
 class _Clocked(Policy):
-    """A clock and, per expert, whether the policy counts it resident and when it last was used
-    (the tie-break of every policy below)."""
+    """A clock, the set of experts the policy counts resident, and per expert (a list indexed
+    by expert id) the clock value of its last use -- the tie-break of every policy below. The
+    per-step policies keep plain lists: a pool consults them for a handful of experts per layer
+    and token, where array-library calls would cost more than the work."""
 
     def __init__(self, capacity, n_experts):
         super().__init__(capacity, n_experts)
         self.clock = 0
-        self.held = np.zeros(self.n_experts, dtype=bool)
-        self.used_at = np.zeros(self.n_experts, dtype=np.int64)
+        self.held = set()
+        self.used_at = [0] * self.n_experts
 
     def _stamp(self, e: int) -> None:
         self.clock += 1
         self.used_at[e] = self.clock
 
-    def _mask(self, exclude) -> np.ndarray:
-        m = self.held.copy()
-        if exclude:
-            ex = np.fromiter((int(x) for x in exclude), dtype=np.int64)
-            m[ex[(ex >= 0) & (ex < self.n_experts)]] = False
-        return m
+    def _lowest(self, primary, exclude=()) -> int:
+        """The held expert outside `exclude` with the smallest (primary[e], used_at[e])
+        (primary None: used_at alone), -1 if there is none."""
+        used = self.used_at
+        best, bp, bu = -1, 0.0, 0
+        for e in self.held:
+            if exclude and e in exclude:
+                continue
+            p = primary[e] if primary is not None else 0.0
+            if best < 0 or p < bp or (p == bp and used[e] < bu):
+                best, bp, bu = e, p, used[e]
+        return best
 
 
 class LRU(_Clocked):
@@ -100,21 +108,21 @@ class LRU(_Clocked):
     name = "lru"
 
     def admit(self, e, rank=0):
-        self.held[e] = True
+        self.held.add(e)
         self._stamp(e)
 
     def touch(self, e, rank=0):
         self._stamp(e)
 
     def victim(self, exclude=()):
-        return _argmin2(self.held, None, self.used_at)
+        return self._lowest(None)
 
     def evicted(self, e):
-        self.held[e] = False
+        self.held.discard(e)
 
 
 class LFUDA(_Clocked):
-    """LFU with dynamic aging (policies/lfuda.py:67-161), over arrays.
+    """LFU with dynamic aging (policies/lfuda.py:67-161), over per-expert lists.
 
     credit[e] accumulates per use (saturating at fcap) and survives eviction scaled by
     ghost_decay; prio[e] = age at the last use + credit; the victim is the resident expert with
@@ -131,20 +139,20 @@ class LFUDA(_Clocked):
         self.fcap = None if fcap is None else float(fcap)
         self.ghost_decay = float(ghost_decay)
         self.age = 0.0
-        self.credit = np.zeros(self.n_experts, dtype=np.float64)
-        self.prio = np.zeros(self.n_experts, dtype=np.float64)
+        self.credit = [0.0] * self.n_experts
+        self.prio = [0.0] * self.n_experts
 
     def _use(self, e: int, rank: int) -> None:
         self._stamp(e)
         gain = 1.0 if self.rank_weight == 0.0 else 1.0 + self.rank_weight / (1.0 + rank)
-        c = float(self.credit[e]) + gain
+        c = self.credit[e] + gain
         if self.fcap is not None and c > self.fcap:
             c = self.fcap
         self.credit[e] = c
         self.prio[e] = self.age + c
 
     def admit(self, e, rank=0):
-        self.held[e] = True
+        self.held.add(e)
         if not self.keep_ghost:
             self.credit[e] = 0.0
         self._use(e, rank)
@@ -153,12 +161,12 @@ class LFUDA(_Clocked):
         self._use(e, rank)
 
     def victim(self, exclude=()):
-        return _argmin2(self._mask(exclude), self.prio, self.used_at)
+        return self._lowest(self.prio, exclude)
 
     def evicted(self, e):
-        if self.held[e]:
-            self.age = max(self.age, float(self.prio[e]))
-        self.held[e] = False
+        if e in self.held:
+            self.age = max(self.age, self.prio[e])
+        self.held.discard(e)
         if not self.keep_ghost:
             self.credit[e] = 0.0
         elif self.ghost_decay != 1.0:
@@ -173,7 +181,7 @@ class WindowedLFU(_Clocked):
         super().__init__(capacity, n_experts)
         self.window = int(window)
         self.recent: deque = deque()
-        self.uses = np.zeros(self.n_experts, dtype=np.int64)
+        self.uses = [0] * self.n_experts
 
     def _use(self, e):
         self._stamp(e)
@@ -183,17 +191,17 @@ class WindowedLFU(_Clocked):
             self.uses[self.recent.popleft()] -= 1
 
     def admit(self, e, rank=0):
-        self.held[e] = True
+        self.held.add(e)
         self._use(e)
 
     def touch(self, e, rank=0):
         self._use(e)
 
     def victim(self, exclude=()):
-        return _argmin2(self.held, self.uses, self.used_at)
+        return self._lowest(self.uses)
 
     def evicted(self, e):
-        self.held[e] = False
+        self.held.discard(e)
 
 
 class _Lists(Policy):

@@ -247,13 +247,26 @@ def step_requests(indices, ranks=None):
     `ranks` defaults to the position along the last axis of `indices` (the router's top-k
     order)."""
     gi = np.asarray(indices, dtype=np.int64)
+    if ranks is None and gi.ndim >= 1 and gi.size <= 256:   # a decode step: plain loops
+        best = {}
+        for row in gi.reshape(-1, gi.shape[-1]).tolist():
+            for r, e in enumerate(row):
+                if r < best.get(e, r + 1):
+                    best[e] = r
+        uniq = sorted(best)
+        return uniq, [best[e] for e in uniq]
     if ranks is None:
         rk = np.broadcast_to(np.arange(gi.shape[-1], dtype=np.int64), gi.shape) if gi.ndim else gi * 0
     else:
         rk = np.asarray(ranks, dtype=np.int64)
     ids, rs = gi.reshape(-1), rk.reshape(-1)
-    if ids.size == 0:
-        return [], []
+    if ids.size <= 256:                                # a decode step: a dict is cheapest
+        best = {}
+        for e, r in zip(ids.tolist(), rs.tolist()):
+            if r < best.get(e, r + 1):
+                best[e] = r
+        uniq = sorted(best)
+        return uniq, [best[e] for e in uniq]
     order = np.lexsort((rs, ids))                     # by id, then rank
     uniq, first = np.unique(ids[order], return_index=True)
     return uniq.tolist(), rs[order][first].tolist()
@@ -287,6 +300,7 @@ class ExpertPool:
         self.g2s = np.full(n_experts, -1, dtype=np.int32)
         self.s2g = np.full(capacity, -1, dtype=np.int32)
         self.admitted_at = np.zeros(capacity, dtype=np.int64)
+        self._bpe = spec.bytes_per_expert
         self._fresh = self.capacity
         self._admissions = 0
         self.resident = 0               # experts in slots (counted: read per layer per token)
@@ -305,7 +319,7 @@ class ExpertPool:
     # -- construction -------------------------------------------------------
     @property
     def bytes_per_expert(self) -> int:
-        return self.spec.bytes_per_expert
+        return self._bpe
 
     def build(self):
         """Allocate the C slots in HBM (ExpertPool.build, stream.py:570-597)."""
@@ -329,16 +343,20 @@ class ExpertPool:
     def touch(self, experts, ranks=None) -> list:
         """Count a request for each expert; tell the policy about the resident ones (in the
         given order) and return the others, the misses (stream.py:622-642)."""
-        ex = np.asarray(experts, dtype=np.int64).reshape(-1)
-        rk = np.zeros_like(ex) if ranks is None else np.asarray(ranks, dtype=np.int64).reshape(-1)
-        np.add.at(self.uses, ex, 1)
-        present = self.g2s[ex] >= 0
-        self.hits += int(present.sum())
-        self.misses += int((~present).sum())
-        for e, r in zip(ex[present].tolist(), rk[present].tolist()):
-            self.policy.touch(e, r)
-        need = ex[~present].tolist()
-        self.miss_ranks = dict(zip(need, rk[~present].tolist()))
+        ex = [int(e) for e in experts]
+        rk = [0] * len(ex) if ranks is None else [int(r) for r in ranks]
+        table, uses, pol = self.g2s, self.uses, self.policy
+        need, miss_ranks = [], {}
+        for e, r in zip(ex, rk):
+            uses[e] += 1
+            if table[e] >= 0:
+                pol.touch(e, r)
+            else:
+                need.append(e)
+                miss_ranks[e] = r
+        self.hits += len(ex) - len(need)
+        self.misses += len(need)
+        self.miss_ranks = miss_ranks
         return need
 
     def claim_slot(self, protect=()) -> int:

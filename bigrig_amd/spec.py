@@ -1,6 +1,7 @@
 """One MoE layer's shape, quantization and routing rule, and the C descriptor built from it."""
 from __future__ import annotations
 
+import functools
 from dataclasses import dataclass, field
 
 from . import formats as F
@@ -58,8 +59,9 @@ class LayerSpec:
         inter = self.shared_inter if shared else self.inter
         return F.expert_spec(self.hidden, inter, self.quant, self.has_bias)
 
-    @property
+    @functools.cached_property
     def bytes_per_expert(self) -> int:
+        """Packed bytes of one routed expert (computed once: it is read per admission)."""
         return F.spec_bytes(self.expert_spec())
 
     @property

@@ -206,7 +206,7 @@ def test_churn_pool_and_policy_agree():
             pd.admit(e, BLOCK, protect=want)
         assert all(pd.g2s[e] >= 0 for e in want)
     pool_r = {int(e) for e in range(32) if pd.g2s[e] >= 0}
-    assert pool_r == set(np.flatnonzero(pd.policy.held).tolist())
+    assert pool_r == pd.policy.held
     assert pd.policy.victim() in pool_r
     assert pd.policy.age <= pd.evicts * 1.2 + 1
     assert all(pd.g2s[pd.s2g[s]] == s for s in range(12) if pd.s2g[s] >= 0)
@@ -217,7 +217,7 @@ def test_churn_pool_and_policy_agree():
         want = sorted(rng.choice(32, size=8, replace=False).tolist())
         for e in pl.touch(want, list(range(8))):
             pl.admit(e, BLOCK, protect=want)
-    assert {int(e) for e in range(32) if pl.g2s[e] >= 0} == set(np.flatnonzero(pl.policy.held).tolist())
+    assert {int(e) for e in range(32) if pl.g2s[e] >= 0} == pl.policy.held
 
 
 def test_residency_is_counted():
