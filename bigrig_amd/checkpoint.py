@@ -32,8 +32,8 @@ EXPERT_INFIXES = (".mlp.switch_mlp.", ".mlp.experts.", ".feed_forward.experts.",
                   ".ffn.switch_mlp.", ".ffn.experts.", ".mixer.switch_mlp.",
                   ".block_sparse_moe.switch_mlp.", ".block_sparse_moe.experts.")
 
-# the two-layer MLP expert layout some families use; these kernels compute SwiGLU experts only
-MLP_PROJECTIONS = ("fc1", "fc2")
+# the two-layer MLP expert layout some families use (fc2(silu(fc1 x)), stream.py:57, 1167-1169)
+MLP_PROJECTIONS = F.MLP_PROJECTIONS
 
 # safetensors dtype -> (dtype name in the expert spec, bytes per element)
 ST_DTYPES = {"F64": ("float64", 8), "F32": ("float32", 4), "F16": ("float16", 2),
@@ -149,15 +149,17 @@ class CheckpointManifest:
 
 
 def _expert_tensors(tensors: dict):
-    """{layer: {projection: {component: name}}} of the stacked routed-expert tensors, the infix
-    they were found under, and the projection names seen that are not SwiGLU's."""
+    """{layer: {projection: {component: name}}} of the stacked routed-expert tensors (gated
+    gate/up/down or two-layer fc1/fc2), the infix they were found under, and the projection
+    names seen that are neither."""
+    known = set(F.PROJECTIONS) | set(MLP_PROJECTIONS)
     by_layer, infix, other = {}, None, set()
     for name in tensors:
         m = _EXPERT_NAME.match(name)
         if m is None:
             continue
         proj, comp = m.group("proj"), m.group("comp")
-        if proj not in F.PROJECTIONS:
+        if proj not in known:
             other.add(proj)
         elif comp in F.COMPONENTS:
             by_layer.setdefault(int(m.group("layer")), {}).setdefault(proj, {})[comp] = name
@@ -167,9 +169,11 @@ def _expert_tensors(tensors: dict):
 
 def _layer_layout(li: int, comps_of: dict, tensors: dict):
     """(spec, expert count, [(path, offset of expert 0, bytes per expert)] in packing order) of
-    one layer: projections in F.PROJECTIONS order, components in F.COMPONENTS order."""
+    one layer: projections in F.PROJECTIONS (or fc1, fc2) order, components in F.COMPONENTS
+    order."""
+    projections = MLP_PROJECTIONS if set(comps_of) <= set(MLP_PROJECTIONS) else F.PROJECTIONS
     spec, segs, count = {}, [], None
-    for proj in F.PROJECTIONS:
+    for proj in projections:
         if not comps_of.get(proj):
             raise ValueError(f"layer {li} is missing {proj}; the checkpoint is incomplete")
         spec[proj] = {}
@@ -202,10 +206,9 @@ def expert_manifest(model_dir: str) -> CheckpointManifest:
     by_layer, infix, other = _expert_tensors(tensors)
     if not by_layer:
         if other:
-            kind = "a two-layer MLP (fc1/fc2)" if other <= set(MLP_PROJECTIONS) else "a"
-            raise ValueError(f"{root} is a mixture-of-experts model, but its experts use {kind} "
-                             f"{'/'.join(sorted(other))} layout; these kernels compute "
-                             f"gate/up/down (SwiGLU) experts")
+            raise ValueError(f"{root} is a mixture-of-experts model, but its experts use a "
+                             f"{'/'.join(sorted(other))} layout; these kernels compute gated "
+                             f"gate/up/down or two-layer fc1/fc2 experts")
         raise ValueError(f"{root} has no MoE expert tensors (looked for "
                          f"{', '.join('*' + i + '*' for i in EXPERT_INFIXES)})")
     man = CheckpointManifest(model_dir=root, config=cfg)
@@ -218,7 +221,7 @@ def expert_manifest(model_dir: str) -> CheckpointManifest:
                              for e in range(count)})
         man.layers[str(li)] = {
             "n_experts": count, "spec": spec, "bytes_per_expert": per_expert,
-            "quant": quant_for(cfg, f"model.layers.{li}{infix}{F.PROJECTIONS[0]}", spec)}
+            "quant": quant_for(cfg, f"model.layers.{li}{infix}{next(iter(spec))}", spec)}
         man.total_bytes += per_expert * count
     return man
 
@@ -275,12 +278,15 @@ def layer_spec(man: CheckpointManifest, layer: int, **overrides):
     from .spec import LayerSpec
     e = man.layers[str(layer)]
     q = man.quant(layer)
-    gate = e["spec"]["gate_proj"]
-    inter = int(gate["weight"]["shape"][0])
-    hidden = int(gate["weight"]["shape"][1]) * 32 // q.bits
+    two_layer = not F.is_gated(e["spec"])
+    first = e["spec"]["fc1" if two_layer else "gate_proj"]
+    inter = int(first["weight"]["shape"][0])
+    hidden = int(first["weight"]["shape"][1]) * 32 // q.bits
     kw = {"hidden": hidden, "inter": inter, "n_experts": int(e["n_experts"]),
-          "top_k": int(man.top_k or 1), "quant": q, "has_bias": "bias" in gate}
+          "top_k": int(man.top_k or 1), "quant": q, "has_bias": "bias" in first}
     kw.update(routing_from_config(man.config))
+    if two_layer:
+        kw["act"] = "silu_mlp"
     kw.update(overrides)
     spec = LayerSpec(**kw)
     if F.spec_bytes(spec.expert_spec()) != int(e["bytes_per_expert"]):

@@ -79,7 +79,7 @@ int check_desc(const brx_layer_desc* d) {
     } else {
         return fail(BRX_EINVAL, "quant_mode %d unknown", d->quant_mode);
     }
-    if (d->act != BRX_ACT_SWIGLU && d->act != BRX_ACT_SWIGLU_CLAMPED)
+    if (d->act != BRX_ACT_SWIGLU && d->act != BRX_ACT_SWIGLU_CLAMPED && d->act != BRX_ACT_SILU_MLP)
         return fail(BRX_EINVAL, "act %d unknown", d->act);
     if (d->route_mode < 0 || d->route_mode > 2) return fail(BRX_EINVAL, "route_mode %d unknown", d->route_mode);
     if (d->router_dtype != BRX_DT_F32 && d->router_dtype != BRX_DT_BF16)
@@ -693,6 +693,7 @@ int brx_dequant(const brx_layer_desc* d, const void* expert, int proj, int share
     if ((rc = ensure_device())) return rc;
     if (!expert || !out) return fail(BRX_EINVAL, "expert and out are required");
     if (proj < 0 || proj > 2) return fail(BRX_EINVAL, "proj %d outside [0, 2]", proj);
+    if (proj == 1 && d->act == BRX_ACT_SILU_MLP) return fail(BRX_EINVAL, "a two-layer expert has no projection 1");
     if (shared && !d->shared_inter) return fail(BRX_EINVAL, "layer has no shared expert");
     Layout L = make_layout(*d, shared ? d->shared_inter : d->inter);
     hipError_t e = launch_dequant(*d, L, (const uint8_t*)expert, proj, out, (hipStream_t)stream);

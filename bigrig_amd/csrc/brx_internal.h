@@ -24,11 +24,17 @@ struct Layout {
 };
 
 // Offsets in the order stream.pack_experts writes components (weight, scales, biases, bias)
-// for projections gate_proj, up_proj, down_proj (bigrig_engine/stream.py:152-164).
+// for projections gate_proj, up_proj, down_proj (bigrig_engine/stream.py:152-164). A plain
+// two-layer expert (BRX_ACT_SILU_MLP) packs fc1 then fc2: they take slots 0 and 2 and slot 1
+// is absent.
 inline Layout make_layout(const brx_layer_desc& d, int inter) {
     Layout L{};
     int64_t pos = 0;
     for (int p = 0; p < 3; ++p) {
+        if (p == 1 && d.act == BRX_ACT_SILU_MLP) {
+            L.p[1] = Proj{-1, -1, -1, -1, 0, 0};
+            continue;
+        }
         int n_out = p < 2 ? inter : d.hidden;
         int n_in = p < 2 ? d.hidden : inter;
         int64_t G = n_in / d.group_size;
@@ -178,6 +184,7 @@ __device__ __forceinline__ float silu_mul(float g, float u) { return x_sigmoid(g
 
 __device__ __forceinline__ float act_apply(int act, float g, float u, float alpha, float limit) {
     if (act == BRX_ACT_SWIGLU) return silu_mul(g, u);
+    if (act == BRX_ACT_SILU_MLP) return x_sigmoid(g, 1.0f);
     g = fminf(g, limit);
     u = fminf(fmaxf(u, -limit), limit);
     return x_sigmoid(g, alpha) * (u + 1.0f);

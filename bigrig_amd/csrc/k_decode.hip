@@ -485,13 +485,15 @@ __global__ __launch_bounds__(kThreads) void k_dec_gateup(FwdArgs a, uint16_t* __
         const int rr = (tid >> 6) * RW + g;
         const int row = min(r0 + rr, inter - 1);
 
+        // a two-layer expert (fc1 / fc2) has no up projection: only fc1's rows are read
+        const bool gated = a.act != BRX_ACT_SILU_MLP;
         Units<MODE, UPL> ug, uu;
         units_load<MODE, UPL>(base, L.p[0], row, sl, SP, ug);
-        units_load<MODE, UPL>(base, L.p[1], row, sl, SP, uu);
+        if (gated) units_load<MODE, UPL>(base, L.p[1], row, sl, SP, uu);
         float bg = 0.f, bu = 0.f;
         if (L.p[0].bias >= 0) {
             bg = bf2f(reinterpret_cast<const uint16_t*>(base + L.p[0].bias)[row]);
-            bu = bf2f(reinterpret_cast<const uint16_t*>(base + L.p[1].bias)[row]);
+            if (gated) bu = bf2f(reinterpret_cast<const uint16_t*>(base + L.p[1].bias)[row]);
         }
         PairIter pit{en.mm, 0};
         for (int i = 0; i < en.nt; ++i) {
@@ -505,11 +507,11 @@ __global__ __launch_bounds__(kThreads) void k_dec_gateup(FwdArgs a, uint16_t* __
                     const uint4* xu = reinterpret_cast<const uint4*>(xs + ((int64_t)tok * U + un) * kXU);
                     const float sx = MODE == BRX_QUANT_AFFINE ? xsum[tok * U + un] : 0.0f;
                     pg += unit_dot<MODE, UPL>(ug, j, xu, sx, a.scale_f16);
-                    pu += unit_dot<MODE, UPL>(uu, j, xu, sx, a.scale_f16);
+                    if (gated) pu += unit_dot<MODE, UPL>(uu, j, xu, sx, a.scale_f16);
                 }
             }
             pg = group_sum(pg, SP);
-            pu = group_sum(pu, SP);
+            if (gated) pu = group_sum(pu, SP);
             if (sl == 0 && r0 + rr < inter) {
                 const float h = en.slot == kAbsentCode ? absent_nan() : act_apply(a.act, pg + bg, pu + bu, a.alpha, a.limit);
                 hbuf[(int64_t)pair * hstride + r0 + rr] = (uint16_t)f2bf(h);
@@ -555,13 +557,14 @@ __global__ __launch_bounds__(kThreads) void k_dec_gateup(FwdArgs a, uint16_t* __
             const int rr = (tid >> 6) * RW + g;
             const int row = min(r0 + rr, inter - 1);
 
+            const bool gated = a.act != BRX_ACT_SILU_MLP;
             Units<MODE, UPL> ug, uu;
             units_load<MODE, UPL>(base, L.p[0], row, sl, SP, ug);
-            units_load<MODE, UPL>(base, L.p[1], row, sl, SP, uu);
+            if (gated) units_load<MODE, UPL>(base, L.p[1], row, sl, SP, uu);
             float bg = 0.f, bu = 0.f;
             if (L.p[0].bias >= 0) {
                 bg = bf2f(reinterpret_cast<const uint16_t*>(base + L.p[0].bias)[row]);
-                bu = bf2f(reinterpret_cast<const uint16_t*>(base + L.p[1].bias)[row]);
+                if (gated) bu = bf2f(reinterpret_cast<const uint16_t*>(base + L.p[1].bias)[row]);
             }
             if (!staged) {   // the weights are in flight
                 stage_dense<MODE>(a.x, H, a.T, tok_row, xs, xsum);
@@ -580,11 +583,11 @@ __global__ __launch_bounds__(kThreads) void k_dec_gateup(FwdArgs a, uint16_t* __
                         const uint4* xu = reinterpret_cast<const uint4*>(xs + ((int64_t)tok * U + un) * kXU);
                         const float sx = MODE == BRX_QUANT_AFFINE ? xsum[tok * U + un] : 0.0f;
                         pg += unit_dot<MODE, UPL>(ug, j, xu, sx, a.scale_f16);
-                        pu += unit_dot<MODE, UPL>(uu, j, xu, sx, a.scale_f16);
+                        if (gated) pu += unit_dot<MODE, UPL>(uu, j, xu, sx, a.scale_f16);
                     }
                 }
                 pg = group_sum(pg, SP);
-                pu = group_sum(pu, SP);
+                if (gated) pu = group_sum(pu, SP);
                 if (sl == 0 && r0 + rr < inter) {
                     const float h = en.slot == kAbsentCode ? absent_nan()
                                                            : act_apply(a.act, pg + bg, pu + bu, a.alpha, a.limit);

@@ -221,6 +221,7 @@ constexpr int kStA = kBM * kBK * 2;          // stage bytes: A tile
 constexpr int kStS = kBlockN * 4 * 2;        // scale and bias per row, one 32-bit LDS slot each
 constexpr int kStage = kStA + kStS;
 static_assert(kNS % 2 == 0, "the paired scale copies follow stage parity through the unrolled ring");
+static_assert(8 * 16 * (kBlockN + 8) * 2 <= kNS * kStage, "the widest output tile must fit in the ring");
 
 typedef __attribute__((address_space(3))) void* LDS_PTR;
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
@@ -339,21 +340,25 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
     // half kh of the stage segment of row brow[nj] (fragment nj, column l32), so one load
     // instruction reads 32 rows x 32 contiguous bytes. Rows past the matrix repeat its last row.
     const __amdgpu_buffer_rsrc_t rb_rsrc = make_rsrc(base, (uint32_t)L.bytes);
+    // a two-layer expert (fc1 / fc2): the block's 256 first-projection rows are 256 fc1
+    // features, all from matrix 0, instead of 128 gate and the same 128 up features
+    const bool mlp = KIND == 0 && a.act == BRX_ACT_SILU_MLP;
     auto mat_row = [&](int br) __attribute__((always_inline)) {
-        return KIND == 0 ? min(nt * 128 + (br & 127), inter - 1) : min(nt * 256 + br, H - 1);
+        return KIND == 0 ? (mlp ? min(nt * 256 + br, inter - 1) : min(nt * 128 + (br & 127), inter - 1))
+                         : min(nt * 256 + br, H - 1);
     };
     int brow[kNJ];
     uint32_t vbw[kNJ];
 #pragma unroll
     for (int nj = 0; nj < kNJ; ++nj) {
         brow[nj] = KIND == 0 ? nj * 128 + wv * 32 + l32 : wv * 64 + nj * 32 + l32;
-        const int pj = KIND == 0 ? nj : 2;
+        const int pj = KIND == 0 ? (mlp ? 0 : nj) : 2;
         vbw[nj] = (uint32_t)L.p[pj].w + (uint32_t)mat_row(brow[nj]) * (uint32_t)(K / 2) + kh * 16;
     }
     // ---- scales: wave wv copies those of rows 64 wv + lane (one 16-bit value per row and
     // stage: affine scale and bias; MXFP4 the e8m0 bytes of the stage's two groups) into a
     // 32-bit LDS slot per row
-    const int p_w = KIND == 0 ? (wv >= 2 ? 1 : 0) : 2;  // matrix of the rows this wave copies
+    const int p_w = KIND == 0 ? (mlp ? 0 : (wv >= 2 ? 1 : 0)) : 2;  // matrix of the rows this wave copies
     const int so = (int)L.p[p_w].s, bo = (int)L.p[p_w].b;
     const uint32_t vsc = MODE == BRX_QUANT_AFFINE
         ? (uint32_t)mat_row(wv * 64 + lane) * (uint32_t)(K / 64) * 2
@@ -366,7 +371,7 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
     bool spair = (rb & 3) == 0;
 #pragma unroll
     for (int pj = 0; pj < 3; ++pj)
-        if (KIND == 0 ? pj < 2 : pj == 2)
+        if (KIND == 0 ? (pj == 0 || (pj == 1 && !mlp)) : pj == 2)
             spair = spair && ((L.p[pj].s & 3) == 0) && (MODE != BRX_QUANT_AFFINE || (L.p[pj].b & 3) == 0);
     if constexpr (KIND == 1) {
         if (tid < kBM) {
@@ -525,7 +530,33 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
     // of contiguous row segments
     dma_wait_barrier<0>();
     uint16_t* T = reinterpret_cast<uint16_t*>(ring);
-    if constexpr (KIND == 0) {
+    if (mlp) {
+        // 256 fc1 features: fragment nj holds features 128 nj + 32 wv + l32 of the block
+        constexpr int TS = kBlockN + 8;
+        constexpr int CH = kBlockN / 8;
+#pragma unroll
+        for (int nj = 0; nj < kNJ; ++nj) {
+            const int fl = nj * 128 + wv * 32 + l32;
+            const int f = min(nt * kBlockN + fl, inter - 1);
+            const float bg = L.p[0].bias >= 0 ? bf2f(reinterpret_cast<const uint16_t*>(base + L.p[0].bias)[f]) : 0.f;
+#pragma unroll
+            for (int mi = 0; mi < MR; ++mi) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const float h = slot == kAbsentCode ? absent_nan()
+                                                        : act_apply(a.act, acc[mi][nj][i] + bg, 0.f, a.alpha, a.limit);
+                    T[(mi * 32 + 8 * (i >> 2) + 4 * kh + (i & 3)) * TS + fl] = __builtin_bit_cast(uint16_t, (__bf16)h);
+                }
+            }
+        }
+        lds_barrier();
+        for (int c = tid; c < MF * 16 * CH; c += kGemmThreads) {
+            const int r = c / CH, f0 = nt * kBlockN + (c % CH) * 8;
+            if (r < rows && f0 < inter)
+                *reinterpret_cast<u32x4_t*>(hbuf + (int64_t)(m0 + r) * hstride + f0) =
+                    *reinterpret_cast<const u32x4_t*>(T + r * TS + (c % CH) * 8);
+        }
+    } else if constexpr (KIND == 0) {
         constexpr int TS = kBlockN / 2 + 8;                // LDS row stride (elements)
         constexpr int CH = kBlockN / 2 / 8;                // 16-byte chunks per row
         // fragment 0 holds gate, fragment 1 the up rows of the same 32 features; element i of
@@ -601,7 +632,7 @@ void k_pf_gemm(FwdArgs a, const int32_t* __restrict__ order, const int32_t* __re
     const int e = ti.x, m0 = ti.y, rows = ti.z;
     if (KIND == 0) {
         const int inter = e >= a.E ? a.I_sh : a.I;
-        if (nt * (kBlockN / 2) >= inter) return;
+        if (nt * (a.act == BRX_ACT_SILU_MLP ? kBlockN : kBlockN / 2) >= inter) return;
     } else {
         if (nt * kBlockN >= a.H) return;
     }
@@ -702,7 +733,8 @@ template <int MODE, bool F16>
 hipError_t launch_gemm(const FwdArgs& a, const PfWs& w, int E_ext, int Imax, uint16_t* y_routed,
                        int phases, hipStream_t s) {
     if (phases & 1) {
-        const int ntn = (Imax + kBlockN / 2 - 1) / (kBlockN / 2);
+        const int fpb = a.act == BRX_ACT_SILU_MLP ? kBlockN : kBlockN / 2;   // features per block
+        const int ntn = (Imax + fpb - 1) / fpb;
         hipLaunchKernelGGL((k_pf_gemm<MODE, F16, 0>), dim3(w.mt_pad * ntn), dim3(kGemmThreads), 0, s,
                            a, w.order, w.tile_start, w.tinfo, E_ext, ntn, w.hbuf, Imax, y_routed, w.y_shared);
         hipError_t err = hipGetLastError();

@@ -28,6 +28,7 @@ from dataclasses import dataclass, field
 import numpy as np
 
 PROJECTIONS = ("gate_proj", "up_proj", "down_proj")
+MLP_PROJECTIONS = ("fc1", "fc2")      # a plain two-layer expert, fc2(silu(fc1 x)) (stream.py:57)
 COMPONENTS = ("weight", "scales", "biases", "bias")
 
 # e2m1 code -> value (sign in bit 3). OCP Microscaling spec, element type FP4 E2M1.
@@ -109,11 +110,21 @@ def projection_spec(n_out: int, n_in: int, q: QuantSpec, has_bias: bool = False)
     return spec
 
 
-def expert_spec(hidden: int, inter: int, q: QuantSpec, has_bias: bool = False) -> dict:
-    """Manifest `spec` of one gated expert: gate/up are [inter, hidden], down is [hidden, inter]."""
+def expert_spec(hidden: int, inter: int, q: QuantSpec, has_bias: bool = False,
+                gated: bool = True) -> dict:
+    """Manifest `spec` of one expert. Gated: gate/up are [inter, hidden], down is [hidden,
+    inter]. Not gated (a plain two-layer expert): fc1 [inter, hidden], fc2 [hidden, inter]."""
+    if not gated:
+        return {"fc1": projection_spec(inter, hidden, q, has_bias),
+                "fc2": projection_spec(hidden, inter, q, has_bias)}
     return {"gate_proj": projection_spec(inter, hidden, q, has_bias),
             "up_proj": projection_spec(inter, hidden, q, has_bias),
             "down_proj": projection_spec(hidden, inter, q, has_bias)}
+
+
+def is_gated(spec: dict) -> bool:
+    """Whether an expert spec is gated (gate/up/down) or a plain two-layer expert (fc1/fc2)."""
+    return tuple(spec) != MLP_PROJECTIONS
 
 
 def spec_bytes(spec: dict) -> int:
@@ -312,12 +323,13 @@ def dequantize_projection(arrays: dict, proj: str, q: QuantSpec) -> np.ndarray:
 
 
 def make_expert(rng: np.random.Generator, hidden: int, inter: int, q: QuantSpec,
-                std: float = 0.02, has_bias: bool = False, bias_std: float = 0.02) -> bytes:
+                std: float = 0.02, has_bias: bool = False, bias_std: float = 0.02,
+                gated: bool = True) -> bytes:
     """One synthetic expert: N(0, std) weights quantized to `q`, packed in blob layout."""
-    spec = expert_spec(hidden, inter, q, has_bias)
+    spec = expert_spec(hidden, inter, q, has_bias, gated)
     arrays = {}
-    for proj in PROJECTIONS:
-        n_out, n_in = (inter, hidden) if proj != "down_proj" else (hidden, inter)
+    for proj in spec:
+        n_out, n_in = (inter, hidden) if proj in ("gate_proj", "up_proj", "fc1") else (hidden, inter)
         w = (rng.standard_normal((n_out, n_in), dtype=np.float32) * std).astype(np.float32)
         if q.mode == "affine":
             wq, s, b = quantize_affine(w, q.group_size, q.bits, q.scale_dtype)

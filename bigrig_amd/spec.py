@@ -7,7 +7,7 @@ from dataclasses import dataclass, field
 from . import formats as F
 
 _ROUTES = {"softmax_topk": 0, "softmax_topk_renorm": 1, "topk_softmax": 2}
-_ACTS = {"swiglu": 0, "swiglu_clamped": 1}
+_ACTS = {"swiglu": 0, "swiglu_clamped": 1, "silu_mlp": 2}
 _RDT = {"float32": 0, "bfloat16": 1}
 MAX_WIDTH = 8192   # largest hidden / intermediate width libbrx takes
 
@@ -21,7 +21,8 @@ class LayerSpec:
     "softmax_topk_renorm" (Qwen3 norm_topk_prob: then w /= sum(w)), "topk_softmax"
     (gpt-oss: w = softmax(logits[idx])).
     act: "swiglu" = silu(gate) * up; "swiglu_clamped" = gpt-oss's clamped form with
-    alpha/limit.
+    alpha/limit; "silu_mlp" = a plain two-layer expert fc2(silu(fc1 x)) (SwitchMLP,
+    stream.py:1167-1169).
     """
     hidden: int
     inter: int
@@ -55,9 +56,14 @@ class LayerSpec:
     def route_mode(self) -> int:
         return _ROUTES[self.route]
 
+    @property
+    def gated(self) -> bool:
+        """Gated experts (gate/up/down) unless the activation is the plain two-layer fc1/fc2."""
+        return self.act != "silu_mlp"
+
     def expert_spec(self, shared: bool = False) -> dict:
         inter = self.shared_inter if shared else self.inter
-        return F.expert_spec(self.hidden, inter, self.quant, self.has_bias)
+        return F.expert_spec(self.hidden, inter, self.quant, self.has_bias, self.gated)
 
     @functools.cached_property
     def bytes_per_expert(self) -> int:

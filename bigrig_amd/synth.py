@@ -81,8 +81,8 @@ def make_layer_experts(spec: LayerSpec, seed: int, std: float = 0.02, device="cu
     gen = torch.Generator(device=device)
     gen.manual_seed(seed)
     parts = []
-    for proj in F.PROJECTIONS:
-        n_out, n_in = (inter, spec.hidden) if proj != "down_proj" else (spec.hidden, inter)
+    for proj in spec.expert_spec(shared):
+        n_out, n_in = (inter, spec.hidden) if proj in ("gate_proj", "up_proj", "fc1") else (spec.hidden, inter)
         w = torch.randn((E, n_out, n_in), generator=gen, device=device, dtype=torch.float32) * std
         if spec.quant.mode == "affine":
             wq, s, b = quantize_affine_torch(w, spec.quant.group_size, spec.quant.bits)

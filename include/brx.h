@@ -42,10 +42,13 @@ enum {
 enum { BRX_QUANT_AFFINE = 0, BRX_QUANT_MXFP4 = 1 };
 /* scale_dtype (affine only) */
 enum { BRX_SCALE_BF16 = 0, BRX_SCALE_F16 = 1 };
-/* act: gated activations of SwitchGLU (stream.py:1164-1166) */
+/* act: the expert's activation (stream.py:1164-1169) */
 enum { BRX_ACT_SWIGLU = 0,          /* silu(gate) * up                                   */
-       BRX_ACT_SWIGLU_CLAMPED = 1 }; /* gpt-oss: g=min(g,L); u=clip(u,-L,L);
+       BRX_ACT_SWIGLU_CLAMPED = 1,  /* gpt-oss: g=min(g,L); u=clip(u,-L,L);
                                          g*sigmoid(alpha*g)*(u+1)                          */
+       BRX_ACT_SILU_MLP = 2 };      /* plain two-layer expert (SwitchMLP): fc2(silu(fc1 x)),
+                                       projections fc1 [I, H] and fc2 [H, I] packed in that
+                                       order (stream.py:57, 1167-1169); layout slot 1 absent */
 /* route_mode: the router rule of the MoE block (bigrig_engine/adapter.py:75-93) */
 enum { BRX_ROUTE_SOFTMAX_TOPK = 0,        /* p=softmax(logits); w=p[idx] (OLMoE)           */
        BRX_ROUTE_SOFTMAX_TOPK_RENORM = 1, /* ... then w /= sum(w) (Qwen3 norm_topk_prob)   */
@@ -76,8 +79,8 @@ typedef struct brx_layer_desc {
 } brx_layer_desc;
 
 /* Byte offsets of one expert's components inside its packed region, in the order
- * pack_experts writes them (projections gate/up/down, components weight/scales/biases/bias,
- * stream.py:152-164). -1 marks an absent component. */
+ * pack_experts writes them (projections gate/up/down -- or fc1/-/fc2 for BRX_ACT_SILU_MLP --
+ * components weight/scales/biases/bias, stream.py:152-164). -1 marks an absent component. */
 typedef struct brx_expert_layout {
     int64_t weight[3];
     int64_t scales[3];

@@ -79,7 +79,8 @@ def orc_layer(spec) -> OrcLayer:
     q = spec.quant
     return OrcLayer(spec.hidden, spec.inter, 0 if q.mode == "affine" else 1, q.bits, q.group_size,
                     1 if q.scale_dtype == "float16" else 0, int(spec.has_bias),
-                    0 if spec.act == "swiglu" else 1, spec.alpha, spec.limit)
+                    {"swiglu": 0, "swiglu_clamped": 1, "silu_mlp": 2}[spec.act], spec.alpha,
+                    spec.limit)
 
 
 # ------------------------------------------------------------------ C restatement wrappers
@@ -164,22 +165,29 @@ def _silu(g):
 def act_f64(spec, g, u):
     if spec.act == "swiglu":
         return _silu(g) * u
+    if spec.act == "silu_mlp":
+        return _silu(g)
     g = np.minimum(g, spec.limit)
     u = np.clip(u, -spec.limit, spec.limit)
     return g / (1.0 + np.exp(-spec.alpha * g)) * (u + 1.0)
 
 
 def expert_weights_f64(spec, expert: bytes, shared: bool = False):
-    """(Wg, Wu, Wd, bg, bu, bd) float64 from packed bytes (biases zero when absent)."""
+    """(Wg, Wu, Wd, bg, bu, bd) float64 from packed bytes (biases zero when absent). A plain
+    two-layer expert returns (W_fc1, zeros, W_fc2, ...): its up projection contributes nothing."""
     from bigrig_amd import formats as F
     inter = spec.shared_inter if shared else spec.inter
-    es = F.expert_spec(spec.hidden, inter, spec.quant, spec.has_bias)
+    gated = spec.act != "silu_mlp"
+    es = F.expert_spec(spec.hidden, inter, spec.quant, spec.has_bias, gated)
     arrs = F.split_expert(expert, es)
-    W = [F.dequantize_projection(arrs, p, spec.quant).astype(np.float64) for p in F.PROJECTIONS]
+    W = [F.dequantize_projection(arrs, p, spec.quant).astype(np.float64) for p in es]
     if spec.has_bias:
-        B = [F.bf16_bits_to_f32(arrs[(p, "bias")]).astype(np.float64) for p in F.PROJECTIONS]
+        B = [F.bf16_bits_to_f32(arrs[(p, "bias")]).astype(np.float64) for p in es]
     else:
-        B = [np.zeros(W[0].shape[0]), np.zeros(W[1].shape[0]), np.zeros(W[2].shape[0])]
+        B = [np.zeros(m.shape[0]) for m in W]
+    if not gated:
+        W.insert(1, np.zeros_like(W[0]))
+        B.insert(1, np.zeros_like(B[0]))
     return W[0], W[1], W[2], B[0], B[1], B[2]
 
 

@@ -5,8 +5,9 @@
  * the router of the MoE block (softmax over experts, top-k, optional renormalisation, as the
  * reference restates it at bigrig_engine/stream.py:895 and 1436-1439 and describes the rule
  * at bigrig_engine/adapter.py:75-93), MLX affine / MXFP4 dequantization (`mx.dequantize`,
- * bigrig_engine/precision.py:186-189), the per-(token, expert) SwitchGLU arithmetic
- * `down(act(up, gate))` (stream.py:1164-1166, 1270-1271; by-hand oracle
+ * bigrig_engine/precision.py:186-189) at any affine width MLX packs, the per-(token, expert)
+ * SwitchGLU arithmetic `down(act(up, gate))` or the two-layer SwitchMLP `fc2(silu(fc1 x))`
+ * (stream.py:1164-1169, 1270-1271; by-hand oracle
  * tests/test_plan_invariance.py:148-163) and the caller's router-weighted combine
  * (stream.py:1523-1525).
  *
@@ -147,9 +148,14 @@ static void proj_dims(const orc_layer* L, int inter, int p, int* n_out, int* n_i
     else { *n_out = L->H; *n_in = inter; }
 }
 
+/* act 2 (a plain two-layer expert) packs fc1 then fc2: projection slots 0 and 2, slot 1 absent */
 void orc_offsets(const orc_layer* L, int inter, orc_off* o) {
     int64_t pos = 0;
     for (int p = 0; p < 3; ++p) {
+        if (p == 1 && L->act == 2) {
+            o->w[1] = o->s[1] = o->b[1] = o->bias[1] = -1;
+            continue;
+        }
         int n_out, n_in;
         proj_dims(L, inter, p, &n_out, &n_in);
         int64_t G = n_in / L->gs;
@@ -173,22 +179,32 @@ static inline float scale_val(const orc_layer* L, const uint8_t* base, int64_t o
     return L->scale_f16 ? h2f(v) : bf2f(v);
 }
 
-static inline uint32_t nib(const uint8_t* wrow, int k) {
-    return (wrow[k >> 1] >> ((k & 1) * 4)) & 0xFu;
+/* Code k of a packed row: MLX packs every width least significant bit first, whole uint32
+ * words for 2/4/8 bits and byte-aligned runs for 3/5/6 (8 values in 3 bytes for 3 bits), so in
+ * both cases code k occupies bits [bits*k, bits*k + bits) of the row's little-endian bytes. */
+static inline uint32_t qcode(const uint8_t* wrow, int k, int bits) {
+    const int64_t pos = (int64_t)bits * k;
+    const int sh = (int)(pos & 7);
+    uint32_t v = wrow[pos >> 3];
+    if (sh + bits > 8) v |= (uint32_t)wrow[(pos >> 3) + 1] << 8;
+    return (v >> sh) & ((1u << bits) - 1u);
 }
 
-/* fp32 dequantized projection p: out [n_out, n_in]. 4-bit layouts only. */
+static inline int64_t row_bytes(const orc_layer* L, int n_in) { return (int64_t)n_in * L->bits / 8; }
+
+/* fp32 dequantized projection p: out [n_out, n_in]. */
 int orc_dequant(const orc_layer* L, const uint8_t* expert, int inter, int p, float* out) {
-    if (L->bits != 4) return -1;
+    if (L->bits < 2 || L->bits > 8 || (L->quant_mode != 0 && L->bits != 4)) return -1;
     orc_off o;
     orc_offsets(L, inter, &o);
+    if (o.w[p] < 0) return -1;
     int n_out, n_in;
     proj_dims(L, inter, p, &n_out, &n_in);
     int G = n_in / L->gs;
     for (int n = 0; n < n_out; ++n) {
-        const uint8_t* wrow = expert + o.w[p] + (int64_t)n * n_in / 2;
+        const uint8_t* wrow = expert + o.w[p] + (int64_t)n * row_bytes(L, n_in);
         for (int k = 0; k < n_in; ++k) {
-            uint32_t q = nib(wrow, k);
+            uint32_t q = qcode(wrow, k, L->bits);
             int g = k / L->gs;
             float v;
             if (L->quant_mode == 0) {
@@ -213,7 +229,7 @@ static void orc_gemv(const orc_layer* L, const uint8_t* expert, const orc_off* o
     proj_dims(L, inter, p, &n_out, &n_in);
     int G = n_in / L->gs, gs = L->gs;
     for (int n = 0; n < n_out; ++n) {
-        const uint8_t* wrow = expert + o->w[p] + (int64_t)n * n_in / 2;
+        const uint8_t* wrow = expert + o->w[p] + (int64_t)n * row_bytes(L, n_in);
         double acc = 0.0;
         for (int g = 0; g < G; ++g) {
             const float* xg = x + (int64_t)g * gs;
@@ -221,8 +237,8 @@ static void orc_gemv(const orc_layer* L, const uint8_t* expert, const orc_off* o
             if (L->quant_mode == 0) {
                 float sqx = 0.0f, sx = 0.0f;
                 for (int i = 0; i < gs / 2; ++i) {
-                    uint8_t byte = wg[i];
-                    float q0 = (float)(byte & 0xF), q1 = (float)(byte >> 4);
+                    const int k = g * gs + 2 * i;
+                    float q0 = (float)qcode(wrow, k, L->bits), q1 = (float)qcode(wrow, k + 1, L->bits);
                     sqx += q0 * xg[2 * i] + q1 * xg[2 * i + 1];
                     sx += xg[2 * i] + xg[2 * i + 1];
                 }
@@ -250,6 +266,7 @@ static void orc_gemv(const orc_layer* L, const uint8_t* expert, const orc_off* o
 
 static inline float act_fn(const orc_layer* L, float g, float u) {
     if (L->act == 0) return g / (1.0f + expf(-g)) * u;
+    if (L->act == 2) return g / (1.0f + expf(-g));
     g = fminf(g, L->limit);
     u = fminf(fmaxf(u, -L->limit), L->limit);
     return g / (1.0f + expf(-L->alpha * g)) * (u + 1.0f);
@@ -264,7 +281,11 @@ static void orc_expert_row(const orc_layer* L, const uint8_t* expert, int inter,
     float* u = scratch + inter;
     float* h = scratch + 2 * inter;
     orc_gemv(L, expert, &o, inter, 0, x, g);
-    orc_gemv(L, expert, &o, inter, 1, x, u);
+    if (L->act == 2) {
+        for (int i = 0; i < inter; ++i) u[i] = 0.0f;     /* fc2(silu(fc1 x)): no up projection */
+    } else {
+        orc_gemv(L, expert, &o, inter, 1, x, u);
+    }
     for (int i = 0; i < inter; ++i) h[i] = bf2f(f2bf(act_fn(L, g[i], u[i])));
     orc_gemv(L, expert, &o, inter, 2, h, y);
 }
@@ -275,7 +296,7 @@ int orc_moe_forward(const orc_layer* L, const uint8_t* const* experts, int k,
                     const uint8_t* shared, int shared_inter, const uint16_t* x,
                     const int32_t* idx, const float* w, const float* sgate, int T,
                     uint16_t* out, uint16_t* yun, int nthreads) {
-    if (L->bits != 4) return -1;
+    if (L->bits < 2 || L->bits > 8 || (L->quant_mode != 0 && L->bits != 4)) return -1;
     int H = L->H;
     int maxI = L->I > shared_inter ? L->I : shared_inter;
     int P = T * k;

@@ -35,16 +35,17 @@ def write_safetensors(path: str, tensors: dict, metadata: dict | None = None) ->
 def make_checkpoint(d: str, layers: dict, *, infix: str = ".mlp.switch_mlp.", shards: int = 2,
                     config: dict | None = None, seed: int = 0, extra: bool = True) -> dict:
     """Write a checkpoint whose layer li has the experts of layers[li] = (hidden, inter,
-    n_experts, QuantSpec, has_bias). Returns {li: (expert spec, quant, [expert bytes])} -- the
+    n_experts, QuantSpec, has_bias[, gated]) (gated False: fc1/fc2 experts). Returns {li: (expert spec, quant, [expert bytes])} -- the
     argument formats.pack_blob takes -- so a test can pack the same experts into a blob."""
     os.makedirs(d, exist_ok=True)
     rng = np.random.default_rng(seed)
     out = {}
     files = [dict() for _ in range(shards)]
     for n, li in enumerate(sorted(layers)):
-        H, I, E, q, has_bias = layers[li]
-        spec = F.expert_spec(H, I, q, has_bias)
-        experts = [F.make_expert(rng, H, I, q, has_bias=has_bias) for _ in range(E)]
+        H, I, E, q, has_bias, *rest = layers[li]
+        gated = rest[0] if rest else True
+        spec = F.expert_spec(H, I, q, has_bias, gated)
+        experts = [F.make_expert(rng, H, I, q, has_bias=has_bias, gated=gated) for _ in range(E)]
         out[li] = (spec, q, experts)
         parts = [F.split_expert(b, spec) for b in experts]
         tens = files[n % shards]

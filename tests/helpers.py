@@ -27,7 +27,7 @@ def make_layer(spec: LayerSpec, seed: int = 0, bank: int | None = None, zipf: fl
     rng = np.random.default_rng(seed)
     nq = spec.n_experts if bank is None else min(bank, spec.n_experts)
     made = [F.make_expert(rng, spec.hidden, spec.inter, spec.quant, std=expert_std,
-                          has_bias=spec.has_bias) for _ in range(nq)]
+                          has_bias=spec.has_bias, gated=spec.gated) for _ in range(nq)]
     if bank is None:
         experts = made
     else:
@@ -38,7 +38,7 @@ def make_layer(spec: LayerSpec, seed: int = 0, bank: int | None = None, zipf: fl
     shared = sgw = None
     if spec.shared_inter:
         shared = F.make_expert(rng, spec.hidden, spec.shared_inter, spec.quant, std=expert_std,
-                               has_bias=spec.has_bias)
+                               has_bias=spec.has_bias, gated=spec.gated)
         sgw = F.f32_to_bf16_bits(rng.standard_normal(spec.hidden, dtype=np.float32) * router_std)
     return Layer(spec, experts, router, bias, shared, sgw)
 

@@ -175,13 +175,13 @@ def test_checkpoint_errors_name_the_problem(tmp_path):
     (d / "config.json").write_text("{}")
     with pytest.raises(ValueError, match="no MoE expert tensors"):
         CK.expert_manifest(str(d))
-    # a two-layer MLP expert layout is recognised as MoE and refused by name
-    d = tmp_path / "fc"
+    # an expert layout that is neither gated nor fc1/fc2 is recognised as MoE and refused by name
+    d = tmp_path / "odd"
     d.mkdir()
     write_safetensors(str(d / "model.safetensors"),
-                      {"model.layers.0.mlp.switch_mlp.fc1.weight": ("U32", (2, 4, 4), bytes(128))})
+                      {"model.layers.0.mlp.switch_mlp.w_in.weight": ("U32", (2, 4, 4), bytes(128))})
     (d / "config.json").write_text("{}")
-    with pytest.raises(ValueError, match="fc1"):
+    with pytest.raises(ValueError, match="w_in"):
         CK.expert_manifest(str(d))
     # siblings disagreeing on the expert count
     d = str(tmp_path / "mism")
@@ -237,3 +237,21 @@ def test_checkpoint_errors_name_the_problem(tmp_path):
         CK.expert_manifest(d)
     with pytest.raises(KeyError):
         CK.CheckpointManifest("x").expert_segments(9, 9)
+
+
+def test_two_layer_experts_read_as_the_blob_holds_them(tmp_path):
+    """fc1/fc2 experts (SwitchMLP): the reader describes them projection by projection as a
+    packed blob lays them out, and layer_spec gives the two-layer activation."""
+    d = str(tmp_path / "mlp")
+    q = F.QuantSpec(4, 64, "affine", "bfloat16")
+    layers = make_checkpoint(d, {0: (256, 128, 6, q, False, False), 3: (256, 128, 6, q, True, False)},
+                             config={"num_experts_per_tok": 2})
+    cm = CK.expert_manifest(d)
+    for li, (spec, _, experts) in layers.items():
+        assert list(cm.layers[str(li)]["spec"]) == ["fc1", "fc2"]
+        for e in range(6):
+            assert CK.read_expert(cm, li, e) == experts[e]
+    s = CK.layer_spec(cm, 0)
+    assert s.act == "silu_mlp" and (s.hidden, s.inter, s.top_k) == (256, 128, 2)
+    assert s.bytes_per_expert == len(layers[0][2][0])
+    assert CK.layer_spec(cm, 3).has_bias

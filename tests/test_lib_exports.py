@@ -136,3 +136,24 @@ def test_layer_spec_refuses_widths_the_kernels_do_not_take():
         with pytest.raises(ValueError):
             replace(QWEN3_30B_A3B, **kw)
     assert replace(QWEN3_30B_A3B, hidden=8192).hidden == 8192
+
+
+def test_two_layer_expert_layout_matches_formats():
+    """act BRX_ACT_SILU_MLP: fc1 in slot 0, fc2 in slot 2, slot 1 absent -- the offsets of the
+    fc1/fc2 blob layout."""
+    from dataclasses import replace
+    lib = L.load()
+    for base in (QWEN3_30B_A3B, GPT_OSS_120B):
+        spec = replace(base, act="silu_mlp")
+        d = spec.desc()
+        out = L.ExpertLayout()
+        L.check(lib.brx_expert_layout_get(C.byref(d), 0, C.byref(out)))
+        es = spec.expert_spec()
+        offs = F.spec_offsets(es)
+        assert list(es) == ["fc1", "fc2"] and out.bytes_per_expert == F.spec_bytes(es)
+        for slot, proj in ((0, "fc1"), (2, "fc2")):
+            assert out.weight[slot] == offs[(proj, "weight")]
+            assert out.scales[slot] == offs[(proj, "scales")]
+            assert out.biases[slot] == offs.get((proj, "biases"), -1)
+            assert out.bias[slot] == offs.get((proj, "bias"), -1)
+        assert out.weight[1] == out.scales[1] == out.biases[1] == out.bias[1] == -1

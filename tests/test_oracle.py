@@ -163,7 +163,9 @@ def test_router_shared_gate_and_errors():
 # ------------------------------------------------------------------ dequant
 @pytest.mark.parametrize("q", [F.QuantSpec(4, 64, "affine", "bfloat16"),
                                F.QuantSpec(4, 64, "affine", "float16"),
-                               F.QuantSpec(4, 32, "mxfp4")], ids=["bf16", "f16", "mxfp4"])
+                               F.QuantSpec(4, 32, "mxfp4"),
+                               F.QuantSpec(3, 64, "affine", "bfloat16")],
+                         ids=["bf16", "f16", "mxfp4", "3bit"])
 def test_c_dequant_equals_numpy_bitwise(q):
     """The C dequant and formats.dequantize_projection (pinned by closed form in test_formats)
     agree bit for bit, projection by projection."""
@@ -185,6 +187,9 @@ LAYER_SPECS = {
     "qwen3": small(QWEN3_30B_A3B, hidden=256, inter=128, n_experts=16, top_k=4),
     "shared": small(E256_SHARED, hidden=256, inter=64, n_experts=16, top_k=4, shared_inter=64),
     "gptoss": small(GPT_OSS_120B, hidden=256, inter=128, n_experts=16, top_k=4),
+    "mlp": small(QWEN3_30B_A3B, hidden=256, inter=128, n_experts=16, top_k=4, act="silu_mlp"),
+    "3bit": small(QWEN3_30B_A3B, hidden=256, inter=128, n_experts=16, top_k=4,
+                  quant=F.QuantSpec(3, 64, "affine", "bfloat16")),
 }
 
 
@@ -215,7 +220,12 @@ def test_layer_vs_f64_truth(name):
                                     np.zeros_like(idx), np.ones_like(w), want_unreduced=True)
         comb += sg[:, None].astype(np.float64) * F.bf16_bits_to_f32(ysh[:, 0]).astype(np.float64)
     got = F.bf16_bits_to_f32(out).astype(np.float64)
-    assert np.all(np.abs(got - comb) <= 2.0 ** -8 * np.abs(comb) + 1e-9 * np.abs(comb).max())
+    # bf16 rounding of the sum, plus the fp32 summation error of its terms (a sum that cancels
+    # keeps the absolute error of its largest terms)
+    mag = np.einsum("tk,tkh->th", np.abs(w.astype(np.float64)), np.abs(yr))
+    if lay.shared is not None:
+        mag += np.abs(comb)
+    assert np.all(np.abs(got - comb) <= 2.0 ** -8 * np.abs(comb) + 16 * 2.0 ** -24 * mag)
 
 
 def test_layer_threads_do_not_change_bits():
@@ -257,6 +267,48 @@ def test_single_expert_is_a_swiglu_mlp_torch():
     bad2 = ((torch.nn.functional.silu(xt @ Bg.T) * (xt @ Bu.T)).to(torch.bfloat16).float()
             @ Bd.T).numpy()
     assert oracle.rel_l2(got, bad2) > 5e-2
+
+
+def test_single_two_layer_expert_is_a_silu_mlp_torch():
+    """act silu_mlp with k=1, weight 1 is the plain MLP fc2(silu(fc1 x)) (stream.py:1167-1169):
+    torch fp32 on the dequantized fc1 / fc2, h rounded to bf16 as the layer stores it. Planted
+    mistakes -- the activation after fc2 instead of between, or fc1 used as a gated pair -- fail
+    the same tolerance."""
+    import torch
+    spec = small(QWEN3_30B_A3B, hidden=256, inter=128, n_experts=4, top_k=1, act="silu_mlp")
+    lay = make_layer(spec, seed=26)
+    x = make_x(7, spec.hidden, seed=27)
+    e = 1
+    out, _ = oracle.moe_forward(spec, lay.experts, x, np.full((7, 1), e), np.ones((7, 1)))
+    es = spec.expert_spec()
+    assert list(es) == ["fc1", "fc2"] and len(lay.experts[e]) == F.spec_bytes(es)
+    arrs = F.split_expert(lay.experts[e], es)
+    W1, W2 = (torch.from_numpy(F.dequantize_projection(arrs, p, spec.quant)) for p in es)
+    xt = torch.from_numpy(F.bf16_bits_to_f32(x))
+    h = torch.nn.functional.silu(xt @ W1.T).to(torch.bfloat16).float()
+    got = F.bf16_bits_to_f32(out)
+    assert oracle.rel_l2(got, (h @ W2.T).numpy()) < 5e-3
+    late = torch.nn.functional.silu((xt @ W1.T) @ W2.T).numpy()
+    assert oracle.rel_l2(got, late) > 5e-2
+    gated = ((torch.nn.functional.silu(xt @ W1.T) * (xt @ W1.T)) @ W2.T).numpy()
+    assert oracle.rel_l2(got, gated) > 5e-2
+
+
+def test_three_bit_layer_dequantizes_the_packed_codes():
+    """3-bit affine: the oracle's dequant reads code k at bits [3k, 3k + 3) of the row, so a
+    row whose codes are a known sequence dequantizes to s * q + b of exactly that sequence."""
+    spec = small(QWEN3_30B_A3B, hidden=128, inter=64, n_experts=1, top_k=1,
+                 quant=F.QuantSpec(3, 64, "affine", "bfloat16"))
+    es = spec.expert_spec()
+    arrs = F.split_expert(F.make_expert(np.random.default_rng(28), 128, 64, spec.quant), es)
+    codes = (np.arange(64 * 128) * 5 + 3) % 8
+    arrs[("gate_proj", "weight")] = F.pack_bits(codes.reshape(64, 128), 3)
+    s = np.full(arrs[("gate_proj", "scales")].shape, 0x3F80, np.uint16)     # 1.0
+    b = np.full(s.shape, 0xBF00, np.uint16)                                  # -0.5
+    arrs[("gate_proj", "scales")], arrs[("gate_proj", "biases")] = s, b
+    blob = F.join_expert(arrs, es)
+    got = oracle.dequant(spec, blob, 0)
+    assert np.array_equal(got, codes.reshape(64, 128).astype(np.float32) - 0.5)
 
 
 def test_brute_force_tiny_layer_torch_f64():
