@@ -12,6 +12,33 @@ constexpr int kWave = 64;
 constexpr int kMaxTableEdits = 32;   // table entries one brx_pool_publish_async launch sets
 constexpr int kMaxWidth = 8192;      // largest hidden / intermediate width the kernels take
 
+// Kernel weight modes: the public quant modes, plus 3-bit affine (BRX_QUANT_AFFINE with 3 bits:
+// a group of 64 codes is 24 bytes, 8 codes per 3 bytes, least significant bits first).
+constexpr int kModeAffine3 = 2;
+template <int MODE>
+constexpr bool kAffine = MODE != BRX_QUANT_MXFP4;   // scale + bias per group of 64
+
+// The 24 bits of 3-byte group m (codes 8m .. 8m + 7) of a 3-bit affine group held in six
+// little-endian words (only the low 24 bits of the result are meaningful).
+__device__ __forceinline__ uint32_t group24(const uint32_t w[6], int m) {
+    switch (m & 7) {
+        case 0: return w[0];
+        case 1: return __builtin_amdgcn_alignbit(w[1], w[0], 24);
+        case 2: return __builtin_amdgcn_alignbit(w[2], w[1], 16);
+        case 3: return w[2] >> 8;
+        case 4: return w[3];
+        case 5: return __builtin_amdgcn_alignbit(w[4], w[3], 24);
+        case 6: return __builtin_amdgcn_alignbit(w[5], w[4], 16);
+        default: return w[5] >> 8;
+    }
+}
+
+// Codes i and i + 4 of a 3-byte group in the low bits of the two 16-bit halves.
+__device__ __forceinline__ uint32_t pair3(uint32_t g, int i) {
+    const uint32_t t = g >> (3 * i);
+    return (t & 0x7u) | ((t << 4) & 0x70000u);
+}
+
 // ------------------------------------------------------------------ layout (host + device)
 struct Proj {
     int64_t w, s, b, bias;  // byte offsets inside the expert (-1 = absent)
@@ -87,7 +114,7 @@ struct FwdArgs {
     int32_t capacity;
     int32_t auto_shared;        // token mode: every token also runs the shared expert
     int32_t T, H, I, I_sh, E, k;
-    int32_t quant_mode, scale_f16, has_bias, act;
+    int32_t quant_mode, scale_f16, has_bias, act;   // quant_mode: a kernel mode (kModeAffine3 for 3 bits)
     float alpha, limit;
     int32_t yrows;              // rows of yun
     int32_t route_mode;
@@ -295,6 +322,18 @@ typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+// sum_{i} (128 + q_i) * x_i over the 8 codes of a 3-byte group `g` (3-bit affine), with the
+// activations paired as for dot8_q4.
+__device__ __forceinline__ float dot8_q3(uint32_t g, const uint32_t* xp, float acc) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t qp = pair3(g, i) | 0x43004300u;
+        acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, qp),
+                                              __builtin_bit_cast(bf16x2_t, xp[i]), acc, false);
+    }
+    return acc;
+}
 
 // sum_{i} (128 + q_i) * x_i over the 8 nibbles of `wd`, accumulated into acc.
 // xp[i] packs (x_{i}, x_{i+4}) as bf16x2: nibble i and nibble i+4 of the word land in the

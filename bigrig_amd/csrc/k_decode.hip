@@ -18,7 +18,8 @@
 // layer has one, is the last entry and takes every token.
 //
 // A weight row of K inputs is U = K/64 units of 32 bytes (64 nibbles: one affine group with
-// one scale and one bias, or two MXFP4 groups whose two e8m0 scales are one 16-bit load). SP
+// one scale and one bias, or two MXFP4 groups whose two e8m0 scales are one 16-bit load; 24
+// bytes for a 3-bit affine group, 8 codes per 3 bytes). SP
 // consecutive lanes own a row, lane s the UPL units s + SP j, so each load instruction of a
 // row group reads SP adjacent 32-byte units. The activations a block multiplies (x for
 // gate/up, h for down) are staged once in LDS in the order the dot product wants them, with
@@ -191,14 +192,26 @@ template <int MODE, int UPL>
 __device__ __forceinline__ void units_load(const uint8_t* base, const Proj& P, int row, int s, int SP,
                                            Units<MODE, UPL>& u) {
     const int U = P.n_in / 64;
-    const uint4* wrow = reinterpret_cast<const uint4*>(base + P.w + (int64_t)row * (P.n_in / 2));
+    if constexpr (MODE == kModeAffine3) {
+        // 24 bytes a unit (rows and units are 8-byte aligned): three 8-byte loads
+        const uint2* wrow = reinterpret_cast<const uint2*>(base + P.w + (int64_t)row * (P.n_in * 3 / 8));
 #pragma unroll
-    for (int j = 0; j < UPL; ++j) {
-        const int un = min(s + SP * j, U - 1);
-        u.w[j][0] = wrow[2 * un];
-        u.w[j][1] = wrow[2 * un + 1];
+        for (int j = 0; j < UPL; ++j) {
+            const int un = min(s + SP * j, U - 1);
+            const uint2 a = wrow[3 * un], b = wrow[3 * un + 1], c = wrow[3 * un + 2];
+            u.w[j][0] = make_uint4(a.x, a.y, b.x, b.y);
+            u.w[j][1] = make_uint4(c.x, c.y, 0u, 0u);
+        }
+    } else {
+        const uint4* wrow = reinterpret_cast<const uint4*>(base + P.w + (int64_t)row * (P.n_in / 2));
+#pragma unroll
+        for (int j = 0; j < UPL; ++j) {
+            const int un = min(s + SP * j, U - 1);
+            u.w[j][0] = wrow[2 * un];
+            u.w[j][1] = wrow[2 * un + 1];
+        }
     }
-    if constexpr (MODE == BRX_QUANT_AFFINE) {
+    if constexpr (kAffine<MODE>) {
         const uint16_t* sp = reinterpret_cast<const uint16_t*>(base + P.s) + (int64_t)row * U;
         const uint16_t* bp = reinterpret_cast<const uint16_t*>(base + P.b) + (int64_t)row * U;
 #pragma unroll
@@ -224,13 +237,16 @@ __device__ __forceinline__ float unit_dot(const Units<MODE, UPL>& u, int j, cons
                                           int scale_f16) {
     const uint32_t wd[8] = {u.w[j][0].x, u.w[j][0].y, u.w[j][0].z, u.w[j][0].w,
                             u.w[j][1].x, u.w[j][1].y, u.w[j][1].z, u.w[j][1].w};
-    if constexpr (MODE == BRX_QUANT_AFFINE) {
+    if constexpr (kAffine<MODE>) {
         float acc = 0.0f;
 #pragma unroll
         for (int m = 0; m < 8; ++m) {
             const uint4 xv = xu[m];
             const uint32_t xp[4] = {xv.x, xv.y, xv.z, xv.w};
-            acc = dot8_q4(wd[m], xp, acc);
+            if constexpr (MODE == kModeAffine3)
+                acc = dot8_q3(group24(wd, m), xp, acc);
+            else
+                acc = dot8_q4(wd[m], xp, acc);
         }
         const float sc = scale_f16 ? h2f(u.s[j]) : bf2f(u.s[j]);
         const float bi = scale_f16 ? h2f(u.b[j]) : bf2f(u.b[j]);
@@ -322,7 +338,7 @@ __device__ __forceinline__ void stage_store(int K, int nrows, int base, const St
         const int un = pi >> 3, q = pi & 7;
         uint32_t in[4] = {st.v[b].x, st.v[b].y, st.v[b].z, st.v[b].w}, o[4];
         float part = 0.0f;
-        if constexpr (MODE == BRX_QUANT_AFFINE) {
+        if constexpr (kAffine<MODE>) {
             perm8(in, o);
 #pragma unroll
             for (int z = 0; z < 4; ++z)
@@ -334,7 +350,7 @@ __device__ __forceinline__ void stage_store(int K, int nrows, int base, const St
         }
         if (ok)
             *reinterpret_cast<uint4*>(xs + ((int64_t)r * U + un) * kXU + q * 16) = make_uint4(o[0], o[1], o[2], o[3]);
-        if constexpr (MODE == BRX_QUANT_AFFINE) {
+        if constexpr (kAffine<MODE>) {
             part = sum8_dpp(part);
             if (ok && q == 0) sums[r * U + un] = part;
         }
@@ -371,7 +387,7 @@ __device__ __forceinline__ void stage_dense(const uint16_t* __restrict__ src, in
             const int un = pi >> 3, q = pi & 7;
             uint32_t in[4] = {v[b].x, v[b].y, v[b].z, v[b].w}, o[4];
             float part = 0.0f;
-            if constexpr (MODE == BRX_QUANT_AFFINE) {
+            if constexpr (kAffine<MODE>) {
                 perm8(in, o);
 #pragma unroll
                 for (int z = 0; z < 4; ++z)
@@ -383,7 +399,7 @@ __device__ __forceinline__ void stage_dense(const uint16_t* __restrict__ src, in
             }
             if (ok)
                 *reinterpret_cast<uint4*>(xs + ((int64_t)r * U + un) * kXU + q * 16) = make_uint4(o[0], o[1], o[2], o[3]);
-            if constexpr (MODE == BRX_QUANT_AFFINE) {
+            if constexpr (kAffine<MODE>) {
                 part = sum8_dpp(part);
                 if (ok && q == 0) sums[r * U + un] = part;
             }
@@ -505,7 +521,7 @@ __global__ __launch_bounds__(kThreads) void k_dec_gateup(FwdArgs a, uint16_t* __
                 const int un = sl + SP * j;
                 if (un < U) {
                     const uint4* xu = reinterpret_cast<const uint4*>(xs + ((int64_t)tok * U + un) * kXU);
-                    const float sx = MODE == BRX_QUANT_AFFINE ? xsum[tok * U + un] : 0.0f;
+                    const float sx = kAffine<MODE> ? xsum[tok * U + un] : 0.0f;
                     pg += unit_dot<MODE, UPL>(ug, j, xu, sx, a.scale_f16);
                     if (gated) pu += unit_dot<MODE, UPL>(uu, j, xu, sx, a.scale_f16);
                 }
@@ -581,7 +597,7 @@ __global__ __launch_bounds__(kThreads) void k_dec_gateup(FwdArgs a, uint16_t* __
                     const int un = sl + SP * j;
                     if (un < U) {
                         const uint4* xu = reinterpret_cast<const uint4*>(xs + ((int64_t)tok * U + un) * kXU);
-                        const float sx = MODE == BRX_QUANT_AFFINE ? xsum[tok * U + un] : 0.0f;
+                        const float sx = kAffine<MODE> ? xsum[tok * U + un] : 0.0f;
                         pg += unit_dot<MODE, UPL>(ug, j, xu, sx, a.scale_f16);
                         if (gated) pu += unit_dot<MODE, UPL>(uu, j, xu, sx, a.scale_f16);
                     }
@@ -781,7 +797,7 @@ __global__ __launch_bounds__(kThreads) void k_dec_down(FwdArgs a, const uint16_t
                     if (i < nt && un < U) {
                         const int hr = all_fit ? s_pair[s_first[u] + i] : srow + i;
                         const uint4* hu = reinterpret_cast<const uint4*>(hs + ((int64_t)hr * Umax + un) * kXU);
-                        const float sx = MODE == BRX_QUANT_AFFINE ? hsum[hr * Umax + un] : 0.0f;
+                        const float sx = kAffine<MODE> ? hsum[hr * Umax + un] : 0.0f;
                         p += unit_dot<MODE, UPL>(ud, j, hu, sx, a.scale_f16);
                     }
                 }
@@ -858,7 +874,7 @@ __global__ __launch_bounds__(kThreads) void k_dec_down_fit(FwdArgs a, const uint
                 const int un = sl + SP * j;
                 if (i < nt && un < U) {
                     const uint4* hu = reinterpret_cast<const uint4*>(hs + ((int64_t)hr * Umax + un) * kXU);
-                    const float sx = MODE == BRX_QUANT_AFFINE ? hsum[hr * Umax + un] : 0.0f;
+                    const float sx = kAffine<MODE> ? hsum[hr * Umax + un] : 0.0f;
                     p += unit_dot<MODE, UPL>(ud, j, hu, sx, a.scale_f16);
                 }
             }
@@ -981,6 +997,7 @@ size_t decode_workspace_bytes(const FwdArgs& a) {
 hipError_t launch_decode(const FwdArgs& a, void* ws, int phases, hipStream_t s) {
     DecTable* table = reinterpret_cast<DecTable*>(ws);
     uint16_t* hbuf = reinterpret_cast<uint16_t*>(reinterpret_cast<char*>(ws) + table_bytes());
+    if (a.quant_mode == kModeAffine3) return launch_mode<kModeAffine3>(a, hbuf, table, phases, s);
     return a.quant_mode == BRX_QUANT_AFFINE ? launch_mode<BRX_QUANT_AFFINE>(a, hbuf, table, phases, s)
                                             : launch_mode<BRX_QUANT_MXFP4>(a, hbuf, table, phases, s);
 }

@@ -6,14 +6,19 @@
 namespace brx {
 namespace {
 
+// Code k of a row sits at bits [bits k, bits k + bits) of the row's bytes, least significant
+// bit first (a 3-bit code may straddle two bytes).
 template <int MODE>
 __global__ __launch_bounds__(256) void k_dequant(const uint8_t* __restrict__ base, Proj P,
-                                                 int scale_f16, float* __restrict__ out) {
+                                                 int scale_f16, int bits, float* __restrict__ out) {
     const int row = blockIdx.x;
     const int n_in = P.n_in;
+    const uint8_t* wrow = base + P.w + (int64_t)row * (n_in * bits / 8);
     for (int k = threadIdx.x; k < n_in; k += blockDim.x) {
-        uint32_t byte = base[P.w + (int64_t)row * (n_in / 2) + k / 2];
-        uint32_t q = (byte >> ((k & 1) * 4)) & 0xFu;
+        const int bit = k * bits;
+        uint32_t two = wrow[bit >> 3];
+        if ((bit & 7) + bits > 8) two |= (uint32_t)wrow[(bit >> 3) + 1] << 8;
+        const uint32_t q = (two >> (bit & 7)) & ((1u << bits) - 1u);
         float v;
         if constexpr (MODE == BRX_QUANT_AFFINE) {
             const int G = n_in / 64;
@@ -47,10 +52,10 @@ hipError_t launch_dequant(const brx_layer_desc& d, const Layout& L, const uint8_
     const Proj& P = L.p[proj];
     if (d.quant_mode == BRX_QUANT_AFFINE)
         hipLaunchKernelGGL(k_dequant<BRX_QUANT_AFFINE>, dim3(P.n_out), dim3(256), 0, s, expert, P,
-                           d.scale_dtype == BRX_SCALE_F16 ? 1 : 0, out);
+                           d.scale_dtype == BRX_SCALE_F16 ? 1 : 0, d.bits, out);
     else
         hipLaunchKernelGGL(k_dequant<BRX_QUANT_MXFP4>, dim3(P.n_out), dim3(256), 0, s, expert, P, 0,
-                           out);
+                           4, out);
     return hipGetLastError();
 }
 

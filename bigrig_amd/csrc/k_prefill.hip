@@ -179,6 +179,7 @@ __device__ __forceinline__ uint32_t pk_bf16(float lo, float hi) {
 // native vector (not HIP's uint4 struct, whose copies are memcpys that keep arrays of it in
 // scratch memory)
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x3_t __attribute__((ext_vector_type(3)));
 
 // ------------------------------------------------------------------ grouped GEMM
 // One block = 256 threads = 4 waves, one wave per SIMD; the tile is MF * 16 rows (one M tile
@@ -266,16 +267,18 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint3
 //     exact when widened to fp32) and v_fma_mix_f32 forms fma(q 2^-24, s 2^24, b): the product
 //     is exactly s q, so the result is the same fl(s q + b) as fmaf(s, q, b). `s24` is s 2^24
 //     (exact for any scale below 2^104). A mask of 0x000F000F takes two nibbles at once, so a
-//     word costs 7 extractions, 8 fma_mix and 4 packs.
+//     word costs 7 extractions, 8 fma_mix and 4 packs. 3-bit codes arrive as a 24-bit group
+//     (8 codes, 3 bits each) and are paired the same way (code i and code 4 + i).
 //   MXFP4: the hardware converts two e2m1 codes with the e8m0 scale, exact in bf16.
 template <int MODE>
 __device__ __forceinline__ bf16x8_t dq8(uint32_t w, float s24, float b, float sc) {
     uint32_t o[4];
-    if constexpr (MODE == BRX_QUANT_AFFINE) {
+    if constexpr (kAffine<MODE>) {
         float v[8];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const uint32_t t = (w >> (4 * i)) & 0x000F000Fu;     // nibbles i (low half), 4 + i
+            // codes i (low half) and 4 + i (high half)
+            const uint32_t t = MODE == kModeAffine3 ? pair3(w, i) : (w >> (4 * i)) & 0x000F000Fu;
             v[i] = __builtin_fmaf((float)__builtin_bit_cast(_Float16, (uint16_t)(t & 0xFFFFu)), s24, b);
             v[4 + i] = __builtin_fmaf((float)__builtin_bit_cast(_Float16, (uint16_t)(t >> 16)), s24, b);
         }
@@ -303,7 +306,7 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
     // loads per wave of an odd stage (A copies, B loads) and of an even stage (+ the scale copies
     // of it and the next stage)
     constexpr int NV1 = NA + kNJ;
-    constexpr int NV0 = NV1 + (MODE == BRX_QUANT_AFFINE ? 2 : 1);
+    constexpr int NV0 = NV1 + (kAffine<MODE> ? 2 : 1);
     const bool sh = e >= a.E;
     const int inter = sh ? a.I_sh : a.I;
     const int H = a.H;
@@ -353,14 +356,16 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
     for (int nj = 0; nj < kNJ; ++nj) {
         brow[nj] = KIND == 0 ? nj * 128 + wv * 32 + l32 : wv * 64 + nj * 32 + l32;
         const int pj = KIND == 0 ? (mlp ? 0 : nj) : 2;
-        vbw[nj] = (uint32_t)L.p[pj].w + (uint32_t)mat_row(brow[nj]) * (uint32_t)(K / 2) + kh * 16;
+        vbw[nj] = MODE == kModeAffine3
+            ? (uint32_t)L.p[pj].w + (uint32_t)mat_row(brow[nj]) * (uint32_t)(K * 3 / 8) + kh * 12
+            : (uint32_t)L.p[pj].w + (uint32_t)mat_row(brow[nj]) * (uint32_t)(K / 2) + kh * 16;
     }
     // ---- scales: wave wv copies those of rows 64 wv + lane (one 16-bit value per row and
     // stage: affine scale and bias; MXFP4 the e8m0 bytes of the stage's two groups) into a
     // 32-bit LDS slot per row
     const int p_w = KIND == 0 ? (mlp ? 0 : (wv >= 2 ? 1 : 0)) : 2;  // matrix of the rows this wave copies
     const int so = (int)L.p[p_w].s, bo = (int)L.p[p_w].b;
-    const uint32_t vsc = MODE == BRX_QUANT_AFFINE
+    const uint32_t vsc = kAffine<MODE>
         ? (uint32_t)mat_row(wv * 64 + lane) * (uint32_t)(K / 64) * 2
         : (uint32_t)mat_row(wv * 64 + lane) * (uint32_t)(K / 32);
     // the scales of two stages are one 4-byte copy when every scale row and array of the
@@ -372,7 +377,7 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
 #pragma unroll
     for (int pj = 0; pj < 3; ++pj)
         if (KIND == 0 ? (pj == 0 || (pj == 1 && !mlp)) : pj == 2)
-            spair = spair && ((L.p[pj].s & 3) == 0) && (MODE != BRX_QUANT_AFFINE || (L.p[pj].b & 3) == 0);
+            spair = spair && ((L.p[pj].s & 3) == 0) && (!kAffine<MODE> || (L.p[pj].b & 3) == 0);
     if constexpr (KIND == 1) {
         if (tid < kBM) {
             int d = -1;
@@ -405,20 +410,27 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
                 const int gp = g & ~1;
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(rb_rsrc, (LDS_PTR)(st + SA + wv * 256), 4, vsc,
                                                          so + gp * 2, 0, 0);
-                if constexpr (MODE == BRX_QUANT_AFFINE)
+                if constexpr (kAffine<MODE>)
                     __builtin_amdgcn_raw_ptr_buffer_load_lds(rb_rsrc, (LDS_PTR)(st + SA + 1024 + wv * 256), 4,
                                                              vsc, bo + gp * 2, 0, 0);
             }
         } else {
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rb_rsrc, (LDS_PTR)(st + SA + wv * 256), 2, vsc,
                                                      so + g * 2, 0, 0);
-            if constexpr (MODE == BRX_QUANT_AFFINE)
+            if constexpr (kAffine<MODE>)
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(rb_rsrc, (LDS_PTR)(st + SA + 1024 + wv * 256), 2,
                                                          vsc, bo + g * 2, 0, 0);
         }
 #pragma unroll
-        for (int nj = 0; nj < kNJ; ++nj)
-            br.w[nj] = __builtin_amdgcn_raw_buffer_load_b128(rb_rsrc, vbw[nj], g * 32, 0);
+        for (int nj = 0; nj < kNJ; ++nj) {
+            if constexpr (MODE == kModeAffine3) {
+                // 3-bit: the lane's half of the stage segment is 12 bytes (4 groups of 8 codes)
+                const u32x3_t w3 = __builtin_amdgcn_raw_buffer_load_b96(rb_rsrc, vbw[nj], g * 24, 0);
+                br.w[nj] = u32x4_t{w3[0], w3[1], w3[2], 0u};
+            } else {
+                br.w[nj] = __builtin_amdgcn_raw_buffer_load_b128(rb_rsrc, vbw[nj], g * 32, 0);
+            }
+        }
     };
     // Fragments are 32 x 32 (v_mfma_f32_32x32x16_bf16): MR row blocks of 32 by kNJ column
     // blocks of 32 per wave. Lane l works on row / column l % 32 of a fragment and on K half
@@ -441,7 +453,7 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
         for (int nj = 0; nj < kNJ; ++nj) {
             const int br = brow[nj];
             f.s[nj] = (*reinterpret_cast<const uint32_t*>(ss + SA + br * 4) >> sh) & 0xFFFFu;
-            if constexpr (MODE == BRX_QUANT_AFFINE)
+            if constexpr (kAffine<MODE>)
                 f.b[nj] = (*reinterpret_cast<const uint32_t*>(ss + SA + 1024 + br * 4) >> sh) & 0xFFFFu;
         }
     };
@@ -450,14 +462,23 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
 #pragma unroll
         for (int nj = 0; nj < kNJ; ++nj) {
             float sv = 0.f, bv = 0.f, sc = 0.f;
-            if constexpr (MODE == BRX_QUANT_AFFINE) {
+            if constexpr (kAffine<MODE>) {
                 sv = (F16 ? h2f(f.s[nj]) : bf2f(f.s[nj])) * 16777216.0f;   // s 2^24, exact
                 bv = F16 ? h2f(f.b[nj]) : bf2f(f.b[nj]);
             } else {
                 // chunk 4 kh + kk lies in the stage's 32-wide group kh
                 sc = e8m0_f32((f.s[nj] >> (8 * kh)) & 0xFFu);
             }
-            bop[nj] = dq8<MODE>(bw.w[nj][kk], sv, bv, sc);
+            uint32_t wk = bw.w[nj][kk];
+            if constexpr (MODE == kModeAffine3) {
+                // the 24-bit group kk of the lane's 12 bytes
+                const u32x4_t& q = bw.w[nj];
+                wk = kk == 0 ? q[0]
+                   : kk == 1 ? __builtin_amdgcn_alignbit(q[1], q[0], 24)
+                   : kk == 2 ? __builtin_amdgcn_alignbit(q[2], q[1], 16)
+                             : q[2] >> 8;
+            }
+            bop[nj] = dq8<MODE>(wk, sv, bv, sc);
         }
     };
 
@@ -796,7 +817,10 @@ hipError_t launch_prefill(const FwdArgs& a, void* ws, size_t ws_bytes, int phase
                             w.tile_start, w.tinfo, s);
         if (err != hipSuccess) return err;
     }
-    if (a.quant_mode == BRX_QUANT_AFFINE)
+    if (a.quant_mode == kModeAffine3)
+        err = a.scale_f16 ? launch_gemm<kModeAffine3, true>(a, w, E_ext, Imax, y_routed, phases, s)
+                          : launch_gemm<kModeAffine3, false>(a, w, E_ext, Imax, y_routed, phases, s);
+    else if (a.quant_mode == BRX_QUANT_AFFINE)
         err = a.scale_f16 ? launch_gemm<BRX_QUANT_AFFINE, true>(a, w, E_ext, Imax, y_routed, phases, s)
                           : launch_gemm<BRX_QUANT_AFFINE, false>(a, w, E_ext, Imax, y_routed, phases, s);
     else

@@ -88,6 +88,10 @@ class LayerSpec:
 # intermediate, routing rule, quantization).
 OLMOE_1B_7B = LayerSpec(2048, 1024, 64, 8, route="softmax_topk", router_dtype="float32")
 QWEN3_30B_A3B = LayerSpec(2048, 768, 128, 8, route="softmax_topk_renorm")
+# the layout of the shipped Qwen3-30B-A3B-3bit blob (3-bit affine, group 64, bf16 scale + bias:
+# data/blobs/Qwen3-30B-A3B-3bit.experts.manifest.json, 2,064,384 bytes per expert)
+QWEN3_30B_A3B_3BIT = LayerSpec(2048, 768, 128, 8, route="softmax_topk_renorm",
+                               quant=F.QuantSpec(3, 64, "affine", "bfloat16"))
 E256_SHARED = LayerSpec(2048, 512, 256, 8, route="softmax_topk_renorm", shared_inter=512)
 GPT_OSS_120B = LayerSpec(2880, 2880, 128, 4, quant=F.QuantSpec(4, 32, "mxfp4"), has_bias=True,
                          act="swiglu_clamped", route="topk_softmax")

@@ -14,7 +14,8 @@ from .spec import LayerSpec
 
 def quantize_affine_torch(w, group_size: int = 64, bits: int = 4):
     """(packed int32 [..., N, K*bits/32], scales bf16, biases bf16): formats.quantize_affine
-    on torch tensors (bits dividing 32)."""
+    on torch tensors. Code k of a row lands at bits [bits k, bits k + bits) of the row's
+    words, least significant first (a 3-bit code may straddle two words)."""
     import torch
     *lead, N, K = w.shape
     n_bins = float((1 << bits) - 1)
@@ -30,9 +31,19 @@ def quantize_affine_torch(w, group_size: int = 64, bits: int = 4):
     scales = torch.where(nz, edge / torch.where(nz, q0, torch.ones_like(q0)), scales)
     biases = torch.where(nz, edge, torch.zeros_like(edge))
     q = torch.clamp(torch.round((g - biases[..., None]) / scales[..., None]), 0, n_bins)
-    q = q.to(torch.int64).reshape(*lead, N, K * bits // 32, 32 // bits)
-    shifts = torch.arange(32 // bits, device=w.device, dtype=torch.int64) * bits
-    word = (q << shifts).sum(-1)
+    q = q.to(torch.int64).reshape(*lead, N, K)
+    if 32 % bits == 0:
+        q = q.reshape(*lead, N, K * bits // 32, 32 // bits)
+        shifts = torch.arange(32 // bits, device=w.device, dtype=torch.int64) * bits
+        word = (q << shifts).sum(-1)
+    else:
+        pos = torch.arange(K, device=w.device, dtype=torch.int64) * bits
+        wi, sh = pos // 32, pos % 32
+        n_words = K * bits // 32
+        word = torch.zeros(*lead, N, n_words, device=w.device, dtype=torch.int64)
+        word.index_add_(-1, wi, (q << sh) & 0xFFFFFFFF)
+        spill = torch.where(sh + bits > 32, q >> (32 - sh).clamp_max(31), torch.zeros_like(q))
+        word.index_add_(-1, (wi + 1).clamp_max(n_words - 1), spill)
     word = torch.where(word >= 2 ** 31, word - 2 ** 32, word).to(torch.int32)
     return word, scales.to(torch.bfloat16), biases.to(torch.bfloat16)
 

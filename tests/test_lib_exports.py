@@ -75,7 +75,7 @@ def test_expert_layout_matches_formats(spec):
 
 
 BAD = [("hidden", 100, "hidden"), ("inter", 0, "inter"), ("n_experts", 513, "n_experts"),
-       ("top_k", 0, "top_k"), ("bits", 3, "affine"), ("group_size", 128, "affine"),
+       ("top_k", 0, "top_k"), ("bits", 5, "affine"), ("group_size", 128, "affine"),
        ("quant_mode", 7, "quant_mode"), ("act", 5, "act"), ("route_mode", 3, "route_mode"),
        ("router_dtype", 9, "router_dtype"), ("shared_inter", 96, "shared_inter"),
        ("hidden", 8256, "at most 8192"), ("inter", 8256, "at most 8192"),
