@@ -258,18 +258,29 @@ def read_expert(man: CheckpointManifest, layer: int, expert: int) -> bytes:
 
 
 def routing_from_config(cfg: dict) -> dict:
-    """The block's routing rule and activation as LayerSpec fields, from config.json: softmax
-    top-k, renormalised when `norm_topk_prob` is set (adapter.py:75-93); gpt-oss applies the
+    """The block's routing rule and activation as LayerSpec fields, from config.json, decided as
+    adapter.py:75-93 describes it: sigmoid scoring when `score_function` / `scoring_func` names
+    it, softmax when it names softmax, and otherwise sigmoid exactly when the config has
+    expert groups; group-limited when `n_group` / `topk_group` are set; renormalised when
+    `norm_topk_prob` is set; weights scaled by `routed_scaling_factor`. gpt-oss applies the
     softmax to the top-k logits and a clamped SwiGLU (`swiglu_limit`)."""
     mt = str(cfg.get("model_type", "")).lower()
-    fn = str(cfg.get("score_function") or cfg.get("scoring_func") or "softmax").lower()
-    if "sigmoid" in fn or cfg.get("n_group") or cfg.get("topk_group"):
-        raise ValueError("sigmoid / group-limited routing is not a rule these kernels implement")
     if mt == "gpt_oss":
         return {"route": "topk_softmax", "act": "swiglu_clamped",
                 "limit": float(cfg.get("swiglu_limit", 7.0))}
-    return {"route": "softmax_topk_renorm" if cfg.get("norm_topk_prob") else "softmax_topk",
-            "act": "swiglu"}
+    fn = str(cfg.get("score_function") or cfg.get("scoring_func") or "").lower()
+    grouped = bool(cfg.get("n_group") or cfg.get("topk_group"))
+    sigmoid = "sigmoid" in fn or ("softmax" not in fn and grouped)
+    norm = bool(cfg.get("norm_topk_prob"))
+    out = {"route": ("sigmoid_topk" if sigmoid else "softmax_topk") + ("_renorm" if norm else ""),
+           "act": "swiglu"}
+    if grouped:
+        n_group = int(cfg.get("n_group") or 1)
+        out.update(n_group=n_group, topk_group=int(cfg.get("topk_group") or n_group))
+    scale = cfg.get("routed_scaling_factor")
+    if scale is not None:
+        out["route_scale"] = float(scale)
+    return out
 
 
 def layer_spec(man: CheckpointManifest, layer: int, **overrides):

@@ -81,7 +81,21 @@ int check_desc(const brx_layer_desc* d) {
     }
     if (d->act != BRX_ACT_SWIGLU && d->act != BRX_ACT_SWIGLU_CLAMPED && d->act != BRX_ACT_SILU_MLP)
         return fail(BRX_EINVAL, "act %d unknown", d->act);
-    if (d->route_mode < 0 || d->route_mode > 2) return fail(BRX_EINVAL, "route_mode %d unknown", d->route_mode);
+    if (d->route_mode < 0 || d->route_mode > BRX_ROUTE_SIGMOID_TOPK_RENORM)
+        return fail(BRX_EINVAL, "route_mode %d unknown", d->route_mode);
+    if (d->n_group < 0 || d->n_group > 64)
+        return fail(BRX_EINVAL, "n_group %d outside [0, 64]", d->n_group);
+    if (d->n_group > 1) {
+        if (d->n_experts % d->n_group)
+            return fail(BRX_EINVAL, "n_group %d does not divide n_experts %d", d->n_group, d->n_experts);
+        if (d->topk_group < 1 || d->topk_group > d->n_group)
+            return fail(BRX_EINVAL, "topk_group %d outside [1, n_group %d]", d->topk_group, d->n_group);
+        if (d->top_k > d->topk_group * (d->n_experts / d->n_group))
+            return fail(BRX_EINVAL, "top_k %d exceeds the %d experts of topk_group %d groups", d->top_k,
+                        d->topk_group * (d->n_experts / d->n_group), d->topk_group);
+    }
+    if (!(d->route_scale >= 0.0f) || d->route_scale > 1e30f)
+        return fail(BRX_EINVAL, "route_scale must be finite and >= 0 (0 means 1)");
     if (d->router_dtype != BRX_DT_F32 && d->router_dtype != BRX_DT_BF16)
         return fail(BRX_EINVAL, "router_dtype %d unknown", d->router_dtype);
     if (d->shared_inter < 0 || d->shared_inter % 64)
@@ -476,7 +490,11 @@ static FwdArgs make_args(const brx_layer_desc* d, brx_pool* p, const void* x, in
     a.out = (uint16_t*)out;
     a.yun = (uint16_t*)y_rows;
     a.yrows = yrows;
-    a.route_mode = d->route_mode;
+    const RouteRule rr = route_rule(*d, nullptr);
+    a.route_mode = rr.mode;
+    a.n_group = rr.n_group;
+    a.topk_group = rr.topk_group;
+    a.route_scale = rr.scale;
     a.err = p->err_dev;
     return a;
 }
@@ -641,6 +659,7 @@ static int block_forward_impl(const brx_layer_desc* d, brx_pool* p, const void* 
     if (decode) {
         if (do_route) e = launch_router_logits(*d, x, w_router, router_bias, shared_gate_w, T, logits, s);
         a.logits = logits;
+        a.route_bias = route_rule(*d, router_bias).bias;
         a.route_idx = ridx;
         a.route_w = rw;
         a.route_sg = rsg;

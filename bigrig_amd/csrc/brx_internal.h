@@ -108,6 +108,7 @@ struct FwdArgs {
     float* route_w;             // [T, k]
     float* route_sg;            // [T] or null
     int32_t* err;               // the pool's error word {flag, expert} (device), or null
+    const float* route_bias;    // sigmoid routing: the selection (score-correction) bias [E] or null
     Layout lay;                 // routed expert layout
     Layout lay_sh;              // shared expert layout
     int32_t P;                  // routed (token, expert) pairs
@@ -117,7 +118,9 @@ struct FwdArgs {
     int32_t quant_mode, scale_f16, has_bias, act;   // quant_mode: a kernel mode (kModeAffine3 for 3 bits)
     float alpha, limit;
     int32_t yrows;              // rows of yun
-    int32_t route_mode;
+    int16_t route_mode;
+    uint8_t n_group, topk_group;   // group-limited routing (1, 1: none); at most 64
+    float route_scale;          // multiplies every routing weight
 };
 static_assert(sizeof(FwdArgs) <= 480, "kernel argument blocks must stay under 512 bytes");
 
@@ -299,6 +302,100 @@ __device__ __forceinline__ void wave_topk(const float v[kPer], int E, int k, int
     }
 }
 
+// The routing rule a ranking applies beyond plain top-k of the logits.
+struct RouteRule {
+    const float* bias;   // sigmoid modes: selection bias [E] or null
+    int mode, n_group, topk_group;
+    float scale;
+};
+
+__device__ __forceinline__ bool route_sigmoid(int mode) { return mode >= BRX_ROUTE_SIGMOID_TOPK; }
+
+// e^x as x = n ln2 + r (|r| <= ln2 / 2; ln2 split into a 12-bit head and a tail, Cody-Waite),
+// e^r by its Taylor polynomial of degree 7 in Horner form with fused multiply-adds, scaled by
+// 2^n: every step is one correctly rounded operation, so the host restatement of the routing
+// gives the same bits (within 2 ulp of e^x). The sigmoid routing scores use it because their
+// order decides the experts.
+__device__ __forceinline__ float exp_rt(float x) {
+    if (x > 88.5f) return __builtin_inff();
+    if (x < -104.0f) return 0.0f;
+    const float n = __builtin_rintf(x * 1.44269502f);
+    float r = __builtin_fmaf(-n, 0.693115234375f, x);
+    r = __builtin_fmaf(-n, 3.19461833e-05f, r);
+    float p = 1.98412701e-04f;
+    p = __builtin_fmaf(p, r, 1.38888892e-03f);
+    p = __builtin_fmaf(p, r, 8.33333377e-03f);
+    p = __builtin_fmaf(p, r, 4.16666679e-02f);
+    p = __builtin_fmaf(p, r, 1.66666672e-01f);
+    p = __builtin_fmaf(p, r, 0.5f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    return __builtin_ldexpf(p, (int)n);
+}
+__device__ __forceinline__ float sigmoid_f(float v) { return 1.0f / (1.0f + exp_rt(-v)); }
+
+// Selection values of the experts this lane holds (lane l: experts l + 64 i), from their logits:
+// the logit itself (softmax modes) or sigmoid(logit) + bias (sigmoid modes); with groups
+// (n_group > 1) the experts outside the topk_group best groups are then taken out (softmax:
+// -inf; sigmoid: 0). A group's score is its largest logit (softmax) or the sum of its two
+// largest selection values (sigmoid; the second largest is the largest of the others after one
+// holder of the maximum, the lowest id, is set aside); groups rank by score, ties to the lower
+// group, as the top-k does.
+template <int kPer>
+__device__ __forceinline__ void route_values(const float v[kPer], const RouteRule& rr, int E, float c[kPer]) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const bool sig = route_sigmoid(rr.mode);
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+        const int e = min(lane + kWave * i, E - 1);
+        c[i] = sig ? sigmoid_f(v[i]) + (rr.bias ? rr.bias[e] : 0.0f) : v[i];
+    }
+    if (rr.n_group <= 1) return;
+    const int G = E / rr.n_group;
+    float gs = -__builtin_inff();          // lane g: group g's score
+    for (int g = 0; g < rr.n_group; ++g) {
+        float lm = -__builtin_inff();
+        bool mem[kPer];
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const int e = lane + kWave * i;
+            mem[i] = e >= g * G && e < (g + 1) * G;
+            if (mem[i]) lm = fmaxf(lm, c[i]);
+        }
+        const float m1 = wave_max(lm);
+        float score = m1;
+        if (sig) {
+            int first = -1;
+#pragma unroll
+            for (int i = 0; i < kPer; ++i) {
+                const uint64_t b = __ballot(mem[i] && c[i] == m1);
+                if (first < 0 && b) first = kWave * i + __builtin_ctzll(b);
+            }
+            float l2 = -__builtin_inff();
+#pragma unroll
+            for (int i = 0; i < kPer; ++i)
+                if (mem[i] && lane + kWave * i != first) l2 = fmaxf(l2, c[i]);
+            score = m1 + wave_max(l2);
+        }
+        if (lane == g) gs = score;
+    }
+    uint64_t keep = 0;
+    bool live = lane < rr.n_group;
+    for (int r = 0; r < rr.topk_group; ++r) {
+        const float m = wave_max(live ? gs : -__builtin_inff());
+        uint64_t b = __ballot(live && gs == m);
+        if (!b) b = __ballot(live);        // only NaN scores left: the lowest live group
+        const int g = __builtin_ctzll(b);
+        keep |= 1ull << g;
+        if (lane == g) live = false;
+    }
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+        const int grp = min((lane + kWave * i) / G, 63);
+        if (!((keep >> grp) & 1ull)) c[i] = sig ? 0.0f : -__builtin_inff();
+    }
+}
+
 // Routing weight of the rank this lane holds (lanes >= k return 0): softmax over all E logits
 // then the selected entries (renormalised to sum 1 for BRX_ROUTE_SOFTMAX_TOPK_RENORM), or a
 // softmax over the k selected logits (BRX_ROUTE_TOPK_SOFTMAX).
@@ -316,6 +413,40 @@ __device__ __forceinline__ float wave_route_weight(const float v[kPer], int E, i
     float w = ex / wave_sum(part);
     if (mode == BRX_ROUTE_SOFTMAX_TOPK_RENORM) w = w / wave_sum(w);
     return w;
+}
+
+// The rule's top-k for one token whose logits this wave holds: lane r < k ends holding rank
+// r's expert in sel_e and its selection value in sel_v (softmax modes: the logit). Softmax
+// modes without groups rank the logits directly.
+template <int kPer>
+__device__ __forceinline__ void wave_select(const float v[kPer], const RouteRule& rr, int E, int k,
+                                            int& sel_e, float& sel_v) {
+    if (!route_sigmoid(rr.mode) && rr.n_group <= 1) {
+        wave_topk<kPer>(v, E, k, sel_e, sel_v);
+        return;
+    }
+    float c[kPer];
+    route_values<kPer>(v, rr, E, c);
+    wave_topk<kPer>(c, E, k, sel_e, sel_v);
+}
+
+// The routing weight of the rank this lane holds (lanes >= k: 0), after wave_select. Softmax
+// modes weigh as wave_route_weight (an eligible expert's selection value is its logit);
+// sigmoid modes weigh sigmoid(logit) of the chosen expert, read back from `lrow` (the token's
+// logits in memory), renormalised to sum 1 for BRX_ROUTE_SIGMOID_TOPK_RENORM. The weight is
+// then multiplied by the rule's scale.
+template <int kPer>
+__device__ __forceinline__ float wave_weight(const float v[kPer], const float* lrow, const RouteRule& rr,
+                                             int E, int k, int sel_e, float sel_v) {
+    const int lane = threadIdx.x & (kWave - 1);
+    float w;
+    if (!route_sigmoid(rr.mode)) {
+        w = wave_route_weight<kPer>(v, E, k, rr.mode, sel_v);
+    } else {
+        const float s = lane < k && sel_e >= 0 ? sigmoid_f(lrow[sel_e]) : 0.0f;
+        w = rr.mode == BRX_ROUTE_SIGMOID_TOPK_RENORM ? s / wave_sum(s) : s;
+    }
+    return w * rr.scale;
 }
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
@@ -356,6 +487,17 @@ __device__ __forceinline__ void perm8(const uint32_t in[4], uint32_t out[4]) {
     out[1] = (in[0] >> 16) | (in[2] & 0xFFFF0000u);
     out[2] = (in[1] & 0xFFFFu) | (in[3] << 16);
     out[3] = (in[1] >> 16) | (in[3] & 0xFFFF0000u);
+}
+
+// The descriptor's routing rule (route_scale 0 means 1).
+inline RouteRule route_rule(const brx_layer_desc& d, const float* bias) {
+    RouteRule r;
+    r.bias = d.route_mode >= BRX_ROUTE_SIGMOID_TOPK ? bias : nullptr;
+    r.mode = d.route_mode;
+    r.n_group = d.n_group > 1 ? d.n_group : 1;
+    r.topk_group = d.n_group > 1 ? d.topk_group : 1;
+    r.scale = d.route_scale == 0.0f ? 1.0f : d.route_scale;
+    return r;
 }
 
 // ------------------------------------------------------------------ launchers

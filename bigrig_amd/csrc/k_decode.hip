@@ -137,16 +137,17 @@ __device__ __forceinline__ void route_rank(const FwdArgs& a, const RouteRegs<kPe
                                            bool publish) {
     const int lane = threadIdx.x & 63;
     const int E = a.E, k = a.k;
+    const RouteRule rr{a.route_bias, a.route_mode, a.n_group, a.topk_group, a.route_scale};
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) {
         const int t = (threadIdx.x >> 6) + kWaves * tt;
         if (t >= a.T) break;   // wave-uniform
         int sel_e;
         float sel_v;
-        wave_topk<kPer>(rg.v[tt], E, k, sel_e, sel_v);
+        wave_select<kPer>(rg.v[tt], rr, E, k, sel_e, sel_v);
         if (lane < k) s_e[t * k + lane] = sel_e;
         if (publish) {
-            const float w = wave_route_weight<kPer>(rg.v[tt], E, k, a.route_mode, sel_v);
+            const float w = wave_weight<kPer>(rg.v[tt], a.logits + (int64_t)t * (E + 1), rr, E, k, sel_e, sel_v);
             if (lane < k) {
                 a.route_idx[t * k + lane] = sel_e;
                 a.route_w[t * k + lane] = w;

@@ -1,4 +1,5 @@
-// Router top-k: logits = x . W_r^T (+ bias), top-k by logit, routing weights.
+// Router top-k: logits = x . W_r^T (+ bias), top-k by logit (or by the sigmoid rules'
+// selection values), routing weights.
 //
 // Replaces the MoE block's `gate(x)` + softmax + argpartition + take (+ renorm) that the
 // reference restates at bigrig_engine/stream.py:895 and 1436-1439 (rule: adapter.py:75-93).
@@ -242,7 +243,7 @@ __global__ __launch_bounds__(WPB * kWave) void k_router_logits(
 // Top-k of one token's logits row `l` ([E + 1], the last entry the shared-gate logit) and its
 // routing weights, by the calling wave.
 template <int kPer>
-__device__ __forceinline__ void topk_row(const float* __restrict__ l, int t, int E, int k, int mode,
+__device__ __forceinline__ void topk_row(const float* __restrict__ l, int t, int E, int k, const RouteRule& rr,
                                          int has_sg, int32_t* __restrict__ out_idx,
                                          float* __restrict__ out_w, float* __restrict__ out_sg) {
     const int lane = threadIdx.x & 63;
@@ -254,8 +255,8 @@ __device__ __forceinline__ void topk_row(const float* __restrict__ l, int t, int
     }
     int my_id;
     float my_v;
-    wave_topk<kPer>(v, E, k, my_id, my_v);
-    const float wt = wave_route_weight<kPer>(v, E, k, mode, my_v);
+    wave_select<kPer>(v, rr, E, k, my_id, my_v);
+    const float wt = wave_weight<kPer>(v, l, rr, E, k, my_id, my_v);
     if (lane < k) {
         out_idx[(int64_t)t * k + lane] = my_id;
         out_w[(int64_t)t * k + lane] = wt;
@@ -266,11 +267,11 @@ __device__ __forceinline__ void topk_row(const float* __restrict__ l, int t, int
 // One wave per token over logits [T][E + 1].
 template <int kPer>
 __global__ __launch_bounds__(kRouterThreads) void k_router_topk(
-    const float* __restrict__ logits, int T, int E, int k, int mode, int has_sg,
+    const float* __restrict__ logits, int T, int E, int k, RouteRule rr, int has_sg,
     int32_t* __restrict__ out_idx, float* __restrict__ out_w, float* __restrict__ out_sg) {
     const int t = blockIdx.x * (kRouterThreads / kWave) + (threadIdx.x >> 6);
     if (t >= T) return;
-    topk_row<kPer>(logits + (int64_t)t * (E + 1), t, E, k, mode, has_sg, out_idx, out_w, out_sg);
+    topk_row<kPer>(logits + (int64_t)t * (E + 1), t, E, k, rr, has_sg, out_idx, out_w, out_sg);
 }
 
 template <bool WF32>
@@ -285,12 +286,13 @@ hipError_t logits_launch(const brx_layer_desc& d, const void* x, const void* w_r
     return hipGetLastError();
 }
 
-hipError_t topk_launch(const brx_layer_desc& d, int T, int has_sg, const float* logits,
+hipError_t topk_launch(const brx_layer_desc& d, int T, int has_sg, const float* logits, const float* bias,
                        int32_t* out_idx, float* out_w, float* out_sg, hipStream_t s) {
     const int E = d.n_experts;
+    const RouteRule rr = route_rule(d, bias);
     dim3 grid((T + 3) / 4), block(kRouterThreads);
 #define BRX_TOPK(KP) hipLaunchKernelGGL(k_router_topk<KP>, grid, block, 0, s, logits, T, E, d.top_k, \
-                                        d.route_mode, has_sg, out_idx, out_w, out_sg)
+                                        rr, has_sg, out_idx, out_w, out_sg)
     if (E <= 64) BRX_TOPK(1);
     else if (E <= 128) BRX_TOPK(2);
     else if (E <= 256) BRX_TOPK(4);
@@ -308,6 +310,8 @@ size_t router_workspace_bytes(const brx_layer_desc& d, int T) {
 hipError_t launch_router_logits(const brx_layer_desc& d, const void* x, const void* w_router,
                                 const float* bias, const void* sgw, int T, float* logits,
                                 hipStream_t s) {
+    // sigmoid rules keep the logits raw: their bias enters the selection only
+    if (d.route_mode >= BRX_ROUTE_SIGMOID_TOPK) bias = nullptr;
     return d.router_dtype == BRX_DT_F32 ? logits_launch<true>(d, x, w_router, bias, sgw, T, logits, s)
                                         : logits_launch<false>(d, x, w_router, bias, sgw, T, logits, s);
 }
@@ -320,7 +324,7 @@ hipError_t launch_router(const brx_layer_desc& d, const void* x, const void* w_r
     if (T <= kSmallT) {
         hipError_t e = launch_router_logits(d, x, w_router, bias, sgw, T, ws_logits, s);
         if (e != hipSuccess) return e;
-        return topk_launch(d, T, sgw ? 1 : 0, ws_logits, out_idx, out_w, out_sg, s);
+        return topk_launch(d, T, sgw ? 1 : 0, ws_logits, bias, out_idx, out_w, out_sg, s);
     }
     // many tokens: logits by token tiles, then the same top-k kernel
     // rows per block: 32 (each weight row read once per 16-token tile, by one wave), fewer
@@ -332,15 +336,16 @@ hipError_t launch_router(const brx_layer_desc& d, const void* x, const void* w_r
     while (RPB > 4 && tiles * ((rows + RPB - 1) / RPB) < 512) RPB /= 2;
     dim3 grid(tiles, (rows + RPB - 1) / RPB);
     const size_t lds = sizeof(uint16_t) * (size_t)TT * d.hidden;
+    const float* lbias = d.route_mode >= BRX_ROUTE_SIGMOID_TOPK ? nullptr : bias;
     if (f32)
         hipLaunchKernelGGL((k_router_tiled<true, TT>), grid, dim3(kRouterThreads), lds, s, (const uint16_t*)x,
-                           w_router, bias, (const uint16_t*)sgw, T, d.hidden, d.n_experts, RPB, ws_logits);
+                           w_router, lbias, (const uint16_t*)sgw, T, d.hidden, d.n_experts, RPB, ws_logits);
     else
         hipLaunchKernelGGL((k_router_tiled<false, TT>), grid, dim3(kRouterThreads), lds, s, (const uint16_t*)x,
-                           w_router, bias, (const uint16_t*)sgw, T, d.hidden, d.n_experts, RPB, ws_logits);
+                           w_router, lbias, (const uint16_t*)sgw, T, d.hidden, d.n_experts, RPB, ws_logits);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    return topk_launch(d, T, sgw ? 1 : 0, ws_logits, out_idx, out_w, out_sg, s);
+    return topk_launch(d, T, sgw ? 1 : 0, ws_logits, bias, out_idx, out_w, out_sg, s);
 }
 
 }  // namespace brx

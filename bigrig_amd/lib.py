@@ -17,8 +17,10 @@ QUANT_AFFINE, QUANT_MXFP4 = 0, 1
 SCALE_BF16, SCALE_F16 = 0, 1
 ACT_SWIGLU, ACT_SWIGLU_CLAMPED = 0, 1
 ROUTE_SOFTMAX_TOPK, ROUTE_SOFTMAX_TOPK_RENORM, ROUTE_TOPK_SOFTMAX = 0, 1, 2
+ROUTE_SIGMOID_TOPK, ROUTE_SIGMOID_TOPK_RENORM = 3, 4
 DT_F32, DT_BF16 = 0, 1
 FWD_FORCE_DECODE, FWD_FORCE_PREFILL, FWD_PHASE_A, FWD_PHASE_B, FWD_PHASE_R = 1, 2, 4, 8, 16
+ABI_VERSION = 2         # brx_abi_version() of the library this binding matches (BRX_ABI_VERSION)
 NOALLOC_SCRATCH_BYTES = 16 << 20
 
 EXPORTS = (
@@ -39,7 +41,8 @@ class LayerDesc(C.Structure):
                 ("group_size", C.c_int32), ("scale_dtype", C.c_int32), ("has_bias", C.c_int32),
                 ("act", C.c_int32), ("alpha", C.c_float), ("limit", C.c_float),
                 ("route_mode", C.c_int32), ("router_dtype", C.c_int32),
-                ("shared_inter", C.c_int32), ("reserved", C.c_int32)]
+                ("shared_inter", C.c_int32), ("n_group", C.c_int32), ("topk_group", C.c_int32),
+                ("route_scale", C.c_float), ("reserved", C.c_int32 * 2)]
 
 
 class ExpertLayout(C.Structure):
@@ -111,8 +114,9 @@ def load(path: str | None = None):
             fn = getattr(lib, name)
             fn.argtypes = args
             fn.restype = res
-        if lib.brx_abi_version() != 1:
-            raise RuntimeError(f"{p} has ABI {lib.brx_abi_version()}, this binding expects 1")
+        if lib.brx_abi_version() != ABI_VERSION:
+            raise RuntimeError(f"{p} has ABI {lib.brx_abi_version()}, this binding expects "
+                               f"{ABI_VERSION}: rebuild the library")
         if path is None:
             _lib = lib
         return lib

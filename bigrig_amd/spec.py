@@ -6,7 +6,8 @@ from dataclasses import dataclass, field
 
 from . import formats as F
 
-_ROUTES = {"softmax_topk": 0, "softmax_topk_renorm": 1, "topk_softmax": 2}
+_ROUTES = {"softmax_topk": 0, "softmax_topk_renorm": 1, "topk_softmax": 2, "sigmoid_topk": 3,
+           "sigmoid_topk_renorm": 4}
 _ACTS = {"swiglu": 0, "swiglu_clamped": 1, "silu_mlp": 2}
 _RDT = {"float32": 0, "bfloat16": 1}
 MAX_WIDTH = 8192   # largest hidden / intermediate width libbrx takes
@@ -19,7 +20,11 @@ class LayerSpec:
     route: how the block turns logits into (indices, weights) -- the rule adapter.py:75-93
     records per model: "softmax_topk" (OLMoE: w = softmax(logits)[idx]),
     "softmax_topk_renorm" (Qwen3 norm_topk_prob: then w /= sum(w)), "topk_softmax"
-    (gpt-oss: w = softmax(logits[idx])).
+    (gpt-oss: w = softmax(logits[idx])), "sigmoid_topk" / "sigmoid_topk_renorm" (DeepSeek-V3-style
+    scoring: select on sigmoid(logits) + the router bias, weigh sigmoid(logits)[idx], optionally
+    renormalised). n_group > 1 makes the selection group-limited (the topk_group best of
+    n_group contiguous expert groups stay eligible); route_scale multiplies every weight
+    (routed_scaling_factor).
     act: "swiglu" = silu(gate) * up; "swiglu_clamped" = gpt-oss's clamped form with
     alpha/limit; "silu_mlp" = a plain two-layer expert fc2(silu(fc1 x)) (SwitchMLP,
     stream.py:1167-1169).
@@ -36,6 +41,9 @@ class LayerSpec:
     route: str = "softmax_topk_renorm"
     router_dtype: str = "bfloat16"
     shared_inter: int = 0
+    n_group: int = 0
+    topk_group: int = 0
+    route_scale: float = 1.0
 
     def __post_init__(self):
         if self.route not in _ROUTES:
@@ -46,6 +54,15 @@ class LayerSpec:
             raise ValueError(f"router_dtype {self.router_dtype!r} not in {sorted(_RDT)}")
         if not 1 <= self.top_k <= self.n_experts:
             raise ValueError(f"top_k {self.top_k} outside [1, {self.n_experts}]")
+        if self.n_group > 1:
+            G = self.n_experts // self.n_group if self.n_group <= 64 else 0
+            if (not G or self.n_experts % self.n_group or
+                    not 1 <= self.topk_group <= self.n_group or self.top_k > self.topk_group * G):
+                raise ValueError(f"group-limited routing needs n_group <= 64 dividing n_experts, "
+                                 f"1 <= topk_group <= n_group and top_k <= topk_group * group size "
+                                 f"(n_group {self.n_group}, topk_group {self.topk_group})")
+        if not self.route_scale > 0:
+            raise ValueError(f"route_scale {self.route_scale} must be positive")
         for name in ("hidden", "inter", "shared_inter"):
             v = getattr(self, name)
             if v % 64 or v > MAX_WIDTH or (v <= 0 and name != "shared_inter") or v < 0:
@@ -55,6 +72,11 @@ class LayerSpec:
     @property
     def route_mode(self) -> int:
         return _ROUTES[self.route]
+
+    @property
+    def route_rule(self) -> dict:
+        """The oracle router's keyword arguments for this layer's rule beyond its mode."""
+        return {"n_group": self.n_group, "topk_group": self.topk_group, "scale": self.route_scale}
 
     @property
     def gated(self) -> bool:
@@ -81,7 +103,8 @@ class LayerSpec:
                          0 if q.mode == "affine" else 1, q.bits, q.group_size,
                          1 if q.scale_dtype == "float16" else 0, int(self.has_bias),
                          _ACTS[self.act], self.alpha, self.limit, self.route_mode,
-                         _RDT[self.router_dtype], self.shared_inter, 0)
+                         _RDT[self.router_dtype], self.shared_inter, self.n_group,
+                         self.topk_group, self.route_scale)
 
 
 # The synthetic layer shapes the benchmarks and parity tests run (hidden, experts, top-k,

@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define BRX_ABI_VERSION 1
+#define BRX_ABI_VERSION 2
 
 enum {
     BRX_OK = 0,
@@ -49,10 +49,14 @@ enum { BRX_ACT_SWIGLU = 0,          /* silu(gate) * up                          
        BRX_ACT_SILU_MLP = 2 };      /* plain two-layer expert (SwitchMLP): fc2(silu(fc1 x)),
                                        projections fc1 [I, H] and fc2 [H, I] packed in that
                                        order (stream.py:57, 1167-1169); layout slot 1 absent */
-/* route_mode: the router rule of the MoE block (bigrig_engine/adapter.py:75-93) */
+/* route_mode: the router rule of the MoE block (bigrig_engine/adapter.py:75-93: softmax or
+ * sigmoid scoring, optionally group-limited, optionally normalised) */
 enum { BRX_ROUTE_SOFTMAX_TOPK = 0,        /* p=softmax(logits); w=p[idx] (OLMoE)           */
        BRX_ROUTE_SOFTMAX_TOPK_RENORM = 1, /* ... then w /= sum(w) (Qwen3 norm_topk_prob)   */
-       BRX_ROUTE_TOPK_SOFTMAX = 2 };      /* w = softmax(logits[idx]) (gpt-oss)            */
+       BRX_ROUTE_TOPK_SOFTMAX = 2,        /* w = softmax(logits[idx]) (gpt-oss)            */
+       BRX_ROUTE_SIGMOID_TOPK = 3,        /* s=sigmoid(logits); select on s + bias;
+                                             w = s[idx] (DeepSeek-V3-style scoring)        */
+       BRX_ROUTE_SIGMOID_TOPK_RENORM = 4 };/* ... then w /= sum(w)                          */
 /* router weight dtype */
 enum { BRX_DT_F32 = 0, BRX_DT_BF16 = 1 };
 
@@ -75,7 +79,16 @@ typedef struct brx_layer_desc {
     int32_t router_dtype;  /* BRX_DT_*: dtype of the router weight [E, H]                   */
     int32_t shared_inter;  /* intermediate width of an always-on shared expert, 0 = none
                               (any multiple of 64 up to 8192, independent of inter)          */
-    int32_t reserved;
+    /* Group-limited selection (n_group > 1): the experts form n_group contiguous groups of
+     * E / n_group; each group is scored (softmax modes: its largest logit; sigmoid modes: the
+     * sum of its two largest selection scores s + bias), the topk_group best groups stay
+     * eligible (ties to the lower group) and the others drop out of the top-k (sigmoid modes:
+     * their selection scores become 0; softmax modes: they are never picked). 0 or 1: none. */
+    int32_t n_group;
+    int32_t topk_group;
+    float   route_scale;   /* routed_scaling_factor: every routing weight is multiplied by it
+                              (0 means 1)                                                     */
+    int32_t reserved[2];
 } brx_layer_desc;
 
 /* Byte offsets of one expert's components inside its packed region, in the order
@@ -189,7 +202,9 @@ int brx_pool_admit_async(brx_pool* p, int expert, int slot, const void* host_src
 /* Router top-k for T tokens: logits = x . W_r^T (+ bias), then the layer's routing rule.
  *   x        [T, H] bf16 (device)
  *   w_router [E, H] fp32 or bf16 per d->router_dtype (device)
- *   bias     [E] fp32 or NULL: added to the logits (router bias, synthetic Zipf bias)
+ *   bias     [E] fp32 or NULL: softmax modes add it to the logits (router bias, synthetic
+ *            Zipf bias); sigmoid modes add it to the sigmoid scores for selection only (the
+ *            score-correction bias), the weights being the uncorrected scores
  *   shared_gate_w [H] bf16 or NULL: shared-expert gate row; out_shared_gate[t] =
  *            sigmoid(x_t . w) when given
  *   out_idx  [T, k] int32: experts by descending logit, ties to the lower id

@@ -60,8 +60,10 @@ def lib():
         vp = C.c_void_p
         _lib.orc_dot_lane_tree.argtypes = [vp, vp, C.c_int, C.c_int]
         _lib.orc_dot_lane_tree.restype = C.c_float
+        _lib.orc_exp_rt.argtypes = [C.c_float]
+        _lib.orc_exp_rt.restype = C.c_float
         _lib.orc_router.argtypes = [vp, vp, C.c_int, vp, vp, C.c_int, C.c_int, C.c_int, C.c_int,
-                                    C.c_int, vp, vp, vp, vp]
+                                    C.c_int, C.c_int, C.c_int, C.c_float, vp, vp, vp, vp]
         _lib.orc_dequant.argtypes = [C.POINTER(OrcLayer), vp, C.c_int, C.c_int, vp]
         _lib.orc_moe_forward.argtypes = [C.POINTER(OrcLayer), vp, C.c_int, vp, C.c_int, vp, vp, vp,
                                          vp, C.c_int, vp, vp, C.c_int]
@@ -90,9 +92,13 @@ def dot_lane_tree(x_bits: np.ndarray, w, w_f32: bool) -> float:
     return float(lib().orc_dot_lane_tree(_p(x), _p(w), int(w_f32), x.shape[-1]))
 
 
-def router(x_bits, w, w_f32: bool, bias, k: int, mode: int, shared_gate_w=None):
+def router(x_bits, w, w_f32: bool, bias, k: int, mode: int, shared_gate_w=None, n_group: int = 0,
+           topk_group: int = 0, scale: float = 1.0):
     """(logits [T,E] f32, idx [T,k] i32, w [T,k] f32, sgate [T] f32|None) in the kernels' order.
-    mode: 0 softmax-topk, 1 softmax-topk-renorm, 2 topk-softmax."""
+    mode: 0 softmax-topk, 1 softmax-topk-renorm, 2 topk-softmax, 3 sigmoid-topk (bias enters
+    the selection only), 4 sigmoid-topk-renorm; n_group > 1 limits the top-k to the
+    topk_group best expert groups; the weights are multiplied by `scale`. Sigmoid modes return
+    the raw logits."""
     x = np.ascontiguousarray(x_bits, dtype=np.uint16)
     T, H = x.shape
     wr = np.ascontiguousarray(w, dtype=np.float32 if w_f32 else np.uint16)
@@ -103,8 +109,8 @@ def router(x_bits, w, w_f32: bool, bias, k: int, mode: int, shared_gate_w=None):
     idx = np.zeros((T, k), np.int32)
     wts = np.zeros((T, k), np.float32)
     sgo = np.zeros(T, np.float32) if sg is not None else None
-    rc = lib().orc_router(_p(x), _p(wr), int(w_f32), _p(b), _p(sg), T, H, E, k, mode,
-                          _p(logits), _p(idx), _p(wts), _p(sgo))
+    rc = lib().orc_router(_p(x), _p(wr), int(w_f32), _p(b), _p(sg), T, H, E, k, mode, n_group,
+                          topk_group, float(scale), _p(logits), _p(idx), _p(wts), _p(sgo))
     if rc != 0:
         raise ValueError("orc_router rejected its arguments")
     return logits, idx, wts, sgo
@@ -218,15 +224,43 @@ def moe_forward_f64(spec, experts: list, x_bits, idx, w, shared=None, sgate=None
     return out, y
 
 
-def router_f64(x_bits, w, w_f32: bool, bias, k: int, mode: int):
-    """float64 logits and the top-k set/weights from them (closed form)."""
+def exp_rt(x) -> np.ndarray:
+    """The routing exponential (orc_exp_rt) over an array of float32 inputs."""
+    xs = np.asarray(x, np.float32).reshape(-1)
+    f = lib().orc_exp_rt
+    return np.array([f(float(v)) for v in xs], np.float32).reshape(np.shape(x))
+
+
+def router_f64(x_bits, w, w_f32: bool, bias, k: int, mode: int, n_group: int = 0,
+               topk_group: int = 0, scale: float = 1.0):
+    """float64 logits and the top-k set/weights from them (closed form, by sorting): sigmoid
+    modes select on sigmoid + bias and weigh the sigmoid; groups score by their largest logit
+    (softmax) or the sum of their two largest selection values (sigmoid, the two last entries
+    of the group's sorted values), the topk_group best stay eligible."""
     from bigrig_amd import formats as F
     x = F.bf16_bits_to_f32(x_bits).astype(np.float64)
     W = (np.asarray(w, np.float64) if w_f32 else F.bf16_bits_to_f32(w).astype(np.float64))
     lg = x @ W.T
-    if bias is not None:
-        lg = lg + np.asarray(bias, np.float64)
-    order = np.argsort(-lg, axis=-1, kind="stable")[:, :k]
+    sig = mode >= 3
+    b = None if bias is None else np.asarray(bias, np.float64)
+    if b is not None and not sig:
+        lg = lg + b
+    s = 1.0 / (1.0 + np.exp(-lg)) if sig else None
+    c = (s + (0.0 if b is None else b)) if sig else lg.copy()
+    if n_group > 1:
+        T, E = c.shape
+        g = c.reshape(T, n_group, E // n_group)
+        gscore = np.sort(g, -1)[..., -2:].sum(-1) if sig else g.max(-1)
+        best = np.argsort(-gscore, axis=-1, kind="stable")[:, :topk_group]
+        keep = np.zeros((T, n_group), bool)
+        np.put_along_axis(keep, best, True, -1)
+        c = np.where(np.repeat(keep, E // n_group, axis=1), c, 0.0 if sig else -np.inf)
+    order = np.argsort(-c, axis=-1, kind="stable")[:, :k]
+    if sig:
+        wts = np.take_along_axis(s, order, -1)
+        if mode == 4:
+            wts = wts / wts.sum(-1, keepdims=True)
+        return lg, order, wts * scale
     sel = np.take_along_axis(lg, order, -1)
     if mode == 2:
         ex = np.exp(sel - sel[:, :1])
@@ -237,7 +271,7 @@ def router_f64(x_bits, w, w_f32: bool, bias, k: int, mode: int):
         wts = np.take_along_axis(p, order, -1)
         if mode == 1:
             wts = wts / wts.sum(-1, keepdims=True)
-    return lg, order, wts
+    return lg, order, wts * scale
 
 
 def rel_l2(a, b) -> float:

@@ -83,12 +83,86 @@ float orc_dot_lane_tree(const uint16_t* x, const void* w, int w_f32, int H) {
     return a[0];
 }
 
-/* logits [T, E]; idx [T, k]; wts [T, k]; mode 0 softmax-topk, 1 + renorm, 2 topk-softmax.
+/* e^x as x = n ln2 + r (|r| <= ln2 / 2; ln2 split into a 12-bit head and a tail, Cody-Waite),
+ * e^r by its Taylor polynomial of degree 7 in Horner form with fused multiply-adds, scaled by
+ * 2^n. Every step is one correctly rounded operation, so the kernels' copy of this function
+ * gives the same bits; within 2 ulp of e^x. Used for the sigmoid routing scores, whose
+ * ordering must agree bit for bit. */
+float orc_exp_rt(float x) {
+    if (x > 88.5f) return INFINITY;
+    if (x < -104.0f) return 0.0f;
+    const float n = rintf(x * 1.44269502f);
+    float r = fmaf(-n, 0.693115234375f, x);
+    r = fmaf(-n, 3.19461833e-05f, r);
+    float p = 1.98412701e-04f;
+    p = fmaf(p, r, 1.38888892e-03f);
+    p = fmaf(p, r, 8.33333377e-03f);
+    p = fmaf(p, r, 4.16666679e-02f);
+    p = fmaf(p, r, 1.66666672e-01f);
+    p = fmaf(p, r, 0.5f);
+    p = fmaf(p, r, 1.0f);
+    p = fmaf(p, r, 1.0f);
+    return ldexpf(p, (int)n);
+}
+
+static float sigmoid_rt(float v) { return 1.0f / (1.0f + orc_exp_rt(-v)); }
+
+/* Selection values of one token (mode 3/4: sigmoid(logit) + bias; else the logit), with the
+ * experts outside the topk_group best of n_group contiguous groups taken out (sigmoid: 0;
+ * softmax: never picked, marked in `out`). A group scores its largest logit (softmax) or the
+ * sum of its two largest selection values (sigmoid), following mlx_lm's group_expert_select /
+ * group_limited_greedy (DeepSeek-V3 / V2 routers; the rule adapter.py:75-93 names). Group ties
+ * go to the lower group. */
+static void orc_select_values(const float* lg, const float* bias, int E, int mode, int n_group,
+                              int topk_group, float* c, unsigned char* out) {
+    const int sig = mode >= 3;
+    for (int e = 0; e < E; ++e) {
+        c[e] = sig ? sigmoid_rt(lg[e]) + (bias ? bias[e] : 0.0f) : lg[e];
+        out[e] = 0;
+    }
+    if (n_group <= 1) return;
+    const int G = E / n_group;
+    float gs[64];
+    for (int g = 0; g < n_group; ++g) {
+        /* the largest value and the largest of the rest (one holder of the maximum set aside) */
+        int i1 = -1;
+        for (int e = g * G; e < (g + 1) * G; ++e)
+            if (i1 < 0 || c[e] > c[i1]) i1 = e;
+        float second = -INFINITY;
+        for (int e = g * G; e < (g + 1) * G; ++e)
+            if (e != i1 && c[e] > second) second = c[e];
+        gs[g] = sig ? c[i1] + second : c[i1];
+    }
+    unsigned char keep[64] = {0};
+    for (int r = 0; r < topk_group; ++r) {
+        int best = -1;
+        for (int g = 0; g < n_group; ++g)
+            if (!keep[g] && (best < 0 || gs[g] > gs[best])) best = g;
+        keep[best] = 1;
+    }
+    for (int e = 0; e < E; ++e)
+        if (!keep[e / G]) {
+            if (sig) c[e] = 0.0f;
+            else out[e] = 1;
+        }
+}
+
+/* logits [T, E]; idx [T, k]; wts [T, k]; mode 0 softmax-topk, 1 + renorm, 2 topk-softmax,
+ * 3 sigmoid-topk (select on sigmoid + bias, weigh sigmoid), 4 + renorm. Softmax modes add `bias`
+ * to the logits; sigmoid modes use it for selection only. n_group > 1 limits the top-k to the
+ * topk_group best groups; every weight is multiplied by `scale`.
  * shared_gate_w [H] bf16 or NULL -> sgate [T] = sigmoid(dot). Returns 0, or -1 on bad args. */
 int orc_router(const uint16_t* x, const void* w, int w_f32, const float* bias,
                const uint16_t* shared_gate_w, int T, int H, int E, int k, int mode,
+               int n_group, int topk_group, float scale,
                float* logits, int32_t* idx, float* wts, float* sgate) {
-    if (H % 8 || k < 1 || k > E || E < 1) return -1;
+    if (H % 8 || k < 1 || k > E || E < 1 || mode < 0 || mode > 4) return -1;
+    if (n_group > 1 && (n_group > 64 || E % n_group || topk_group < 1 || topk_group > n_group ||
+                        k > topk_group * (E / n_group)))
+        return -1;
+    const int sig = mode >= 3;
+    float* c = (float*)malloc(sizeof(float) * (size_t)E);
+    unsigned char* taken = (unsigned char*)malloc((size_t)E);
     for (int t = 0; t < T; ++t) {
         const uint16_t* xt = x + (size_t)t * H;
         float* lg = logits + (size_t)t * E;
@@ -96,40 +170,51 @@ int orc_router(const uint16_t* x, const void* w, int w_f32, const float* bias,
             const void* we = w_f32 ? (const void*)((const float*)w + (size_t)e * H)
                                    : (const void*)((const uint16_t*)w + (size_t)e * H);
             float v = orc_dot_lane_tree(xt, we, w_f32, H);
-            if (bias) v = v + bias[e];
+            if (bias && !sig) v = v + bias[e];
             lg[e] = v;
         }
-        unsigned char* taken = (unsigned char*)calloc((size_t)E, 1);
+        orc_select_values(lg, sig ? bias : NULL, E, mode, n_group, topk_group, c, taken);
         for (int r = 0; r < k; ++r) {
             int best = -1;
             for (int e = 0; e < E; ++e)
-                if (!taken[e] && (best < 0 || lg[e] > lg[best])) best = e;
+                if (!taken[e] && (best < 0 || c[e] > c[best])) best = e;
             taken[best] = 1;
             idx[(size_t)t * k + r] = best;
         }
-        free(taken);
         float* wt = wts + (size_t)t * k;
         const int32_t* it = idx + (size_t)t * k;
-        float m = lg[it[0]];
-        if (mode == 2) {
-            float s = 0.0f;
-            for (int r = 0; r < k; ++r) s += expf(lg[it[r]] - m);
-            for (int r = 0; r < k; ++r) wt[r] = expf(lg[it[r]] - m) / s;
-        } else {
-            float s = 0.0f;
-            for (int e = 0; e < E; ++e) s += expf(lg[e] - m);
-            for (int r = 0; r < k; ++r) wt[r] = expf(lg[it[r]] - m) / s;
-            if (mode == 1) {
+        if (sig) {
+            for (int r = 0; r < k; ++r) wt[r] = sigmoid_rt(lg[it[r]]);
+            if (mode == 4) {
                 float z = 0.0f;
                 for (int r = 0; r < k; ++r) z += wt[r];
                 for (int r = 0; r < k; ++r) wt[r] = wt[r] / z;
             }
+        } else {
+            float m = lg[it[0]];
+            if (mode == 2) {
+                float s = 0.0f;
+                for (int r = 0; r < k; ++r) s += expf(lg[it[r]] - m);
+                for (int r = 0; r < k; ++r) wt[r] = expf(lg[it[r]] - m) / s;
+            } else {
+                float s = 0.0f;
+                for (int e = 0; e < E; ++e) s += expf(lg[e] - m);
+                for (int r = 0; r < k; ++r) wt[r] = expf(lg[it[r]] - m) / s;
+                if (mode == 1) {
+                    float z = 0.0f;
+                    for (int r = 0; r < k; ++r) z += wt[r];
+                    for (int r = 0; r < k; ++r) wt[r] = wt[r] / z;
+                }
+            }
         }
+        for (int r = 0; r < k; ++r) wt[r] = wt[r] * scale;
         if (shared_gate_w && sgate) {
             float d = orc_dot_lane_tree(xt, shared_gate_w, 0, H);
             sgate[t] = 1.0f / (1.0f + expf(-d));
         }
     }
+    free(c);
+    free(taken);
     return 0;
 }
 

@@ -14,7 +14,9 @@ import pytest
 
 from bigrig_amd import checkpoint as CK
 from bigrig_amd import formats as F
+from bigrig_amd.spec import QWEN3_30B_A3B
 from tests.ckpt_util import make_checkpoint, write_safetensors
+from tests.helpers import small
 
 Q4 = F.QuantSpec(4, 64, "affine")
 Q3 = F.QuantSpec(3, 64, "affine")
@@ -101,8 +103,30 @@ def test_layer_spec_and_routing_from_config(tmp_path):
     assert s.bytes_per_expert == cm.layers["0"]["bytes_per_expert"]
     assert CK.layer_spec(cm, 0, top_k=4).top_k == 4
     assert CK.routing_from_config({"norm_topk_prob": False})["route"] == "softmax_topk"
-    with pytest.raises(ValueError, match="sigmoid"):
-        CK.routing_from_config({"scoring_func": "sigmoid", "n_group": 8})
+
+
+def test_routing_rule_follows_the_adapter():
+    """adapter.py:75-93: the named score function wins; with none named, expert groups mean
+    sigmoid; groups make the selection group-limited; norm_topk_prob renormalises;
+    routed_scaling_factor scales the weights."""
+    r = CK.routing_from_config({"scoring_func": "sigmoid", "n_group": 8, "topk_group": 4,
+                                "norm_topk_prob": True, "routed_scaling_factor": 2.5})
+    assert r == {"route": "sigmoid_topk_renorm", "act": "swiglu", "n_group": 8, "topk_group": 4,
+                 "route_scale": 2.5}
+    assert CK.routing_from_config({"n_group": 8, "topk_group": 3})["route"] == "sigmoid_topk"
+    v2 = CK.routing_from_config({"scoring_func": "softmax", "n_group": 8, "topk_group": 3,
+                                 "routed_scaling_factor": 16.0})
+    assert v2["route"] == "softmax_topk" and v2["n_group"] == 8 and v2["route_scale"] == 16.0
+    assert CK.routing_from_config({"score_function": "sigmoid"})["route"] == "sigmoid_topk"
+    assert "n_group" not in CK.routing_from_config({"norm_topk_prob": True})
+    spec = small(QWEN3_30B_A3B, n_experts=256, **{k: v for k, v in r.items() if k != "act"})
+    assert (spec.route_mode, spec.n_group, spec.topk_group, spec.route_scale) == (4, 8, 4, 2.5)
+    d = spec.desc()
+    assert (d.route_mode, d.n_group, d.topk_group, d.route_scale) == (4, 8, 4, 2.5)
+    with pytest.raises(ValueError, match="group-limited"):
+        small(QWEN3_30B_A3B, n_experts=256, top_k=8, n_group=8, topk_group=0)
+    with pytest.raises(ValueError, match="group-limited"):
+        small(QWEN3_30B_A3B, n_experts=100, n_group=8, topk_group=2)
 
 
 def test_quantisation_is_decided_by_the_tensors(tmp_path):

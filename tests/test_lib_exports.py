@@ -33,9 +33,9 @@ def test_library_loads_and_exports_every_symbol():
     raw = C.CDLL(L.LIB)
     for name in _declared():
         assert hasattr(raw, name), name
-    assert lib.brx_abi_version() == 1
+    assert lib.brx_abi_version() == L.ABI_VERSION == 2
     src = open(HEADER).read()
-    assert int(re.search(r"#define BRX_ABI_VERSION (\d+)", src).group(1)) == 1
+    assert int(re.search(r"#define BRX_ABI_VERSION (\d+)", src).group(1)) == L.ABI_VERSION
 
 
 def test_header_enums_match_binding():
@@ -43,14 +43,16 @@ def test_header_enums_match_binding():
     for cname, val in (("BRX_EINVAL", L.BRX_EINVAL), ("BRX_ESTATE", L.BRX_ESTATE),
                        ("BRX_ERANGE", L.BRX_ERANGE), ("BRX_QUANT_MXFP4", L.QUANT_MXFP4),
                        ("BRX_ACT_SWIGLU_CLAMPED", L.ACT_SWIGLU_CLAMPED),
-                       ("BRX_ROUTE_TOPK_SOFTMAX", L.ROUTE_TOPK_SOFTMAX), ("BRX_DT_BF16", L.DT_BF16),
+                       ("BRX_ROUTE_TOPK_SOFTMAX", L.ROUTE_TOPK_SOFTMAX),
+                       ("BRX_ROUTE_SIGMOID_TOPK_RENORM", L.ROUTE_SIGMOID_TOPK_RENORM),
+                       ("BRX_DT_BF16", L.DT_BF16),
                        ("BRX_FWD_FORCE_PREFILL", L.FWD_FORCE_PREFILL),
                        ("BRX_FWD_PHASE_B", L.FWD_PHASE_B), ("BRX_FWD_PHASE_R", L.FWD_PHASE_R)):
         m = re.search(rf"\b{cname}\s*=\s*(-?\d+)", src) or \
             re.search(rf"#define {cname}\s+\(?(-?\d+)u?", src)
         assert m, cname
         assert int(m.group(1)) == val, cname
-    assert C.sizeof(L.LayerDesc) == 64 and C.sizeof(L.ExpertLayout) == 13 * 8
+    assert C.sizeof(L.LayerDesc) == 80 and C.sizeof(L.ExpertLayout) == 13 * 8
 
 
 @pytest.mark.parametrize("spec", SPECS, ids=lambda s: f"H{s.hidden}I{s.inter}{s.quant.mode}")
@@ -76,8 +78,9 @@ def test_expert_layout_matches_formats(spec):
 
 BAD = [("hidden", 100, "hidden"), ("inter", 0, "inter"), ("n_experts", 513, "n_experts"),
        ("top_k", 0, "top_k"), ("bits", 5, "affine"), ("group_size", 128, "affine"),
-       ("quant_mode", 7, "quant_mode"), ("act", 5, "act"), ("route_mode", 3, "route_mode"),
-       ("router_dtype", 9, "router_dtype"), ("shared_inter", 96, "shared_inter"),
+       ("quant_mode", 7, "quant_mode"), ("act", 5, "act"), ("route_mode", 5, "route_mode"),
+       ("n_group", 65, "n_group"), ("n_group", 3, "divide"), ("n_group", 4, "topk_group 0 outside"),
+       ("route_scale", -1.0, "route_scale"), ("router_dtype", 9, "router_dtype"), ("shared_inter", 96, "shared_inter"),
        ("hidden", 8256, "at most 8192"), ("inter", 8256, "at most 8192"),
        ("shared_inter", 8256, "at most 8192")]
 

@@ -160,6 +160,118 @@ def test_router_shared_gate_and_errors():
         oracle.router(x[:, :250], wr[:, :250], False, None, 2, 1)   # H not a multiple of 8
 
 
+# ------------------------------------------------------------------ sigmoid / group-limited
+def test_exp_rt_is_within_two_ulp():
+    """The routing exponential against float64 exp over its whole normal range and the
+    reduction's edges (n ln2 +- ln2/2), where a wrong split constant or a dropped Taylor term
+    shows first."""
+    xs = np.concatenate([np.linspace(-87.0, 88.0, 20001, dtype=np.float32),
+                         (np.arange(-120, 121) * np.log(2) / 2).astype(np.float32),
+                         np.float32([0.0, -0.0, 1e-8, -1e-8, 0.5, -0.5])])
+    xs = xs[(xs > -87.0) & (xs < 88.5)]
+    got = oracle.exp_rt(xs).astype(np.float64)
+    want = np.exp(xs.astype(np.float64))
+    ulp = np.spacing(want.astype(np.float32)).astype(np.float64)
+    assert (np.abs(got - want) <= 2 * ulp).all(), np.max(np.abs(got - want) / ulp)
+    assert oracle.exp_rt(np.float32([0.0]))[0] == 1.0
+    assert np.isinf(oracle.exp_rt(np.float32([100.0]))[0])
+    assert oracle.exp_rt(np.float32([-200.0]))[0] == 0.0
+
+
+def _onehot_router(logits):
+    """(x bits [1, 8], fp32 router [E, 8]) whose logits are exactly `logits`: x = e_0."""
+    E = len(logits)
+    w = np.zeros((E, 8), np.float32)
+    w[:, 0] = logits
+    x = np.zeros((1, 8), np.uint16)
+    x[0, 0] = 0x3F80                      # bf16 1.0
+    return x, w
+
+
+def test_group_limited_kats():
+    """Hand-built logits where each rule's choice is known. Two groups of four experts, one
+    group kept, top-2:
+      - sigmoid: group 0 = [3, -3, -3, -3], group 1 = [2, 2, -3, -3]. Top-2 sums pick group 1
+        (0.881 + 0.881 > 0.953 + 0.047), where scoring by the maximum would pick group 0; the
+        tied pair goes lower id first; the weights are the plain sigmoids.
+      - a selection bias of +1 on expert 1 moves the choice to group 0 ([1, 0]) while the
+        weights stay sigmoid(logit): the bias selects, it does not weigh.
+      - softmax groups score by their maximum logit: group 0, experts [0, 1]."""
+    lg = np.float32([3, -3, -3, -3, 2, 2, -3, -3])
+    x, w = _onehot_router(lg)
+    sig = lambda v: 1.0 / (1.0 + np.exp(-np.float64(v)))
+    _, idx, wt, _ = oracle.router(x, w, True, None, 2, 3, n_group=2, topk_group=1)
+    assert idx.tolist() == [[4, 5]]
+    np.testing.assert_allclose(wt[0], [sig(2), sig(2)], rtol=1e-6)
+    bias = np.zeros(8, np.float32)
+    bias[1] = 1.0
+    lgo, idx, wt, _ = oracle.router(x, w, True, bias, 2, 3, n_group=2, topk_group=1)
+    assert idx.tolist() == [[1, 0]] and (lgo == lg).all()     # logits stay raw
+    np.testing.assert_allclose(wt[0], [sig(-3), sig(3)], rtol=1e-6)
+    _, idx, wt, _ = oracle.router(x, w, True, None, 2, 0, n_group=2, topk_group=1)
+    assert idx.tolist() == [[0, 1]]
+    p = np.exp(lg - lg.max()) / np.exp(lg - lg.max()).sum()
+    np.testing.assert_allclose(wt[0], p[[0, 1]], rtol=1e-6)
+    # renormalised sigmoid weights sum to one, then carry the scale
+    _, _, wt, _ = oracle.router(x, w, True, None, 2, 4, n_group=2, topk_group=1, scale=2.5)
+    np.testing.assert_allclose(wt.sum(), 2.5, rtol=1e-6)
+
+
+GROUP_RULES = [  # (E, k, mode, n_group, topk_group, scale, bias)
+    (256, 8, 4, 8, 4, 2.5, True),        # DeepSeek-V3 shape
+    (256, 8, 3, 8, 4, 1.0, False),
+    (64, 6, 0, 8, 3, 16.0, False),       # DeepSeek-V2-style softmax groups
+    (128, 8, 4, 0, 0, 1.0, True),        # sigmoid, no groups
+    (64, 4, 1, 4, 2, 1.0, False),
+]
+
+
+@pytest.mark.parametrize("rule", GROUP_RULES, ids=lambda r: f"E{r[0]}k{r[1]}m{r[2]}g{r[3]}/{r[4]}")
+def test_group_rules_match_f64(rule):
+    """The C rule against the float64 closed form (sorting, group top-2 from sorted groups),
+    rows in order with weights to 2e-6."""
+    E, k, mode, ng, tg, scale, with_bias = rule
+    rng = np.random.default_rng(E + 7 * k + mode)
+    H = 256
+    wr = rng.standard_normal((E, H)).astype(np.float32) * 0.05
+    bias = (rng.standard_normal(E).astype(np.float32) * 0.05) if with_bias else None
+    x = make_x(48, H, seed=E + mode)
+    _, idx, wt, _ = oracle.router(x, wr, True, bias, k, mode, n_group=ng, topk_group=tg,
+                                  scale=scale)
+    _, idx64, w64 = oracle.router_f64(x, wr, True, bias, k, mode, n_group=ng, topk_group=tg,
+                                      scale=scale)
+    assert np.array_equal(idx, idx64)
+    np.testing.assert_allclose(wt, w64, rtol=2e-6, atol=1e-7)
+    if ng > 1:    # every pick lies in at most topk_group groups
+        assert max(len(set((r // (E // ng)).tolist())) for r in idx) <= tg
+
+
+def test_group_rule_reductions():
+    """Special cases that reduce to the plain rules: keeping every group is no limit; sigmoid
+    without bias picks the softmax top-k (both monotonic in the logit); the scale multiplies the
+    weights exactly."""
+    rng = np.random.default_rng(21)
+    E, H, k = 64, 128, 6
+    wr = rng.standard_normal((E, H)).astype(np.float32) * 0.05
+    x = make_x(16, H, seed=22)
+    for mode in (0, 1, 3, 4):
+        base = oracle.router(x, wr, True, None, k, mode)
+        allg = oracle.router(x, wr, True, None, k, mode, n_group=8, topk_group=8)
+        assert np.array_equal(base[1], allg[1]) and np.array_equal(base[2], allg[2])
+    _, i_soft, _, _ = oracle.router(x, wr, True, None, k, 0)
+    lg, i_sig, w_sig, _ = oracle.router(x, wr, True, None, k, 3)
+    assert np.array_equal(i_soft, i_sig)
+    np.testing.assert_allclose(w_sig, 1 / (1 + np.exp(-np.take_along_axis(lg, i_sig, -1)
+                                                     .astype(np.float64))), rtol=1e-6)
+    _, _, w1, _ = oracle.router(x, wr, True, None, k, 4, n_group=8, topk_group=2)
+    _, _, w3, _ = oracle.router(x, wr, True, None, k, 4, n_group=8, topk_group=2, scale=3.0)
+    assert np.array_equal(w3, w1 * np.float32(3.0))
+    with pytest.raises(ValueError):
+        oracle.router(x, wr, True, None, k, 4, n_group=8, topk_group=0)
+    with pytest.raises(ValueError):
+        oracle.router(x, wr, True, None, 20, 4, n_group=8, topk_group=2)   # k > 2 groups of 8
+
+
 # ------------------------------------------------------------------ dequant
 @pytest.mark.parametrize("q", [F.QuantSpec(4, 64, "affine", "bfloat16"),
                                F.QuantSpec(4, 64, "affine", "float16"),
