@@ -657,12 +657,12 @@ static int block_forward_impl(const brx_layer_desc* d, brx_pool* p, const void* 
     a.sgate = rsg;
     hipError_t e = hipSuccess;
     if (decode) {
-        if (do_route) e = launch_router_logits(*d, x, w_router, router_bias, shared_gate_w, T, logits, s);
         a.logits = logits;
         a.route_bias = route_rule(*d, router_bias).bias;
         a.route_idx = ridx;
         a.route_w = rw;
         a.route_sg = rsg;
+        if (do_route) e = launch_router_logits(*d, x, w_router, router_bias, shared_gate_w, T, logits, s);
     } else if (do_route) {
         e = launch_router(*d, x, w_router, router_bias, shared_gate_w, T, ridx, rw, rsg, logits, s);
     }

@@ -41,7 +41,8 @@ __device__ __forceinline__ uint32_t pair3(uint32_t g, int i) {
 
 // ------------------------------------------------------------------ layout (host + device)
 struct Proj {
-    int64_t w, s, b, bias;  // byte offsets inside the expert (-1 = absent)
+    int32_t w, s, b, bias;  // byte offsets inside the expert (-1 = absent); widths <= 8192 keep
+                            // an expert under 2^31 bytes
     int32_t n_out, n_in;
 };
 
@@ -67,16 +68,16 @@ inline Layout make_layout(const brx_layer_desc& d, int inter) {
         int64_t G = n_in / d.group_size;
         L.p[p].n_out = n_out;
         L.p[p].n_in = n_in;
-        L.p[p].w = pos;
+        L.p[p].w = (int32_t)pos;
         pos += (int64_t)n_out * n_in * d.bits / 8;
         if (d.quant_mode == BRX_QUANT_AFFINE) {
-            L.p[p].s = pos; pos += (int64_t)n_out * G * 2;
-            L.p[p].b = pos; pos += (int64_t)n_out * G * 2;
+            L.p[p].s = (int32_t)pos; pos += (int64_t)n_out * G * 2;
+            L.p[p].b = (int32_t)pos; pos += (int64_t)n_out * G * 2;
         } else {
-            L.p[p].s = pos; pos += (int64_t)n_out * G;
+            L.p[p].s = (int32_t)pos; pos += (int64_t)n_out * G;
             L.p[p].b = -1;
         }
-        if (d.has_bias) { L.p[p].bias = pos; pos += (int64_t)n_out * 2; }
+        if (d.has_bias) { L.p[p].bias = (int32_t)pos; pos += (int64_t)n_out * 2; }
         else L.p[p].bias = -1;
     }
     L.bytes = pos;
@@ -242,18 +243,37 @@ __device__ __forceinline__ float readlane_f(float v, int lane) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
 }
 
+// v combined with a row broadcast (DPP row_bcast:15 or row_bcast:31) into the rows `rows`;
+// the other rows keep v.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ float bcast_f(float v) {
+    const int b = __builtin_bit_cast(int, v);
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(b, b, CTRL, ROWS, 0xF, false));
+}
+
 // Max over the 64 lanes of a wave, returned to every lane: quad_perm [1,0,3,2] and [2,3,0,1],
-// row_half_mirror and row_mirror leave each row of 16 lanes holding its maximum; the four row
-// results are then combined through lane reads.
+// row_half_mirror and row_mirror leave each row of 16 lanes holding its maximum; row_bcast:15
+// into rows 1 and 3 and row_bcast:31 into rows 2 and 3 carry them to lane 63, read once (one
+// lane read instead of four: the top-k ranking calls this k times in a dependent chain).
 __device__ __forceinline__ float wave_max(float v) {
     v = fmaxf(v, dpp_f<0xB1>(v));
     v = fmaxf(v, dpp_f<0x4E>(v));
     v = fmaxf(v, dpp_f<0x141>(v));
     v = fmaxf(v, dpp_f<0x140>(v));
-    return fmaxf(fmaxf(readlane_f(v, 0), readlane_f(v, 16)), fmaxf(readlane_f(v, 32), readlane_f(v, 48)));
+    v = fmaxf(v, bcast_f<0x142, 0xA>(v));
+    v = fmaxf(v, bcast_f<0x143, 0xC>(v));
+    return readlane_f(v, 63);
 }
 
-// Sum over the 64 lanes of a wave by the same pattern, returned to every lane.
+// Sum over the 64 lanes of a wave by an xor butterfly (offsets 32, 16, ..., 1): the router
+// logits' reduction order.
+__device__ __forceinline__ float wave_sum_xor(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+}
+
+// Sum over the 64 lanes of a wave by wave_max's DPP pattern, returned to every lane.
 __device__ __forceinline__ float wave_sum(float v) {
     v += dpp_f<0xB1>(v);
     v += dpp_f<0x4E>(v);
@@ -432,18 +452,25 @@ __device__ __forceinline__ void wave_select(const float v[kPer], const RouteRule
 
 // The routing weight of the rank this lane holds (lanes >= k: 0), after wave_select. Softmax
 // modes weigh as wave_route_weight (an eligible expert's selection value is its logit);
-// sigmoid modes weigh sigmoid(logit) of the chosen expert, read back from `lrow` (the token's
-// logits in memory), renormalised to sum 1 for BRX_ROUTE_SIGMOID_TOPK_RENORM. The weight is
-// then multiplied by the rule's scale.
+// sigmoid modes weigh sigmoid(logit) of the chosen expert, whose logit is fetched from the
+// lane holding it (lane sel_e % 64, register sel_e / 64), renormalised to sum 1 for
+// BRX_ROUTE_SIGMOID_TOPK_RENORM. The weight is then multiplied by the rule's scale.
 template <int kPer>
-__device__ __forceinline__ float wave_weight(const float v[kPer], const float* lrow, const RouteRule& rr,
-                                             int E, int k, int sel_e, float sel_v) {
+__device__ __forceinline__ float wave_weight(const float v[kPer], const RouteRule& rr, int E, int k, int sel_e,
+                                             float sel_v) {
     const int lane = threadIdx.x & (kWave - 1);
     float w;
     if (!route_sigmoid(rr.mode)) {
         w = wave_route_weight<kPer>(v, E, k, rr.mode, sel_v);
     } else {
-        const float s = lane < k && sel_e >= 0 ? sigmoid_f(lrow[sel_e]) : 0.0f;
+        const int src = sel_e >= 0 ? sel_e : 0;
+        float lg = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const float t = __shfl(v[i], src & (kWave - 1), kWave);
+            if ((src >> 6) == i) lg = t;
+        }
+        const float s = lane < k && sel_e >= 0 ? sigmoid_f(lg) : 0.0f;
         w = rr.mode == BRX_ROUTE_SIGMOID_TOPK_RENORM ? s / wave_sum(s) : s;
     }
     return w * rr.scale;

@@ -147,7 +147,7 @@ __device__ __forceinline__ void route_rank(const FwdArgs& a, const RouteRegs<kPe
         wave_select<kPer>(rg.v[tt], rr, E, k, sel_e, sel_v);
         if (lane < k) s_e[t * k + lane] = sel_e;
         if (publish) {
-            const float w = wave_weight<kPer>(rg.v[tt], a.logits + (int64_t)t * (E + 1), rr, E, k, sel_e, sel_v);
+            const float w = wave_weight<kPer>(rg.v[tt], rr, E, k, sel_e, sel_v);
             if (lane < k) {
                 a.route_idx[t * k + lane] = sel_e;
                 a.route_w[t * k + lane] = w;
@@ -615,6 +615,122 @@ __global__ __launch_bounds__(kThreads) void k_dec_gateup(FwdArgs a, uint16_t* __
     }
 }
 
+// ------------------------------------------------------------------ gate/up, one token
+// One token's gate/up: entry u is pair u (the shared expert last) and the (entry, row) items
+// are dealt out one per row group, RG row groups a block, in order. Wave 0 ranks the routing,
+// holds the slot table in registers and resolves every entry's slot before the block's one
+// barrier -- no per-block entry planning, which for several tokens merges repeated experts --
+// and block 0 records the entry table for the down kernel.
+template <int MODE, int UPL, int KP>
+__global__ __launch_bounds__(kThreads) void k_dec_gateup1(FwdArgs a, uint16_t* __restrict__ hbuf, int hstride,
+                                                          DecTable* __restrict__ table, int lsp, int nu) {
+    prefetch_args(a);
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    __shared__ int32_t s_slot[kMaxU];
+    constexpr int kG = 8;                         // slot-table registers per lane (E <= 512)
+    const int SP = 1 << lsp;
+    const int lane = threadIdx.x & 63, tid = threadIdx.x, wv = tid >> 6;
+    const int H = a.H, U = H / 64, E = a.E, P = a.P;
+    const int Imax = hstride;
+    uint8_t* xs = lds;
+    float* xsum = reinterpret_cast<float*>(lds + (size_t)U * kXU);
+    // one round trip: the routing (logits or the given pairs), the slot table (wave 0) and x
+    const int ng = (E + kWave - 1) / kWave;
+    int g2s[kG];
+    if (wv == 0) {
+#pragma unroll
+        for (int i = 0; i < kG; ++i) g2s[i] = i < ng ? a.g2s[min(lane + kWave * i, E - 1)] : -1;
+    }
+    int pe = 0;
+    if constexpr (KP == 0) pe = a.pexp[min(lane, P - 1)];
+    RouteRegs<(KP > 0 ? KP : 1)> rg;
+    if constexpr (KP > 0)
+        if (wv == 0) route_load<KP>(a, rg);
+    StageRegs st;
+    auto tok_row = [](int i) { return i; };
+    stage_issue(a.x, H, 1, tok_row, 0, st);
+    stage_store<MODE>(H, 1, 0, st, xs, xsum);
+    stage_rows<MODE>(a.x, H, 1, tok_row, xs, xsum, kStageB);
+    if (wv == 0) {
+        int e = pe;
+        if constexpr (KP > 0) {
+            const RouteRule rr{a.route_bias, a.route_mode, a.n_group, a.topk_group, a.route_scale};
+            float sel_v;
+            wave_select<KP>(rg.v[0], rr, E, a.k, e, sel_v);
+            if (blockIdx.x == 0) {
+                const float w = wave_weight<KP>(rg.v[0], rr, E, a.k, e, sel_v);
+                if (lane < a.k) {
+                    a.route_idx[lane] = e;
+                    a.route_w[lane] = w;
+                }
+                if (lane == 0 && a.route_sg)
+                    a.route_sg[0] = 1.0f / (1.0f + expf(-a.logits[E]));
+            }
+        }
+        // entry lane < P: expert e's slot, fetched from the lane holding its table entry
+        const int ec = min(max(e, 0), E - 1);
+        int v = -1;
+#pragma unroll
+        for (int i = 0; i < kG; ++i) {
+            const int t = __shfl(g2s[i], ec & (kWave - 1), kWave);
+            if (i == (ec >> 6)) v = t;
+        }
+        int slot = -1;
+        if (lane < P) {
+            slot = slot_code(a, ec, v);
+            if (slot == kAbsentCode) note_absent(a, ec);
+        }
+        if (lane < nu) s_slot[lane] = slot;
+        if (blockIdx.x == 0 && lane < nu) {
+            DecEntry& d = table->ent[lane];
+            d.slot = slot;
+            d.nt = 1;
+            d.pair[0] = lane;
+        }
+        if (blockIdx.x == 0 && lane == 0) table->n = nu;
+    }
+    __syncthreads();
+
+    const int RGn = kWaves * (kWave >> lsp);          // row groups per block
+    const int g = lane >> lsp, sl = lane & (SP - 1);
+    const int q = blockIdx.x * RGn + wv * (kWave >> lsp) + g;
+    const int u = min(q / Imax, nu - 1), r = q - (q / Imax) * Imax;
+    const int slot = s_slot[u];
+    const bool sh = slot == -1;
+    const int inter = sh ? a.I_sh : a.I;
+    const bool ok = q < nu * Imax && r < inter;
+    const Layout& L = sh ? a.lay_sh : a.lay;
+    const uint8_t* base = code_base(a, clamp_code(a, slot));
+    const int row = min(r, inter - 1);
+    const bool gated = a.act != BRX_ACT_SILU_MLP;
+    if (!ok) return;   // rows past a narrower entry (no barrier follows)
+    Units<MODE, UPL> ug, uu;
+    units_load<MODE, UPL>(base, L.p[0], row, sl, SP, ug);
+    if (gated) units_load<MODE, UPL>(base, L.p[1], row, sl, SP, uu);
+    float bg = 0.f, bu = 0.f;
+    if (L.p[0].bias >= 0) {
+        bg = bf2f(reinterpret_cast<const uint16_t*>(base + L.p[0].bias)[row]);
+        if (gated) bu = bf2f(reinterpret_cast<const uint16_t*>(base + L.p[1].bias)[row]);
+    }
+    float pg = 0.f, pu = 0.f;
+#pragma unroll
+    for (int j = 0; j < UPL; ++j) {
+        const int un = sl + SP * j;
+        if (un < U) {
+            const uint4* xu = reinterpret_cast<const uint4*>(xs + (int64_t)un * kXU);
+            const float sx = kAffine<MODE> ? xsum[un] : 0.0f;
+            pg += unit_dot<MODE, UPL>(ug, j, xu, sx, a.scale_f16);
+            if (gated) pu += unit_dot<MODE, UPL>(uu, j, xu, sx, a.scale_f16);
+        }
+    }
+    pg = group_sum(pg, SP);
+    if (gated) pu = group_sum(pu, SP);
+    if (sl == 0) {
+        const float h = slot == kAbsentCode ? absent_nan() : act_apply(a.act, pg + bg, pu + bu, a.alpha, a.limit);
+        hbuf[(int64_t)u * hstride + r] = (uint16_t)f2bf(h);
+    }
+}
+
 // ------------------------------------------------------------------ down + combine
 // Each pair's row result rounded to bf16 (the projection's output, with its bias), the
 // unreduced rows when asked for, and the k-ordered combine out[t] = sum_j w[t,j] * y[t,j]
@@ -927,6 +1043,24 @@ hipError_t launch_gateup(const FwdArgs& a, uint16_t* hbuf, DecTable* table, int 
     return hipGetLastError();
 }
 
+// One token (token mode): one (entry, row) item per row group.
+template <int MODE, int UPL>
+hipError_t launch_gateup1(const FwdArgs& a, uint16_t* hbuf, DecTable* table, int nu, int Imax, int SP,
+                          hipStream_t s) {
+    const int RGn = kWaves * (kWave / SP);
+    const int nblk = (nu * Imax + RGn - 1) / RGn;
+    const size_t lds = (size_t)(a.H / 64) * (kXU + 4);
+    const int lsp = __builtin_ctz(SP);
+#define BRX_G1(KP) hipLaunchKernelGGL((k_dec_gateup1<MODE, UPL, KP>), dim3(nblk), dim3(kThreads), lds, s, a, hbuf, \
+                                      Imax, table, lsp, nu)
+    if (!a.logits) BRX_G1(0);
+    else if (a.E <= 64) BRX_G1(1);
+    else if (a.E <= 128) BRX_G1(2);
+    else BRX_G1(4);
+#undef BRX_G1
+    return hipGetLastError();
+}
+
 template <int MODE, int UPL>
 hipError_t launch_down(const FwdArgs& a, uint16_t* hbuf, DecTable* table, int nu, int PT, int Imax, int SP,
                        hipStream_t s) {
@@ -973,7 +1107,13 @@ hipError_t launch_mode(const FwdArgs& a, uint16_t* hbuf, DecTable* table, int ph
         // us per layer on H = 2048); several tokens: two units per lane, half the blocks,
         // each staging x once for twice the rows
         pick_split(a.H / 64, a.T > 1 ? 2 : 1, SP, upl_);
-        hipError_t err = [&]() -> hipError_t { BRX_UPL_CASES(launch_gateup, a, hbuf, table, nu, Imax, SP, s); }();
+        hipError_t err;
+        if (a.T == 1 && !a.ptok && upl_ <= 2 && a.E <= 256 && nu <= kWave) {
+            err = upl_ == 1 ? launch_gateup1<MODE, 1>(a, hbuf, table, nu, Imax, SP, s)
+                            : launch_gateup1<MODE, 2>(a, hbuf, table, nu, Imax, SP, s);
+        } else {
+            err = [&]() -> hipError_t { BRX_UPL_CASES(launch_gateup, a, hbuf, table, nu, Imax, SP, s); }();
+        }
         if (err != hipSuccess) return err;
     }
     if (phases & 2) {

@@ -18,12 +18,6 @@ namespace {
 constexpr int kRouterThreads = 256;
 constexpr int kSmallT = 64;  // up to this many tokens: one wave per (row, 4 tokens); above: token tiles
 
-__device__ __forceinline__ float wave_sum_xor(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
-    return v;
-}
-
 // ---------------------------------------------------------------- many tokens
 // k_router_tiled: a block takes a tile of TT tokens (staged in LDS as bf16) and a group of
 // rows; each row's weights are loaded once per block and used for all TT tokens, and a wave
@@ -256,7 +250,7 @@ __device__ __forceinline__ void topk_row(const float* __restrict__ l, int t, int
     int my_id;
     float my_v;
     wave_select<kPer>(v, rr, E, k, my_id, my_v);
-    const float wt = wave_weight<kPer>(v, l, rr, E, k, my_id, my_v);
+    const float wt = wave_weight<kPer>(v, rr, E, k, my_id, my_v);
     if (lane < k) {
         out_idx[(int64_t)t * k + lane] = my_id;
         out_w[(int64_t)t * k + lane] = wt;
