@@ -209,7 +209,8 @@ typedef uint32_t u32x3_t __attribute__((ext_vector_type(3)));
 //   barrier (so every wave's copies are visible and stage s - 1's slot is free);
 //   issue the loads of stage s + NS - 1 (none past the last stage); read the scales of stage
 //   s + 1 from LDS;
-//   MFMA kk of stage s  | dequantize B(s) kk + 1 (kk = 3: B(s + 1) kk 0)
+//   MFMA kk of stage s  | dequantize B(s) kk + 1 (kk = 3: B(s + 1) kk 0), read A(s) kk + 1
+//   (kk = 3: A(s + 1) kk 0) from LDS
 // The MFMA-interleaved VALU code is plain C++ so that the compiler's MFMA hazard checks cover
 // it.
 constexpr int kGemmWaves = 4;
@@ -441,8 +442,11 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
     // stage.
     constexpr int MR = MF / 2;
     // the lane's scales of stage s, read from the ring
+    // the lane's scales of one stage, as the dequantization takes them (converted once a stage):
+    // affine s 2^24 (exact) and b; MXFP4 the e8m0 scale of the stage's 32-wide group kh, which
+    // holds the lane's chunks 4 kh .. 4 kh + 3
     struct SReg {
-        uint32_t s[kNJ], b[kNJ];
+        float s[kNJ], b[kNJ];
     };
     auto fetch_s = [&](SReg& f, int s) __attribute__((always_inline)) {
         // paired scales of an odd stage: the high halves of the previous (even) stage's slots
@@ -452,23 +456,22 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
 #pragma unroll
         for (int nj = 0; nj < kNJ; ++nj) {
             const int br = brow[nj];
-            f.s[nj] = (*reinterpret_cast<const uint32_t*>(ss + SA + br * 4) >> sh) & 0xFFFFu;
-            if constexpr (kAffine<MODE>)
-                f.b[nj] = (*reinterpret_cast<const uint32_t*>(ss + SA + 1024 + br * 4) >> sh) & 0xFFFFu;
+            const uint32_t sv = (*reinterpret_cast<const uint32_t*>(ss + SA + br * 4) >> sh) & 0xFFFFu;
+            if constexpr (kAffine<MODE>) {
+                const uint32_t bv = (*reinterpret_cast<const uint32_t*>(ss + SA + 1024 + br * 4) >> sh) & 0xFFFFu;
+                f.s[nj] = (F16 ? h2f(sv) : bf2f(sv)) * 16777216.0f;
+                f.b[nj] = F16 ? h2f(bv) : bf2f(bv);
+            } else {
+                f.s[nj] = e8m0_f32((sv >> (8 * kh)) & 0xFFu);
+                f.b[nj] = 0.f;
+            }
         }
     };
     // word kk of the lane's stage half, dequantized into MFMA operands
     auto deq = [&](bf16x8_t (&bop)[kNJ], const BReg& bw, const SReg& f, int kk) __attribute__((always_inline)) {
 #pragma unroll
         for (int nj = 0; nj < kNJ; ++nj) {
-            float sv = 0.f, bv = 0.f, sc = 0.f;
-            if constexpr (kAffine<MODE>) {
-                sv = (F16 ? h2f(f.s[nj]) : bf2f(f.s[nj])) * 16777216.0f;   // s 2^24, exact
-                bv = F16 ? h2f(f.b[nj]) : bf2f(f.b[nj]);
-            } else {
-                // chunk 4 kh + kk lies in the stage's 32-wide group kh
-                sc = e8m0_f32((f.s[nj] >> (8 * kh)) & 0xFFu);
-            }
+            const float sv = f.s[nj], bv = f.b[nj], sc = f.s[nj];
             uint32_t wk = bw.w[nj][kk];
             if constexpr (MODE == kModeAffine3) {
                 // the 24-bit group kk of the lane's 12 bytes
@@ -490,17 +493,22 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-    auto mma = [&](int s, const bf16x8_t (&bop)[kNJ], int kk) __attribute__((always_inline)) {
+    // the A fragments of MFMA kk of stage s, read from the ring one K quarter ahead of their use
+    auto lda = [&](int s, int kk, bf16x8_t (&af)[MR]) __attribute__((always_inline)) {
         const uint16_t* As = reinterpret_cast<const uint16_t*>(ring + (s % NS) * SS);
 #pragma unroll
         for (int mi = 0; mi < MR; ++mi) {
             const int m = mi * 32 + l32;
             const int c = (4 * kh + kk) ^ a_key(m);
-            const bf16x8_t af = *reinterpret_cast<const bf16x8_t*>(As + m * 64 + c * 8);
+            af[mi] = *reinterpret_cast<const bf16x8_t*>(As + m * 64 + c * 8);
+        }
+    };
+    auto mma = [&](const bf16x8_t (&af)[MR], const bf16x8_t (&bop)[kNJ]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int mi = 0; mi < MR; ++mi)
 #pragma unroll
             for (int nj = 0; nj < kNJ; ++nj)
-                acc[mi][nj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, bop[nj], acc[mi][nj], 0, 0, 0);
-        }
+                acc[mi][nj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mi], bop[nj], acc[mi][nj], 0, 0, 0);
     };
 
     // prologue: stages 0 .. NS - 2 in flight; wait for stages 0 and 1; B(0) kk 0 dequantized.
@@ -511,9 +519,11 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
     for (int t = 0; t < NS - 1; ++t) issue(t, bq[t]);
     dma_wait_barrier<loads_after(NS, NV0, NV1, 0)>();
     bf16x8_t bop0[kNJ], bop1[kNJ];
+    bf16x8_t a0[MR], a1[MR];
     SReg sc, sn;
     fetch_s(sc, 0);
     deq(bop0, bq[0], sc, 0);
+    lda(0, 0, a0);
     for (int s0 = 0; s0 < nsteps; s0 += NS) {
 #pragma unroll
         for (int u = 0; u < NS; ++u) {
@@ -534,13 +544,17 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
             }
             if (s + NS - 1 < nsteps) issue(s + NS - 1, bq[(u + NS - 1) % NS]);
             fetch_s(sn, s + 1);
-            mma(s, bop0, 0);
+            lda(s, 1, a1);
+            mma(a0, bop0);
             deq(bop1, bq[u], sc, 1);
-            mma(s, bop1, 1);
+            lda(s, 2, a0);
+            mma(a1, bop1);
             deq(bop0, bq[u], sc, 2);
-            mma(s, bop0, 2);
+            lda(s, 3, a1);
+            mma(a0, bop0);
             deq(bop1, bq[u], sc, 3);
-            mma(s, bop1, 3);
+            lda(min(s + 1, nsteps - 1), 0, a0);   // stage s + 1 landed at the top of this one
+            mma(a1, bop1);
             deq(bop0, bq[(u + 1) % NS], sn, 0);
             sc = sn;
         }
