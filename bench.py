@@ -42,6 +42,9 @@ sys.path.insert(0, ROOT)
 
 METRIC = "MoE-layer tokens/s at batch 1 and 2048-token prefill; % of HBM/MFMA roofline"
 HBM_PEAK_GBS = 8000.0
+# the decode kernel the roofline line times: one token, affine 4-bit, routing ranked in-kernel
+# for E <= 128 (k_dec_gateup1<MODE, UPL, KP>)
+DECODE_GATEUP_KERNEL = "k_dec_gateup1<0, 1, 2>"
 BF16_PEAK_TFLOPS = 2500.0
 
 
@@ -715,11 +718,15 @@ def main():
         del st
         torch.cuda.empty_cache()
         report = config_report(args)
+    # HBM bytes per launch of the timed kernel, from the committed FETCH_SIZE / WRITE_SIZE
+    # profile; only counters taken on this kernel are reported
     traffic = None
     tp = os.path.join(ROOT, "profiles", "traffic_decode_gateup.json")
     if os.path.exists(tp):
         try:
-            traffic = json.load(open(tp)).get("traffic_bytes")
+            tj = json.load(open(tp))
+            if tj.get("kernel") == DECODE_GATEUP_KERNEL:
+                traffic = tj.get("traffic_bytes")
         except (OSError, ValueError):
             traffic = None
     rec = {
@@ -750,8 +757,8 @@ def main():
             "unit": "GB/s",
             "frac": _r(dec["gateup_gbs"] / HBM_PEAK_GBS if dec["gateup_gbs"] else None, 4),
             "traffic": traffic,
-            "kernel": f"k_dec_gateup, routed in-kernel ({spec.top_k} experts x gate+up, "
-                      f"{dec['gateup_bytes']:,} B per launch)",
+            "kernel": f"{DECODE_GATEUP_KERNEL}: one token's gate/up + SwiGLU, routed in-kernel "
+                      f"({spec.top_k} experts x gate+up, {dec['gateup_bytes']:,} B per launch)",
             "avg_us": _r(dec["gateup_us"], 3),
         },
         "decode_kernels": {
