@@ -41,6 +41,7 @@ constexpr int kMaxTok = 8;
 constexpr int kMaxU = 65;     // 64 routed pairs + the shared expert
 constexpr int kXU = 144;      // LDS bytes per staged activation unit: 64 bf16 + 16 pad
 constexpr int kDownLds = 96 * 1024;   // staged h budget of the down kernel
+constexpr int kEntryRows = 16;        // block rows of the one-launch several-token gate/up kernel
 
 struct DecEntry {
     int32_t slot;             // pool slot, or -1 for the shared expert
@@ -362,17 +363,17 @@ __device__ __forceinline__ void stage_store(int K, int nrows, int base, const St
 // g / (8U), unit (g / 8) % U, piece g % 8) and handed to the threads kStageB at a time, so rows
 // shorter than the block (h rows of 8-16 units) still take one round trip per kStageB * kThreads
 // pieces. The 8 pieces of a unit stay on 8 consecutive lanes.
-template <int MODE, typename RowOf>
+template <int MODE, int NB = kStageB, typename RowOf>
 __device__ __forceinline__ void stage_dense(const uint16_t* __restrict__ src, int K, int nrows, RowOf row_of,
                                             uint8_t* xs, float* sums) {
     const int U = K / 64;
     const int pcs = U * 8;
     const int total = nrows * pcs;
-    for (int base = 0; base < total; base += kStageB * kThreads) {
-        uint4 v[kStageB];
-        int gi[kStageB];
+    for (int base = 0; base < total; base += NB * kThreads) {
+        uint4 v[NB];
+        int gi[NB];
 #pragma unroll
-        for (int b = 0; b < kStageB; ++b) {
+        for (int b = 0; b < NB; ++b) {
             const int g = min(base + b * kThreads + (int)threadIdx.x, total - 1);
             gi[b] = g;
             const int r = g / pcs, pi = g - r * pcs;
@@ -380,7 +381,7 @@ __device__ __forceinline__ void stage_dense(const uint16_t* __restrict__ src, in
             v[b] = *reinterpret_cast<const uint4*>(src + off);
         }
 #pragma unroll
-        for (int b = 0; b < kStageB; ++b) {
+        for (int b = 0; b < NB; ++b) {
             if (base + b * kThreads >= total) break;   // uniform
             const bool ok = base + b * kThreads + (int)threadIdx.x < total;
             const int g = gi[b];
@@ -731,6 +732,258 @@ __global__ __launch_bounds__(kThreads) void k_dec_gateup1(FwdArgs a, uint16_t* _
     }
 }
 
+// ------------------------------------------------------------------ several tokens
+// k_dec_plan: one block ranks every token's top-k once (wave t takes token t; with the pairs
+// given, they are read instead) and plans the step: the pairs routed to one expert are merged,
+// in pair order, into entries of at most 8 pairs, numbered in order of their first pair (so an
+// expert is read once for all the step's tokens that chose it); the shared expert, when the
+// layer has one, is the last entry and takes every token. It writes the entry table and the
+// routing (indices, weights, shared-expert gate) that the gate/up and down kernels read.
+constexpr int kPlanThreads = kWave * kMaxTok;
+
+template <int KP>
+__global__ __launch_bounds__(kPlanThreads) void k_dec_plan(FwdArgs a, DecTable* __restrict__ table) {
+    __shared__ int32_t s_e[kWave], s_occ[kWave], s_tot[kWave], s_lq[kWave];
+    __shared__ int32_t s_part[kMaxTok][2][kWave];
+    __shared__ int32_t s_g2s[kPlanThreads];   // E <= 512
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int P = a.P, E = a.E, k = a.k;
+    // the routing and the slot table in one round trip (the table is stored to LDS only after
+    // the ranking, so no wait for it comes first)
+    float v[KP > 0 ? KP : 1];
+    const float* l = a.logits + (int64_t)min(wv, a.T - 1) * (E + 1);
+    if constexpr (KP > 0) {
+#pragma unroll
+        for (int i = 0; i < KP; ++i) {
+            const int e = lane + kWave * i;
+            const float x = l[min(e, E - 1)];   // clamped, branch-free
+            v[i] = e < E ? x : 0.0f;
+        }
+    }
+    float lsg = 0.0f;   // the shared-expert gate's logit
+    if constexpr (KP > 0) lsg = l[E];
+    const int g0 = a.g2s[min(tid, E - 1)];
+    if constexpr (KP > 0) {
+        if (wv < a.T) {   // wave t ranks token t
+            const RouteRule rr{a.route_bias, a.route_mode, a.n_group, a.topk_group, a.route_scale};
+            int sel_e;
+            float sel_v;
+            wave_select<KP>(v, rr, E, k, sel_e, sel_v);
+            const float w = wave_weight<KP>(v, rr, E, k, sel_e, sel_v);
+            if (lane < k) {
+                s_e[wv * k + lane] = sel_e;
+                a.route_idx[wv * k + lane] = sel_e;
+                a.route_w[wv * k + lane] = w;
+            }
+            if (lane == 0 && a.route_sg) a.route_sg[wv] = 1.0f / (1.0f + expf(-lsg));
+        }
+    } else {
+        if (tid < P) s_e[tid] = a.pexp[tid];
+    }
+    if (tid < E) s_g2s[tid] = g0;
+    __syncthreads();
+    // pair p = lane (p < P) against the pairs q of chunk c = wave: q = 8 c .. 8 c + 7. Experts
+    // are clamped (id E names the shared expert); idle pairs match nothing.
+    const int emax = a.shared ? E : E - 1;
+    auto expert = [&](int q) { return q < P ? min(max(s_e[q], 0), emax) : -1 - q; };
+    const int e = expert(lane);
+    {
+        int occ = 0, tot = 0;
+#pragma unroll
+        for (int i = 0; i < kMaxTok; ++i) {
+            const int q = wv * kMaxTok + i;
+            const bool m = expert(q) == e;
+            occ += (m && q < lane) ? 1 : 0;
+            tot += m ? 1 : 0;
+        }
+        s_part[wv][0][lane] = occ;
+        s_part[wv][1][lane] = tot;
+    }
+    __syncthreads();
+    if (wv == 0) {
+        int occ = 0, tot = 0;
+#pragma unroll
+        for (int c = 0; c < kMaxTok; ++c) {
+            occ += s_part[c][0][lane];
+            tot += s_part[c][1][lane];
+        }
+        s_occ[lane] = occ;   // pairs of the same expert before this one
+        s_tot[lane] = tot;   // all pairs of that expert
+    }
+    __syncthreads();
+    // the lane of the pair that leads this pair's entry: the (occ & ~7)-th pair of its expert
+    {
+        const int occ0 = s_occ[lane] & ~(kMaxTok - 1);
+#pragma unroll
+        for (int i = 0; i < kMaxTok; ++i) {
+            const int q = wv * kMaxTok + i;
+            if (expert(q) == e && s_occ[q] == occ0) s_lq[lane] = q;
+        }
+    }
+    __syncthreads();
+    if (wv != 0) return;
+    const int occ = s_occ[lane], occ0 = occ & ~(kMaxTok - 1), lq = s_lq[lane];
+    const uint64_t leads = __ballot(lane < P && occ == occ0);
+    const int nr = __popcll(leads);
+    if (lane < P) {
+        const int u = __popcll(leads & ((1ull << lq) - 1ull));
+        DecEntry& d = table->ent[u];
+        d.pair[occ - occ0] = lane;
+        if (occ == occ0) {
+            int sc = -1;
+            if (e < E) sc = slot_code(a, e, s_g2s[e]);
+            if (sc == kAbsentCode) note_absent(a, e);
+            d.slot = sc;
+            d.nt = min(kMaxTok, s_tot[lane] - occ0);
+        }
+    }
+    if (a.auto_shared) {
+        DecEntry& d = table->ent[nr];
+        if (lane < a.T) d.pair[lane] = P + lane;
+        if (lane == 0) {
+            d.slot = -1;
+            d.nt = a.T;
+        }
+    }
+    // rows past the planned entries are empty: the down kernel reads every row it may be given
+    const int n = nr + (a.auto_shared ? 1 : 0);
+    for (int v = n + lane; v < kMaxU; v += kWave) {
+        table->ent[v].slot = 0;
+        table->ent[v].nt = 0;
+    }
+    if (lane == 0) table->n = n;
+}
+
+// k_dec_gateupT: block b takes entry b / nrb of the plan and its rows (b % nrb) RB ..
+// (b % nrb) RB + RB - 1, for every pair of the entry; blocks past the last entry return. One
+// round trip reads the entry; the weight loads are then issued before the entry's token rows
+// of x are staged, so the two overlap.
+template <int MODE, int UPL>
+__global__ __launch_bounds__(kThreads) void k_dec_gateupT(FwdArgs a, uint16_t* __restrict__ hbuf, int hstride,
+                                                          const DecTable* __restrict__ table, int lsp, int nrb) {
+    prefetch_args(a);
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    __shared__ int32_t s_tok[kMaxTok];
+    const int SP = 1 << lsp;
+    const int lane = threadIdx.x & 63, tid = threadIdx.x;
+    const int H = a.H, U = H / 64;
+    const int u = blockIdx.x / nrb, rb = blockIdx.x - u * nrb;
+    if (u >= table->n) return;   // uniform
+    const DecEntry& en = table->ent[u];
+    const int slot = clamp_code(a, en.slot), nt = min(max(en.nt, 0), kMaxTok);
+    const int PT = a.P + (a.auto_shared ? a.T : 0);
+    const bool sh = slot == -1;
+    const int inter = sh ? a.I_sh : a.I;
+    const int RW = kWave >> lsp;
+    const int r0 = rb * kWaves * RW;
+    if (r0 >= inter) return;   // uniform
+    const Layout& L = sh ? a.lay_sh : a.lay;
+    const uint8_t* base = code_base(a, slot);
+    const int g = lane >> lsp, sl = lane & (SP - 1);
+    const int rr = (tid >> 6) * RW + g;
+    const int row = min(r0 + rr, inter - 1);
+    const bool gated = a.act != BRX_ACT_SILU_MLP;
+    Units<MODE, UPL> ug, uu;
+    units_load<MODE, UPL>(base, L.p[0], row, sl, SP, ug);
+    if (gated) units_load<MODE, UPL>(base, L.p[1], row, sl, SP, uu);
+    float bg = 0.f, bu = 0.f;
+    if (L.p[0].bias >= 0) {
+        bg = bf2f(reinterpret_cast<const uint16_t*>(base + L.p[0].bias)[row]);
+        if (gated) bu = bf2f(reinterpret_cast<const uint16_t*>(base + L.p[1].bias)[row]);
+    }
+    // the entry's token rows, staged while the weights are in flight
+    if (tid < nt) {
+        const int pair = min(max(en.pair[tid], 0), PT - 1);
+        s_tok[tid] = pair < a.P ? pair_tok(a, pair) : pair - a.P;
+    }
+    __syncthreads();
+    uint8_t* xs = lds;
+    float* xsum = reinterpret_cast<float*>(lds + (size_t)kMaxTok * U * kXU);
+    stage_dense<MODE>(a.x, H, nt, [&](int i) { return s_tok[i]; }, xs, xsum);
+    __syncthreads();
+    for (int i = 0; i < nt; ++i) {
+        const int pair = min(max(en.pair[i], 0), PT - 1);
+        float pg = 0.f, pu = 0.f;
+#pragma unroll
+        for (int j = 0; j < UPL; ++j) {
+            const int un = sl + SP * j;
+            if (un < U) {
+                const uint4* xu = reinterpret_cast<const uint4*>(xs + ((int64_t)i * U + un) * kXU);
+                const float sx = kAffine<MODE> ? xsum[i * U + un] : 0.0f;
+                pg += unit_dot<MODE, UPL>(ug, j, xu, sx, a.scale_f16);
+                if (gated) pu += unit_dot<MODE, UPL>(uu, j, xu, sx, a.scale_f16);
+            }
+        }
+        pg = group_sum(pg, SP);
+        if (gated) pu = group_sum(pu, SP);
+        if (sl == 0 && r0 + rr < inter) {
+            const float h = slot == kAbsentCode ? absent_nan() : act_apply(a.act, pg + bg, pu + bu, a.alpha, a.limit);
+            hbuf[(int64_t)pair * hstride + r0 + rr] = (uint16_t)f2bf(h);
+        }
+    }
+}
+
+// k_dec_downT: block b takes entry b / nrb and down rows (b % nrb) RB .. of it: each pair's row
+// result plus the projection's bias, rounded to bf16, into y_routed at the pair's row (the
+// shared expert's into y_shared at its token); the k-ordered combine follows in its own launch.
+// One round trip reads the entry, then the weights and the entry's h rows are requested together.
+template <int MODE, int UPL>
+__global__ __launch_bounds__(kThreads) void k_dec_downT(FwdArgs a, const uint16_t* __restrict__ hbuf, int hstride,
+                                                        const DecTable* __restrict__ table, int lsp, int nrb,
+                                                        uint16_t* __restrict__ y_routed,
+                                                        uint16_t* __restrict__ y_shared) {
+    prefetch_args(a);
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    __shared__ int32_t s_pair[kMaxTok];
+    const int SP = 1 << lsp;
+    const int lane = threadIdx.x & 63, tid = threadIdx.x;
+    const int H = a.H;
+    const int u = blockIdx.x / nrb, rb = blockIdx.x - u * nrb;
+    if (u >= table->n) return;   // uniform
+    const DecEntry& en = table->ent[u];
+    const int slot = clamp_code(a, en.slot), nt = min(max(en.nt, 0), kMaxTok);
+    const int PT = a.P + (a.auto_shared ? a.T : 0);
+    const Layout& L = slot == -1 ? a.lay_sh : a.lay;
+    const int K = L.p[2].n_in, U = K / 64;
+    const int RW = kWave >> lsp;
+    const int r0 = rb * kWaves * RW;
+    if (r0 >= H) return;   // uniform
+    const uint8_t* base = code_base(a, slot);
+    const int g = lane >> lsp, sl = lane & (SP - 1);
+    const int rr = (tid >> 6) * RW + g;
+    const int row = min(r0 + rr, H - 1);
+    Units<MODE, UPL> ud;
+    units_load<MODE, UPL>(base, L.p[2], row, sl, SP, ud);
+    const float bd = L.p[2].bias >= 0 ? bf2f(reinterpret_cast<const uint16_t*>(base + L.p[2].bias)[row]) : 0.f;
+    if (tid < nt) s_pair[tid] = min(max(en.pair[tid], 0), PT - 1);
+    __syncthreads();
+    // h rows are staged at their full width (hstride / 64 units); the entry reads its U
+    const int Us = hstride / 64;
+    uint8_t* hs = lds;
+    float* hsum = reinterpret_cast<float*>(lds + (size_t)kMaxTok * Us * kXU);
+    stage_dense<MODE>(hbuf, hstride, nt, [&](int i) { return s_pair[i]; }, hs, hsum);
+    __syncthreads();
+    for (int i = 0; i < nt; ++i) {
+        const int pair = s_pair[i];
+        float p = 0.f;
+#pragma unroll
+        for (int j = 0; j < UPL; ++j) {
+            const int un = sl + SP * j;
+            if (un < U) {
+                const uint4* hu = reinterpret_cast<const uint4*>(hs + ((int64_t)i * Us + un) * kXU);
+                const float sx = kAffine<MODE> ? hsum[i * Us + un] : 0.0f;
+                p += unit_dot<MODE, UPL>(ud, j, hu, sx, a.scale_f16);
+            }
+        }
+        p = group_sum(p, SP);
+        if (sl == 0 && r0 + rr < H) {
+            const uint16_t y = (uint16_t)f2bf(p + bd);
+            if (pair < a.P) y_routed[(int64_t)pair_row(a, pair) * H + r0 + rr] = y;
+            else if (y_shared) y_shared[(int64_t)(pair - a.P) * H + r0 + rr] = y;
+        }
+    }
+}
+
 // ------------------------------------------------------------------ down + combine
 // Each pair's row result rounded to bf16 (the projection's output, with its bias), the
 // unreduced rows when asked for, and the k-ordered combine out[t] = sum_j w[t,j] * y[t,j]
@@ -1023,7 +1276,7 @@ hipError_t launch_gateup(const FwdArgs& a, uint16_t* hbuf, DecTable* table, int 
     const int RB = kWaves * (kWave / SP);
     // entry rows: one per block row up to 16; past that (several tokens, where most of the
     // P + 1 possible entries are empty) a block takes entries y, y + 16, ...
-    dim3 grid((Imax + RB - 1) / RB, a.T > 1 && nu > 16 ? 16 : nu), block(kThreads);
+    dim3 grid((Imax + RB - 1) / RB, a.T > 1 && nu > kEntryRows ? kEntryRows : nu), block(kThreads);
     // staged x of up to T tokens
     const size_t lds = (size_t)a.T * (a.H / 64) * (kXU + 4);
     const int lsp = __builtin_ctz(SP);
@@ -1061,6 +1314,42 @@ hipError_t launch_gateup1(const FwdArgs& a, uint16_t* hbuf, DecTable* table, int
     return hipGetLastError();
 }
 
+// Several tokens: the plan (one block), then one block per (entry, RB rows) for every entry
+// the step may have (P routed pairs + the shared expert); blocks past the planned entries return.
+template <int MODE, int UPL>
+hipError_t launch_gateupT(const FwdArgs& a, uint16_t* hbuf, DecTable* table, int nu, int Imax, int SP,
+                          hipStream_t s) {
+#define BRX_PLAN(KP) hipLaunchKernelGGL((k_dec_plan<KP>), dim3(1), dim3(kPlanThreads), 0, s, a, table)
+    if (!a.logits) BRX_PLAN(0);
+    else if (a.E <= 64) BRX_PLAN(1);
+    else if (a.E <= 128) BRX_PLAN(2);
+    else if (a.E <= 256) BRX_PLAN(4);
+    else BRX_PLAN(8);
+#undef BRX_PLAN
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+    const int RB = kWaves * (kWave / SP);
+    const int nrb = (Imax + RB - 1) / RB;
+    const size_t lds = (size_t)kMaxTok * (a.H / 64) * (kXU + 4);
+    hipLaunchKernelGGL((k_dec_gateupT<MODE, UPL>), dim3(nu * nrb), dim3(kThreads), lds, s, a, hbuf, Imax, table,
+                       (int)__builtin_ctz(SP), nrb);
+    return hipGetLastError();
+}
+
+// Several tokens, down: one block per (entry, RB rows), then the k-ordered combine.
+template <int MODE, int UPL>
+hipError_t launch_downT(const FwdArgs& a, uint16_t* hbuf, DecTable* table, int nu, int Imax, int SP,
+                        uint16_t* y_routed, uint16_t* y_shared, hipStream_t s) {
+    const int RB = kWaves * (kWave / SP);
+    const int nrb = (a.H + RB - 1) / RB;
+    const size_t lds = (size_t)kMaxTok * (Imax / 64) * (kXU + 4);
+    hipLaunchKernelGGL((k_dec_downT<MODE, UPL>), dim3(nu * nrb), dim3(kThreads), lds, s, a, hbuf, Imax, table,
+                       (int)__builtin_ctz(SP), nrb, y_routed, y_shared);
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess || !a.out) return err;
+    return launch_combine(y_routed, a.auto_shared ? y_shared : nullptr, a.w, a.sgate, a.T, a.k, a.H, a.out, s);
+}
+
 template <int MODE, int UPL>
 hipError_t launch_down(const FwdArgs& a, uint16_t* hbuf, DecTable* table, int nu, int PT, int Imax, int SP,
                        hipStream_t s) {
@@ -1095,22 +1384,31 @@ hipError_t launch_down(const FwdArgs& a, uint16_t* hbuf, DecTable* table, int nu
     } while (0)
 
 template <int MODE>
-hipError_t launch_mode(const FwdArgs& a, uint16_t* hbuf, DecTable* table, int phases, hipStream_t s) {
+hipError_t launch_mode(const FwdArgs& a, uint16_t* hbuf, DecTable* table, uint16_t* y_routed,
+                       uint16_t* y_shared, int phases, hipStream_t s) {
     const int P = a.P;
     const int PT = P + (a.auto_shared ? a.T : 0);
     const int nu = P + (a.auto_shared ? 1 : 0);
     const int Imax = a.I > a.I_sh ? a.I : a.I_sh;
+    // Several tokens with more possible entries than the one-launch kernel's 16 block rows take
+    // in two passes: the plan launch, then one block per (entry, rows). With fewer, every
+    // gate/up block ranks and plans the step itself.
+    const bool per_entry = a.T > 1 && nu > 2 * kEntryRows;
     if (phases & 1) {
         int SP, upl_;
-        // one token: one unit per lane where the row allows it (twice the waves of two units
-        // per lane, each with half the dequant-dot work and far fewer registers: 11.1 -> 10.2
-        // us per layer on H = 2048); several tokens: two units per lane, half the blocks,
-        // each staging x once for twice the rows
+        // one token: one unit per lane where the row allows it (twice the waves of two units per
+        // lane, each with half the dequant-dot work and far fewer registers: 11.1 -> 10.2 us per
+        // layer on H = 2048); several tokens: two units per lane, half the blocks, each staging
+        // x once for twice the rows. The split fixes each row's summation order, so both
+        // several-token kernels take the same one: a step's rows do not depend on how many
+        // pairs share its launch (a pool's span calls against the whole step).
         pick_split(a.H / 64, a.T > 1 ? 2 : 1, SP, upl_);
         hipError_t err;
         if (a.T == 1 && !a.ptok && upl_ <= 2 && a.E <= 256 && nu <= kWave) {
             err = upl_ == 1 ? launch_gateup1<MODE, 1>(a, hbuf, table, nu, Imax, SP, s)
                             : launch_gateup1<MODE, 2>(a, hbuf, table, nu, Imax, SP, s);
+        } else if (per_entry) {
+            err = [&]() -> hipError_t { BRX_UPL_CASES(launch_gateupT, a, hbuf, table, nu, Imax, SP, s); }();
         } else {
             err = [&]() -> hipError_t { BRX_UPL_CASES(launch_gateup, a, hbuf, table, nu, Imax, SP, s); }();
         }
@@ -1118,8 +1416,18 @@ hipError_t launch_mode(const FwdArgs& a, uint16_t* hbuf, DecTable* table, int ph
     }
     if (phases & 2) {
         int SP, upl_;
+        hipError_t err;
+        // (the same split for both down kernels, as for gate/up)
         pick_split(Imax / 64, 3, SP, upl_);
-        hipError_t err = [&]() -> hipError_t { BRX_UPL_CASES(launch_down, a, hbuf, table, nu, PT, Imax, SP, s); }();
+        // several tokens whose h rows are too many for every block to stage them all: one block
+        // per (entry, rows), then the combine; otherwise every block stages every pair's h rows
+        // and combines in its epilogue
+        if (per_entry && (size_t)PT * Imax * 2 > 32 * 1024) {
+            uint16_t* yr = a.yun ? a.yun : y_routed;
+            err = [&]() -> hipError_t { BRX_UPL_CASES(launch_downT, a, hbuf, table, nu, Imax, SP, yr, y_shared, s); }();
+        } else {
+            err = [&]() -> hipError_t { BRX_UPL_CASES(launch_down, a, hbuf, table, nu, PT, Imax, SP, s); }();
+        }
         if (err != hipSuccess) return err;
     }
     return hipSuccess;
@@ -1127,20 +1435,43 @@ hipError_t launch_mode(const FwdArgs& a, uint16_t* hbuf, DecTable* table, int ph
 
 inline size_t table_bytes() { return (sizeof(DecTable) + 255) & ~(size_t)255; }
 
-}  // namespace
+// [table][h rows: PT x Imax bf16] and, for several tokens, [y rows: P x H][shared y rows: T x H]
+struct DecWs {
+    DecTable* table;
+    uint16_t* hbuf;
+    uint16_t* y_routed;
+    uint16_t* y_shared;
+    size_t bytes;
+};
 
-size_t decode_workspace_bytes(const FwdArgs& a) {
+inline DecWs dec_carve(const FwdArgs& a, void* ws) {
     const int PT = a.P + (a.auto_shared ? a.T : 0);
     const int Imax = a.I > a.I_sh ? a.I : a.I_sh;
-    return table_bytes() + (size_t)PT * Imax * 2;
+    auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
+    char* b = reinterpret_cast<char*>(ws);
+    DecWs w{};
+    size_t off = 0;
+    w.table = reinterpret_cast<DecTable*>(b + off); off += table_bytes();
+    w.hbuf = reinterpret_cast<uint16_t*>(b + off); off = al(off + (size_t)PT * Imax * 2);
+    if (a.T > 1) {
+        w.y_routed = reinterpret_cast<uint16_t*>(b + off); off = al(off + (size_t)a.P * a.H * 2);
+        w.y_shared = reinterpret_cast<uint16_t*>(b + off); off = al(off + (size_t)a.T * a.H * 2);
+    }
+    w.bytes = off;
+    return w;
 }
 
+}  // namespace
+
+size_t decode_workspace_bytes(const FwdArgs& a) { return dec_carve(a, nullptr).bytes; }
+
 hipError_t launch_decode(const FwdArgs& a, void* ws, int phases, hipStream_t s) {
-    DecTable* table = reinterpret_cast<DecTable*>(ws);
-    uint16_t* hbuf = reinterpret_cast<uint16_t*>(reinterpret_cast<char*>(ws) + table_bytes());
-    if (a.quant_mode == kModeAffine3) return launch_mode<kModeAffine3>(a, hbuf, table, phases, s);
-    return a.quant_mode == BRX_QUANT_AFFINE ? launch_mode<BRX_QUANT_AFFINE>(a, hbuf, table, phases, s)
-                                            : launch_mode<BRX_QUANT_MXFP4>(a, hbuf, table, phases, s);
+    const DecWs w = dec_carve(a, ws);
+    if (a.quant_mode == kModeAffine3)
+        return launch_mode<kModeAffine3>(a, w.hbuf, w.table, w.y_routed, w.y_shared, phases, s);
+    return a.quant_mode == BRX_QUANT_AFFINE
+        ? launch_mode<BRX_QUANT_AFFINE>(a, w.hbuf, w.table, w.y_routed, w.y_shared, phases, s)
+        : launch_mode<BRX_QUANT_MXFP4>(a, w.hbuf, w.table, w.y_routed, w.y_shared, phases, s);
 }
 
 }  // namespace brx
