@@ -740,6 +740,9 @@ __global__ __launch_bounds__(kThreads) void k_dec_gateup1(FwdArgs a, uint16_t* _
 // layer has one, is the last entry and takes every token. It writes the entry table and the
 // routing (indices, weights, shared-expert gate) that the gate/up and down kernels read.
 constexpr int kPlanThreads = kWave * kMaxTok;
+// pairs per entry the plan forms: an expert chosen by more tokens is read by more entries, so
+// the blocks of a popular expert do no more than 4 tokens' dot products each
+constexpr int kPlanTok = 4;
 
 template <int KP>
 __global__ __launch_bounds__(kPlanThreads) void k_dec_plan(FwdArgs a, DecTable* __restrict__ table) {
@@ -813,7 +816,7 @@ __global__ __launch_bounds__(kPlanThreads) void k_dec_plan(FwdArgs a, DecTable* 
     __syncthreads();
     // the lane of the pair that leads this pair's entry: the (occ & ~7)-th pair of its expert
     {
-        const int occ0 = s_occ[lane] & ~(kMaxTok - 1);
+        const int occ0 = s_occ[lane] & ~(kPlanTok - 1);
 #pragma unroll
         for (int i = 0; i < kMaxTok; ++i) {
             const int q = wv * kMaxTok + i;
@@ -822,7 +825,7 @@ __global__ __launch_bounds__(kPlanThreads) void k_dec_plan(FwdArgs a, DecTable* 
     }
     __syncthreads();
     if (wv != 0) return;
-    const int occ = s_occ[lane], occ0 = occ & ~(kMaxTok - 1), lq = s_lq[lane];
+    const int occ = s_occ[lane], occ0 = occ & ~(kPlanTok - 1), lq = s_lq[lane];
     const uint64_t leads = __ballot(lane < P && occ == occ0);
     const int nr = __popcll(leads);
     if (lane < P) {
@@ -834,7 +837,7 @@ __global__ __launch_bounds__(kPlanThreads) void k_dec_plan(FwdArgs a, DecTable* 
             if (e < E) sc = slot_code(a, e, s_g2s[e]);
             if (sc == kAbsentCode) note_absent(a, e);
             d.slot = sc;
-            d.nt = min(kMaxTok, s_tot[lane] - occ0);
+            d.nt = min(kPlanTok, s_tot[lane] - occ0);
         }
     }
     if (a.auto_shared) {
@@ -854,6 +857,26 @@ __global__ __launch_bounds__(kPlanThreads) void k_dec_plan(FwdArgs a, DecTable* 
     if (lane == 0) table->n = n;
 }
 
+// The (entry, token group, row block) of per-entry block b: blocks u * nrb + rb with u < n take
+// entry u's first kPlanTok pairs; past the n entries, the next groups of the last entry (the
+// shared expert, which takes every token). Returns the row block, or -1 for a block with no
+// work; u, t0 (its first pair's index in the entry) and nt (its pair count) are set otherwise.
+__device__ __forceinline__ int entry_group(const DecTable* table, int b, int nrb, int& u, int& t0, int& nt) {
+    const int n = table->n;
+    u = b / nrb;
+    const int rb = b - u * nrb;
+    int c = 0;
+    if (u >= n) {
+        c = u - n + 1;
+        u = n - 1;
+    }
+    if (u < 0 || u >= kMaxU) return -1;
+    const int nall = min(max(table->ent[u].nt, 0), kMaxTok);
+    t0 = c * kPlanTok;
+    nt = min(kPlanTok, nall - t0);
+    return nt > 0 ? rb : -1;
+}
+
 // k_dec_gateupT: block b takes entry b / nrb of the plan and its rows (b % nrb) RB ..
 // (b % nrb) RB + RB - 1, for every pair of the entry; blocks past the last entry return. One
 // round trip reads the entry; the weight loads are then issued before the entry's token rows
@@ -867,10 +890,11 @@ __global__ __launch_bounds__(kThreads) void k_dec_gateupT(FwdArgs a, uint16_t* _
     const int SP = 1 << lsp;
     const int lane = threadIdx.x & 63, tid = threadIdx.x;
     const int H = a.H, U = H / 64;
-    const int u = blockIdx.x / nrb, rb = blockIdx.x - u * nrb;
-    if (u >= table->n) return;   // uniform
+    int u, t0, nt;
+    const int rb = entry_group(table, blockIdx.x, nrb, u, t0, nt);
+    if (rb < 0) return;   // uniform
     const DecEntry& en = table->ent[u];
-    const int slot = clamp_code(a, en.slot), nt = min(max(en.nt, 0), kMaxTok);
+    const int slot = clamp_code(a, en.slot);
     const int PT = a.P + (a.auto_shared ? a.T : 0);
     const bool sh = slot == -1;
     const int inter = sh ? a.I_sh : a.I;
@@ -893,16 +917,16 @@ __global__ __launch_bounds__(kThreads) void k_dec_gateupT(FwdArgs a, uint16_t* _
     }
     // the entry's token rows, staged while the weights are in flight
     if (tid < nt) {
-        const int pair = min(max(en.pair[tid], 0), PT - 1);
+        const int pair = min(max(en.pair[t0 + tid], 0), PT - 1);
         s_tok[tid] = pair < a.P ? pair_tok(a, pair) : pair - a.P;
     }
     __syncthreads();
     uint8_t* xs = lds;
-    float* xsum = reinterpret_cast<float*>(lds + (size_t)kMaxTok * U * kXU);
+    float* xsum = reinterpret_cast<float*>(lds + (size_t)kPlanTok * U * kXU);
     stage_dense<MODE>(a.x, H, nt, [&](int i) { return s_tok[i]; }, xs, xsum);
     __syncthreads();
     for (int i = 0; i < nt; ++i) {
-        const int pair = min(max(en.pair[i], 0), PT - 1);
+        const int pair = min(max(en.pair[t0 + i], 0), PT - 1);
         float pg = 0.f, pu = 0.f;
 #pragma unroll
         for (int j = 0; j < UPL; ++j) {
@@ -938,10 +962,11 @@ __global__ __launch_bounds__(kThreads) void k_dec_downT(FwdArgs a, const uint16_
     const int SP = 1 << lsp;
     const int lane = threadIdx.x & 63, tid = threadIdx.x;
     const int H = a.H;
-    const int u = blockIdx.x / nrb, rb = blockIdx.x - u * nrb;
-    if (u >= table->n) return;   // uniform
+    int u, t0, nt;
+    const int rb = entry_group(table, blockIdx.x, nrb, u, t0, nt);
+    if (rb < 0) return;   // uniform
     const DecEntry& en = table->ent[u];
-    const int slot = clamp_code(a, en.slot), nt = min(max(en.nt, 0), kMaxTok);
+    const int slot = clamp_code(a, en.slot);
     const int PT = a.P + (a.auto_shared ? a.T : 0);
     const Layout& L = slot == -1 ? a.lay_sh : a.lay;
     const int K = L.p[2].n_in, U = K / 64;
@@ -955,12 +980,12 @@ __global__ __launch_bounds__(kThreads) void k_dec_downT(FwdArgs a, const uint16_
     Units<MODE, UPL> ud;
     units_load<MODE, UPL>(base, L.p[2], row, sl, SP, ud);
     const float bd = L.p[2].bias >= 0 ? bf2f(reinterpret_cast<const uint16_t*>(base + L.p[2].bias)[row]) : 0.f;
-    if (tid < nt) s_pair[tid] = min(max(en.pair[tid], 0), PT - 1);
+    if (tid < nt) s_pair[tid] = min(max(en.pair[t0 + tid], 0), PT - 1);
     __syncthreads();
     // h rows are staged at their full width (hstride / 64 units); the entry reads its U
     const int Us = hstride / 64;
     uint8_t* hs = lds;
-    float* hsum = reinterpret_cast<float*>(lds + (size_t)kMaxTok * Us * kXU);
+    float* hsum = reinterpret_cast<float*>(lds + (size_t)kPlanTok * Us * kXU);
     stage_dense<MODE>(hbuf, hstride, nt, [&](int i) { return s_pair[i]; }, hs, hsum);
     __syncthreads();
     for (int i = 0; i < nt; ++i) {
@@ -1314,6 +1339,12 @@ hipError_t launch_gateup1(const FwdArgs& a, uint16_t* hbuf, DecTable* table, int
     return hipGetLastError();
 }
 
+// Block rows of the per-entry kernels: every entry the step may have, plus the shared expert's
+// token groups past its first.
+inline int entry_groups(const FwdArgs& a, int nu) {
+    return nu + (a.auto_shared ? (a.T - 1) / kPlanTok : 0);
+}
+
 // Several tokens: the plan (one block), then one block per (entry, RB rows) for every entry
 // the step may have (P routed pairs + the shared expert); blocks past the planned entries return.
 template <int MODE, int UPL>
@@ -1330,8 +1361,8 @@ hipError_t launch_gateupT(const FwdArgs& a, uint16_t* hbuf, DecTable* table, int
     if (err != hipSuccess) return err;
     const int RB = kWaves * (kWave / SP);
     const int nrb = (Imax + RB - 1) / RB;
-    const size_t lds = (size_t)kMaxTok * (a.H / 64) * (kXU + 4);
-    hipLaunchKernelGGL((k_dec_gateupT<MODE, UPL>), dim3(nu * nrb), dim3(kThreads), lds, s, a, hbuf, Imax, table,
+    const size_t lds = (size_t)kPlanTok * (a.H / 64) * (kXU + 4);
+    hipLaunchKernelGGL((k_dec_gateupT<MODE, UPL>), dim3(entry_groups(a, nu) * nrb), dim3(kThreads), lds, s, a, hbuf, Imax, table,
                        (int)__builtin_ctz(SP), nrb);
     return hipGetLastError();
 }
@@ -1342,8 +1373,8 @@ hipError_t launch_downT(const FwdArgs& a, uint16_t* hbuf, DecTable* table, int n
                         uint16_t* y_routed, uint16_t* y_shared, hipStream_t s) {
     const int RB = kWaves * (kWave / SP);
     const int nrb = (a.H + RB - 1) / RB;
-    const size_t lds = (size_t)kMaxTok * (Imax / 64) * (kXU + 4);
-    hipLaunchKernelGGL((k_dec_downT<MODE, UPL>), dim3(nu * nrb), dim3(kThreads), lds, s, a, hbuf, Imax, table,
+    const size_t lds = (size_t)kPlanTok * (Imax / 64) * (kXU + 4);
+    hipLaunchKernelGGL((k_dec_downT<MODE, UPL>), dim3(entry_groups(a, nu) * nrb), dim3(kThreads), lds, s, a, hbuf, Imax, table,
                        (int)__builtin_ctz(SP), nrb, y_routed, y_shared);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess || !a.out) return err;
