@@ -5,17 +5,25 @@
 // three projections, the SwiGLU between them (stream.py:1164-1166) and the caller's
 // router-weighted combine (stream.py:1523-1525).
 //
-// Two kernels per layer:
-//   k_dec_gateup  grid (row block, entry row y < 16): gate and up rows of one expert for every
-//                 token routed to it (entries y, y + 16, ... of the step), act() in the
-//                 epilogue, h -> bf16 workspace; its blocks of row block 0 also record the
-//                 entry table the down kernel reads. With the layer's router logits given,
-//                 every block first ranks the top-k itself.
-//   k_dec_down    grid (row block of H): down rows of every entry, each pair's bf16 row result,
-//                 and the k-ordered combine out[t] = sum_j w[t,j] * y[t,j].
-// An entry is a run of at most 8 pairs routed to one expert (so an expert is read once for all
-// the step's tokens that chose it), in order of first appearance; the shared expert, when the
-// layer has one, is the last entry and takes every token.
+// Gate/up, then down:
+//   k_dec_gateup1  one token: one (entry, row) item per row group; every block ranks the
+//                  token's top-k itself and block 0 records the entry table.
+//   k_dec_gateup   several tokens with at most 32 possible entries (or one token the above
+//                  does not take): grid (row block, entry row y < 16), gate and up rows of one
+//                  expert for every token routed to it (entries y, y + 16, ...), act() in the
+//                  epilogue, h -> bf16 workspace; its blocks of row block 0 record the entry
+//                  table. With the layer's router logits given, every block ranks the top-k.
+//   k_dec_plan + k_dec_gateupT  several tokens with more possible entries: one block ranks and
+//                  plans the step once, then one block per (entry, row block).
+//   k_dec_down_fit / k_dec_down  grid (row block of H): down rows of every entry, each pair's
+//                  bf16 row result, and the k-ordered combine out[t] = sum_j w[t,j] * y[t,j].
+//   k_dec_downT + k_combine  after the plan, when every block cannot stage every pair's h row:
+//                  one block per (entry, row block), then the combine.
+// An entry is a run of pairs routed to one expert (at most 8; at most 4 from the plan), so an
+// expert is read once for all the step's tokens that chose it, numbered in order of first
+// appearance; the shared expert, when the layer has one, is the last entry and takes every
+// token. A row's value depends only on the row split (SP, UPL), which the launch fixes from the
+// layer's widths and whether the step has one token or several.
 //
 // A weight row of K inputs is U = K/64 units of 32 bytes (64 nibbles: one affine group with
 // one scale and one bias, or two MXFP4 groups whose two e8m0 scales are one 16-bit load; 24
