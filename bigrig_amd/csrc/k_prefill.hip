@@ -6,8 +6,9 @@
 // restores (token, k) order (stream.py:1558-1561, _scatter_unsort 1829-1831), followed by the
 // caller's router-weighted combine (stream.py:1523-1525).
 //
-//   k_bucket   one block per expert: histogram of all pairs, the expert's run offset, the
-//              stable (pair-order) compaction of its pairs, and one tile descriptor {expert,
+//   k_bucket   one block per expert: in one pass over the pairs, the histogram of all of them
+//              and the stable (pair-order) compaction of the expert's pairs into LDS; then the
+//              expert's run offset, the run copied out in order, and one tile descriptor {expert,
 //              first bucketed row, rows, slot} per 128-row M tile, placed in a tile list that
 //              holds every tile of more than 64 rows before the smaller ones, so the GEMM grids
 //              dispatch the long tiles first and the short ones fill the end.
@@ -50,6 +51,7 @@ constexpr int kBucketThreads = 1024;
 constexpr int kBucketPer = 16;                                 // pairs per lane per pass
 constexpr int kBucketWaveRun = kWave * kBucketPer;            // pairs per wave per pass
 constexpr int kBucketPass = kBucketThreads * kBucketPer;
+constexpr int kBucketListMax = 8192;                          // pairs an LDS list may hold
 
 __device__ __forceinline__ int bucket_expert(const int32_t* __restrict__ pexp, int p, int P, int E, int emax) {
     return p < P ? min(max(pexp[p], 0), emax) : E;
@@ -62,9 +64,11 @@ __global__ __launch_bounds__(kBucketThreads) void k_bucket(const int32_t* __rest
                                                            int32_t* __restrict__ order,
                                                            int32_t* __restrict__ offsets,
                                                            int32_t* __restrict__ tile_start,
-                                                           int4* __restrict__ tinfo) {
-    // E_ext = E + 1 when a shared expert exists (id E); T_sh shared pairs follow the P routed
-    extern __shared__ int32_t hist[];     // [E_ext]
+                                                           int4* __restrict__ tinfo, int lcap) {
+    // E_ext = E + 1 when a shared expert exists (id E); T_sh shared pairs follow the P routed.
+    // LDS: the histogram [E_ext], then a list of up to lcap of this expert's pairs.
+    extern __shared__ int32_t hist[];
+    int32_t* list = hist + E_ext;
     constexpr int kNw = kBucketThreads / kWave;
     __shared__ int32_t wsum[kNw];
     __shared__ int32_t base_s[3];
@@ -72,9 +76,13 @@ __global__ __launch_bounds__(kBucketThreads) void k_bucket(const int32_t* __rest
     const int emax = E_ext - 1;
     const int e = blockIdx.x;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const uint64_t below = (1ull << lane) - 1ull;
     for (int i = tid; i < E_ext; i += kBucketThreads) hist[i] = 0;
     __syncthreads();
-    // histogram of every pair's expert (each block needs all counts below its own expert)
+    // one pass over the pairs: the histogram of every pair's expert (each block needs all counts
+    // below its own expert) and the stable (pair-order) compaction of this expert's pairs into
+    // the LDS list, pair order = (pass, wave, i, lane)
+    int run = 0;
     for (int p0 = 0; p0 < P_ext; p0 += kBucketPass) {
         const int pb = p0 + wv * kBucketWaveRun + lane;
         int ex[kBucketPer];
@@ -83,6 +91,33 @@ __global__ __launch_bounds__(kBucketThreads) void k_bucket(const int32_t* __rest
 #pragma unroll
         for (int i = 0; i < kBucketPer; ++i)
             if (pb + i * kWave < P_ext) atomicAdd(&hist[ex[i]], 1);
+        {
+            uint64_t m[kBucketPer];
+            int cnt = 0;
+#pragma unroll
+            for (int i = 0; i < kBucketPer; ++i) {
+                m[i] = __ballot(pb + i * kWave < P_ext && ex[i] == e);
+                cnt += __popcll(m[i]);
+            }
+            if (lane == 0) wsum[wv] = cnt;
+            __syncthreads();
+            int before = 0, total = 0;
+#pragma unroll
+            for (int w = 0; w < kNw; ++w) {
+                const int v = wsum[w];
+                before += w < wv ? v : 0;
+                total += v;
+            }
+            int dst = run + before;
+#pragma unroll
+            for (int i = 0; i < kBucketPer; ++i) {
+                const int q = dst + __popcll(m[i] & below);
+                if (((m[i] >> lane) & 1ull) && q < lcap) list[q] = pb + i * kWave;
+                dst += __popcll(m[i]);
+            }
+            run += total;
+            __syncthreads();
+        }
     }
     __syncthreads();
     if (wv == 0) {
@@ -118,8 +153,9 @@ __global__ __launch_bounds__(kBucketThreads) void k_bucket(const int32_t* __rest
         }
     }
     __syncthreads();
+    const int n = hist[e], off = base_s[0];
     if (tinfo) {
-        const int n = hist[e], off = base_s[0], big = base_s[1], small = base_s[2];
+        const int big = base_s[1], small = base_s[2];
         int slot = 0;
         if (e < E && g2s) {   // the slot code: a slot, -2 - e for an expert read from host backing
             const int v = g2s[e];
@@ -134,9 +170,13 @@ __global__ __launch_bounds__(kBucketThreads) void k_bucket(const int32_t* __rest
             tinfo[rows > BM / 2 ? big + j : small] = make_int4(e, off + j * BM, rows, slot);
         }
     }
-    // stable compaction of expert e's pairs, pair order = (pass, wave, i, lane)
-    const uint64_t below = (1ull << lane) - 1ull;
-    int run = base_s[0];
+    if (n <= lcap) {
+        // the run, copied out in order (coalesced)
+        for (int i = tid; i < n; i += kBucketThreads) order[off + i] = list[i];
+        return;
+    }
+    // the expert's pairs did not fit the LDS list: a second pass compacts straight into the run
+    run = off;
     for (int p0 = 0; p0 < P_ext; p0 += kBucketPass) {
         const int pb = p0 + wv * kBucketWaveRun + lane;
         uint64_t m[kBucketPer];
@@ -787,8 +827,12 @@ hipError_t launch_gemm(const FwdArgs& a, const PfWs& w, int E_ext, int Imax, uin
 hipError_t launch_bucket(const int32_t* pexp, int P, int E, int E_ext, int T_sh, int BM,
                          const int32_t* g2s, int capacity, int host, int32_t* err, int32_t* order,
                          int32_t* offsets, int32_t* tile_start, int4* tinfo, hipStream_t s) {
-    hipLaunchKernelGGL(k_bucket, dim3(E_ext), dim3(kBucketThreads), sizeof(int32_t) * E_ext, s, pexp, P, E,
-                       E_ext, T_sh, BM, g2s, capacity, host, err, order, offsets, tile_start, tinfo);
+    // each block lists its expert's pairs in LDS during the histogram pass, up to lcap of them;
+    // an expert with more takes a second pass over the pairs
+    const int P_ext = P + T_sh;
+    const int lcap = P_ext < kBucketListMax ? P_ext : kBucketListMax;
+    hipLaunchKernelGGL(k_bucket, dim3(E_ext), dim3(kBucketThreads), sizeof(int32_t) * (E_ext + lcap), s, pexp, P,
+                       E, E_ext, T_sh, BM, g2s, capacity, host, err, order, offsets, tile_start, tinfo, lcap);
     return hipGetLastError();
 }
 
