@@ -191,11 +191,19 @@ def test_unreduced_rows(gpu, T):
     pool.close()
 
 
-def test_sort_pairs_matches_stable_argsort(gpu):
+@pytest.mark.parametrize("case", ["uniform", "crowded"])
+def test_sort_pairs_matches_stable_argsort(gpu, case):
+    """uniform: 333 tokens over 32 experts; crowded: 2600 tokens where expert 5 takes 10,400
+    pairs, more than a block lists in LDS, so its block compacts in a second pass."""
     import torch
     spec = SMALL_AFFINE
     rng = np.random.default_rng(4)
-    idx = rng.integers(0, spec.n_experts, size=(333, spec.top_k)).astype(np.int32)
+    if case == "uniform":
+        idx = rng.integers(0, spec.n_experts, size=(333, spec.top_k)).astype(np.int32)
+    else:
+        idx = rng.integers(0, spec.n_experts, size=(2600, spec.top_k)).astype(np.int32)
+        idx[:, : spec.top_k // 2] = 5
+        assert (idx == 5).sum() > 8192
     order, offsets = ops.sort_pairs(spec, torch.from_numpy(idx).to(gpu))
     o_ref, off_ref = oracle.sort_pairs(idx, spec.n_experts)
     assert np.array_equal(order.cpu().numpy(), o_ref)
