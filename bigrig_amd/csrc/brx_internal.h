@@ -285,16 +285,19 @@ __device__ __forceinline__ float wave_sum(float v) {
 // Top-k of E <= 64 * kPer logits held by one wave (lane l holds expert l + 64 i in v[i]):
 // descending by value, ties to the lower expert id -- the order the oracle's selection loop
 // defines. k rounds of (wave max, lowest id holding it); after the call lane r < k holds rank
-// r's expert and logit.
+// r's expert and logit. With kr < k only the first kr ranks are found (the others hold -1): a
+// prefix of the same order, for a caller that needs only those.
 template <int kPer>
-__device__ __forceinline__ void wave_topk(const float v[kPer], int E, int k, int& sel_e, float& sel_v) {
+__device__ __forceinline__ void wave_topk(const float v[kPer], int E, int k, int& sel_e, float& sel_v,
+                                          int kr = -1) {
     const int lane = threadIdx.x & (kWave - 1);
     bool live[kPer];
 #pragma unroll
     for (int i = 0; i < kPer; ++i) live[i] = lane + kWave * i < E;
     sel_e = -1;
     sel_v = 0.0f;
-    for (int r = 0; r < k; ++r) {
+    const int rounds = kr < 0 ? k : min(kr, k);
+    for (int r = 0; r < rounds; ++r) {
         float lm = -__builtin_inff();
 #pragma unroll
         for (int i = 0; i < kPer; ++i) lm = live[i] ? fmaxf(lm, v[i]) : lm;
@@ -440,14 +443,14 @@ __device__ __forceinline__ float wave_route_weight(const float v[kPer], int E, i
 // modes without groups rank the logits directly.
 template <int kPer>
 __device__ __forceinline__ void wave_select(const float v[kPer], const RouteRule& rr, int E, int k,
-                                            int& sel_e, float& sel_v) {
+                                            int& sel_e, float& sel_v, int kr = -1) {
     if (!route_sigmoid(rr.mode) && rr.n_group <= 1) {
-        wave_topk<kPer>(v, E, k, sel_e, sel_v);
+        wave_topk<kPer>(v, E, k, sel_e, sel_v, kr);
         return;
     }
     float c[kPer];
     route_values<kPer>(v, rr, E, c);
-    wave_topk<kPer>(c, E, k, sel_e, sel_v);
+    wave_topk<kPer>(c, E, k, sel_e, sel_v, kr);
 }
 
 // The routing weight of the rank this lane holds (lanes >= k: 0), after wave_select. Softmax

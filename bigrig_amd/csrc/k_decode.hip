@@ -660,12 +660,19 @@ __global__ __launch_bounds__(kThreads) void k_dec_gateup1(FwdArgs a, uint16_t* _
     stage_issue(a.x, H, 1, tok_row, 0, st);
     stage_store<MODE>(H, 1, 0, st, xs, xsum);
     stage_rows<MODE>(a.x, H, 1, tok_row, xs, xsum, kStageB);
+    // the entries this block's items fall in: only their ranks are needed here (block 0 ranks
+    // all k, to publish the routing and the table), so blocks of the first entries start their
+    // weight loads after fewer rounds
+    const int RGn = kWaves * (kWave >> lsp);          // row groups per block
+    const int u_first = blockIdx.x * RGn / Imax;
+    const int u_last = min(blockIdx.x * RGn + RGn - 1, nu * Imax - 1) / Imax;
+    const int kr = blockIdx.x == 0 ? a.k : (u_first >= P ? 0 : min(u_last, P - 1) + 1);
     if (wv == 0) {
         int e = pe;
         if constexpr (KP > 0) {
             const RouteRule rr{a.route_bias, a.route_mode, a.n_group, a.topk_group, a.route_scale};
             float sel_v;
-            wave_select<KP>(rg.v[0], rr, E, a.k, e, sel_v);
+            wave_select<KP>(rg.v[0], rr, E, a.k, e, sel_v, kr);
             if (blockIdx.x == 0) {
                 const float w = wave_weight<KP>(rg.v[0], rr, E, a.k, e, sel_v);
                 if (lane < a.k) {
@@ -686,8 +693,12 @@ __global__ __launch_bounds__(kThreads) void k_dec_gateup1(FwdArgs a, uint16_t* _
         }
         int slot = -1;
         if (lane < P) {
-            slot = slot_code(a, ec, v);
-            if (slot == kAbsentCode) note_absent(a, ec);
+            if (KP > 0 && lane >= kr) {
+                slot = 0;   // an entry this block does not compute
+            } else {
+                slot = slot_code(a, ec, v);
+                if (slot == kAbsentCode) note_absent(a, ec);
+            }
         }
         if (lane < nu) s_slot[lane] = slot;
         if (blockIdx.x == 0 && lane < nu) {
@@ -700,7 +711,6 @@ __global__ __launch_bounds__(kThreads) void k_dec_gateup1(FwdArgs a, uint16_t* _
     }
     __syncthreads();
 
-    const int RGn = kWaves * (kWave >> lsp);          // row groups per block
     const int g = lane >> lsp, sl = lane & (SP - 1);
     const int q = blockIdx.x * RGn + wv * (kWave >> lsp) + g;
     const int u = min(q / Imax, nu - 1), r = q - (q / Imax) * Imax;
