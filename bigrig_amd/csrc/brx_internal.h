@@ -282,45 +282,74 @@ __device__ __forceinline__ float wave_sum(float v) {
     return (readlane_f(v, 0) + readlane_f(v, 16)) + (readlane_f(v, 32) + readlane_f(v, 48));
 }
 
+// Unsigned max over the 64 lanes of a wave, returned to every lane (wave_max's DPP pattern; 0 is
+// the identity, so lanes a step leaves without a source read 0).
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL, int ROWS>
+__device__ __forceinline__ uint32_t bcast_u(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, CTRL, ROWS, 0xF, false);
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    v = max(v, dpp_u<0xB1>(v));
+    v = max(v, dpp_u<0x4E>(v));
+    v = max(v, dpp_u<0x141>(v));
+    v = max(v, dpp_u<0x140>(v));
+    v = max(v, bcast_u<0x142, 0xA>(v));
+    v = max(v, bcast_u<0x143, 0xC>(v));
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
+// The ranking key of a value: unsigned order of keys is the order of the values, +0 and -0
+// share a key (they compare equal), every NaN keys 1 (below every number) and 0 is left for
+// entries taken or absent.
+__device__ __forceinline__ uint32_t rank_key(float f) {
+    const uint32_t b = __builtin_bit_cast(uint32_t, f + 0.0f);   // -0 + 0 = +0
+    const uint32_t k = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return f != f ? 1u : k;
+}
+__device__ __forceinline__ float rank_value(uint32_t k) {
+    return __builtin_bit_cast(float, (k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
+}
+
 // Top-k of E <= 64 * kPer logits held by one wave (lane l holds expert l + 64 i in v[i]):
 // descending by value, ties to the lower expert id -- the order the oracle's selection loop
-// defines. k rounds of (wave max, lowest id holding it); after the call lane r < k holds rank
-// r's expert and logit. With kr < k only the first kr ranks are found (the others hold -1): a
-// prefix of the same order, for a caller that needs only those.
+// defines -- and NaN after every number (lowest id first; its value reads as -inf). Each round
+// takes the wave max of the values' keys and the lowest id holding it; after the call lane
+// r < k holds rank r's expert and value (fewer than k entries: the ranks past them hold -1 and
+// 0). With kr < k only the first kr ranks are found (the others hold -1): a prefix of the same
+// order, for a caller that needs only those.
 template <int kPer>
 __device__ __forceinline__ void wave_topk(const float v[kPer], int E, int k, int& sel_e, float& sel_v,
                                           int kr = -1) {
     const int lane = threadIdx.x & (kWave - 1);
-    bool live[kPer];
+    uint32_t key[kPer];
 #pragma unroll
-    for (int i = 0; i < kPer; ++i) live[i] = lane + kWave * i < E;
+    for (int i = 0; i < kPer; ++i) key[i] = lane + kWave * i < E ? rank_key(v[i]) : 0u;
     sel_e = -1;
     sel_v = 0.0f;
     const int rounds = kr < 0 ? k : min(kr, k);
     for (int r = 0; r < rounds; ++r) {
-        float lm = -__builtin_inff();
+        uint32_t lm = key[0];
 #pragma unroll
-        for (int i = 0; i < kPer; ++i) lm = live[i] ? fmaxf(lm, v[i]) : lm;
-        const float mx = wave_max(lm);
+        for (int i = 1; i < kPer; ++i) lm = max(lm, key[i]);
+        const uint32_t mx = wave_max_u32(lm);
         int pick = -1;
+        if (mx != 0u) {
 #pragma unroll
-        for (int i = 0; i < kPer; ++i) {
-            const uint64_t b = __ballot(live[i] && v[i] == mx);
-            if (pick < 0 && b) pick = kWave * i + __builtin_ctzll(b);
-        }
-        if (pick < 0) {   // only NaN left: the lowest live id, as a strict > comparison would
-#pragma unroll
-            for (int i = 0; i < kPer; ++i) {
-                const uint64_t b = __ballot(live[i]);
-                if (pick < 0 && b) pick = kWave * i + __builtin_ctzll(b);
+            for (int i = kPer - 1; i >= 0; --i) {
+                const uint64_t b = __ballot(key[i] == mx);
+                if (b) pick = kWave * i + __builtin_ctzll(b);
             }
         }
 #pragma unroll
         for (int i = 0; i < kPer; ++i)
-            if (lane + kWave * i == pick) live[i] = false;
+            if (lane + kWave * i == pick) key[i] = 0u;
         if (lane == r) {
             sel_e = pick;
-            sel_v = pick >= 0 ? mx : 0.0f;
+            sel_v = pick < 0 ? 0.0f : (mx == 1u ? -__builtin_inff() : rank_value(mx));
         }
     }
 }
