@@ -265,11 +265,29 @@ __device__ __forceinline__ float wave_max(float v) {
     return readlane_f(v, 63);
 }
 
-// Sum over the 64 lanes of a wave by an xor butterfly (offsets 32, 16, ..., 1): the router
-// logits' reduction order.
+// Sum over the 64 lanes of a wave by an xor butterfly (offsets 32, 16, ..., 1; every lane adds
+// its partner's value), the router logits' reduction order, returned to every lane. No step goes
+// through LDS: offsets 32 and 16 are the gfx950 lane swaps (v_permlane32_swap, v_permlane16_swap:
+// the half or row that holds the partner is picked per lane), offset 8 is row_ror:8 (lane i + 8
+// mod 16 is i ^ 8), and offset 4 is row_ror:4 -- lane i + 4 mod 16 is i ^ 4 or i ^ 4 ^ 8, and
+// after the offset-8 step lanes i and i ^ 8 hold the same value; offsets 2 and 1 are quad
+// permutes.
 __device__ __forceinline__ float wave_sum_xor(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+    const int lane = threadIdx.x & (kWave - 1);
+    {
+        const auto p = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, v),
+                                                        __builtin_bit_cast(uint32_t, v), false, false);
+        v += __builtin_bit_cast(float, lane < 32 ? p[1] : p[0]);
+    }
+    {
+        const auto p = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, v),
+                                                        __builtin_bit_cast(uint32_t, v), false, false);
+        v += __builtin_bit_cast(float, (lane & 16) ? p[0] : p[1]);
+    }
+    v += dpp_f<0x128>(v);   // row_ror:8
+    v += dpp_f<0x124>(v);   // row_ror:4
+    v += dpp_f<0x4E>(v);    // quad_perm [2,3,0,1]
+    v += dpp_f<0xB1>(v);    // quad_perm [1,0,3,2]
     return v;
 }
 

@@ -229,8 +229,9 @@ __global__ __launch_bounds__(WPB * kWave) void k_router_logits(
     }
 #pragma unroll
     for (int t = 0; t < TT; ++t) {
+        if (t >= nt) break;   // uniform
         float s = wave_sum_xor(acc[t]);
-        if (lane == 0 && t < nt) logits[(int64_t)(t0 + t) * (E + 1) + r] = (r < E && bias) ? s + bias[r] : s;
+        if (lane == 0) logits[(int64_t)(t0 + t) * (E + 1) + r] = (r < E && bias) ? s + bias[r] : s;
     }
 }
 
