@@ -265,25 +265,45 @@ __device__ __forceinline__ float wave_max(float v) {
     return readlane_f(v, 63);
 }
 
+// The value of lane i ^ 16 and of lane i ^ 32, through the gfx950 lane swaps (v_permlane16_swap,
+// v_permlane32_swap: the half or row that holds the partner is picked per lane), not LDS.
+__device__ __forceinline__ uint32_t lane_xor16(uint32_t v) {
+    const auto p = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return (threadIdx.x & 16) ? p[0] : p[1];
+}
+__device__ __forceinline__ uint32_t lane_xor32(uint32_t v) {
+    const auto p = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return (threadIdx.x & 32) ? p[0] : p[1];
+}
+__device__ __forceinline__ float lane_xor16_f(float v) {
+    return __builtin_bit_cast(float, lane_xor16(__builtin_bit_cast(uint32_t, v)));
+}
+__device__ __forceinline__ float lane_xor32_f(float v) {
+    return __builtin_bit_cast(float, lane_xor32(__builtin_bit_cast(uint32_t, v)));
+}
+
+// Inclusive prefix sum of an integer over the 64 lanes: row_shr 1, 2, 4, 8 within each row of 16
+// (lanes shifted in from outside the row read 0), then row_bcast:15 adds row 0's total to row 1
+// and row 2's to row 3, and row_bcast:31 adds rows 0-1's total to rows 2 and 3.
+__device__ __forceinline__ int wave_incl_scan(int v) {
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);
+    return v;
+}
+
 // Sum over the 64 lanes of a wave by an xor butterfly (offsets 32, 16, ..., 1; every lane adds
 // its partner's value), the router logits' reduction order, returned to every lane. No step goes
-// through LDS: offsets 32 and 16 are the gfx950 lane swaps (v_permlane32_swap, v_permlane16_swap:
-// the half or row that holds the partner is picked per lane), offset 8 is row_ror:8 (lane i + 8
+// through LDS: offsets 32 and 16 are the lane swaps above, offset 8 is row_ror:8 (lane i + 8
 // mod 16 is i ^ 8), and offset 4 is row_ror:4 -- lane i + 4 mod 16 is i ^ 4 or i ^ 4 ^ 8, and
 // after the offset-8 step lanes i and i ^ 8 hold the same value; offsets 2 and 1 are quad
 // permutes.
 __device__ __forceinline__ float wave_sum_xor(float v) {
-    const int lane = threadIdx.x & (kWave - 1);
-    {
-        const auto p = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, v),
-                                                        __builtin_bit_cast(uint32_t, v), false, false);
-        v += __builtin_bit_cast(float, lane < 32 ? p[1] : p[0]);
-    }
-    {
-        const auto p = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, v),
-                                                        __builtin_bit_cast(uint32_t, v), false, false);
-        v += __builtin_bit_cast(float, (lane & 16) ? p[0] : p[1]);
-    }
+    v += lane_xor32_f(v);
+    v += lane_xor16_f(v);
     v += dpp_f<0x128>(v);   // row_ror:8
     v += dpp_f<0x124>(v);   // row_ror:4
     v += dpp_f<0x4E>(v);    // quad_perm [2,3,0,1]

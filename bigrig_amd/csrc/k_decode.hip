@@ -298,9 +298,22 @@ __device__ __forceinline__ float group_sum(float v, int SP) {
     if (SP >= 4) v += dpp_f<0x4E>(v);
     if (SP >= 8) v += dpp_f<0x141>(v);
     if (SP >= 16) v += dpp_f<0x140>(v);
-    if (SP >= 32) v += __shfl_xor(v, 16, kWave);
-    if (SP >= 64) v += __shfl_xor(v, 32, kWave);
+    if (SP >= 32) v += lane_xor16_f(v);
+    if (SP >= 64) v += lane_xor32_f(v);
     return v;
+}
+
+// Max of a non-negative integer over the SP consecutive lanes of a row group, the same steps as
+// group_sum.
+__device__ __forceinline__ int group_max(int v, int SP) {
+    uint32_t u = (uint32_t)v;
+    if (SP >= 2) u = max(u, dpp_u<0xB1>(u));
+    if (SP >= 4) u = max(u, dpp_u<0x4E>(u));
+    if (SP >= 8) u = max(u, dpp_u<0x141>(u));
+    if (SP >= 16) u = max(u, dpp_u<0x140>(u));
+    if (SP >= 32) u = max(u, lane_xor16(u));
+    if (SP >= 64) u = max(u, lane_xor32(u));
+    return (int)u;
 }
 
 // ------------------------------------------------------------------ activation staging
@@ -1134,12 +1147,8 @@ __global__ __launch_bounds__(kThreads) void k_dec_down(FwdArgs a, const uint16_t
         const bool has64 = n > kWave;
         nt64 = has64 ? nt64 : 0;
         sl64 = has64 ? sl64 : 0;
-        int inc = nt0;
-        for (int off = 1; off < kWave; off <<= 1) {
-            const int v = __shfl_up(inc, off, kWave);
-            if (lane >= off) inc += v;
-        }
-        const int tot0 = __shfl(inc, kWave - 1, kWave);
+        const int inc = wave_incl_scan(nt0);
+        const int tot0 = __builtin_amdgcn_readlane(inc, kWave - 1);
         s_first[tid] = inc - nt0;
         s_nt[tid] = nt0;
         s_slot[tid] = sl0;
@@ -1201,7 +1210,7 @@ __global__ __launch_bounds__(kThreads) void k_dec_down(FwdArgs a, const uint16_t
             // the SP lanes of one item share nt; lanes past the items have nt = 0 and only take
             // part in the shuffles
             int ntg = nt;
-            for (int off = SP >> 1; off >= 1; off >>= 1) ntg = max(ntg, __shfl_xor(ntg, off, kWave));
+            ntg = group_max(ntg, SP);
             for (int i = 0; i < ntg; ++i) {
                 float p = 0.0f;
 #pragma unroll
@@ -1276,7 +1285,7 @@ __global__ __launch_bounds__(kThreads) void k_dec_down_fit(FwdArgs a, const uint
         // the SP lanes of one item share nt; lanes past the items have nt = 0 and only take
         // part in the sums
         int ntg = nt;
-        for (int off = SP >> 1; off >= 1; off >>= 1) ntg = max(ntg, __shfl_xor(ntg, off, kWave));
+        ntg = group_max(ntg, SP);
 #pragma unroll
         for (int i = 0; i < kMaxTok; ++i) {
             if (i >= ntg) break;
