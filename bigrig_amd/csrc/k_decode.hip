@@ -666,8 +666,11 @@ __global__ __launch_bounds__(kThreads) void k_dec_gateup1(FwdArgs a, uint16_t* _
     int pe = 0;
     if constexpr (KP == 0) pe = a.pexp[min(lane, P - 1)];
     RouteRegs<(KP > 0 ? KP : 1)> rg;
-    if constexpr (KP > 0)
+    float lsg = 0.0f;   // the shared-expert gate's logit (block 0 publishes its sigmoid)
+    if constexpr (KP > 0) {
         if (wv == 0) route_load<KP>(a, rg);
+        if (wv == 0 && blockIdx.x == 0 && a.route_sg) lsg = a.logits[E];
+    }
     StageRegs st;
     auto tok_row = [](int i) { return i; };
     stage_issue(a.x, H, 1, tok_row, 0, st);
@@ -680,20 +683,18 @@ __global__ __launch_bounds__(kThreads) void k_dec_gateup1(FwdArgs a, uint16_t* _
     const int u_first = blockIdx.x * RGn / Imax;
     const int u_last = min(blockIdx.x * RGn + RGn - 1, nu * Imax - 1) / Imax;
     const int kr = blockIdx.x == 0 ? a.k : (u_first >= P ? 0 : min(u_last, P - 1) + 1);
+    // block 0 publishes the routing and the entry table after the barrier (stores issued before
+    // it would be waited for there: they count in the same in-order counter as the loads)
+    int e = pe, eslot = -1;   // wave 0: rank lane's expert and its slot
+    float w = 0.0f, sg = 0.0f;
     if (wv == 0) {
-        int e = pe;
         if constexpr (KP > 0) {
             const RouteRule rr{a.route_bias, a.route_mode, a.n_group, a.topk_group, a.route_scale};
             float sel_v;
             wave_select<KP>(rg.v[0], rr, E, a.k, e, sel_v, kr);
             if (blockIdx.x == 0) {
-                const float w = wave_weight<KP>(rg.v[0], rr, E, a.k, e, sel_v);
-                if (lane < a.k) {
-                    a.route_idx[lane] = e;
-                    a.route_w[lane] = w;
-                }
-                if (lane == 0 && a.route_sg)
-                    a.route_sg[0] = 1.0f / (1.0f + expf(-a.logits[E]));
+                w = wave_weight<KP>(rg.v[0], rr, E, a.k, e, sel_v);
+                if (a.route_sg) sg = 1.0f / (1.0f + expf(-lsg));
             }
         }
         // entry lane < P: expert e's slot, fetched from the lane holding its table entry
@@ -704,25 +705,33 @@ __global__ __launch_bounds__(kThreads) void k_dec_gateup1(FwdArgs a, uint16_t* _
             const int t = __shfl(g2s[i], ec & (kWave - 1), kWave);
             if (i == (ec >> 6)) v = t;
         }
-        int slot = -1;
         if (lane < P) {
             if (KP > 0 && lane >= kr) {
-                slot = 0;   // an entry this block does not compute
+                eslot = 0;   // an entry this block does not compute
             } else {
-                slot = slot_code(a, ec, v);
-                if (slot == kAbsentCode) note_absent(a, ec);
+                eslot = slot_code(a, ec, v);
+                if (eslot == kAbsentCode) note_absent(a, ec);
             }
         }
-        if (lane < nu) s_slot[lane] = slot;
-        if (blockIdx.x == 0 && lane < nu) {
+        if (lane < nu) s_slot[lane] = eslot;
+    }
+    __syncthreads();
+    if (wv == 0 && blockIdx.x == 0) {
+        if constexpr (KP > 0) {
+            if (lane < a.k) {
+                a.route_idx[lane] = e;
+                a.route_w[lane] = w;
+            }
+            if (lane == 0 && a.route_sg) a.route_sg[0] = sg;
+        }
+        if (lane < nu) {
             DecEntry& d = table->ent[lane];
-            d.slot = slot;
+            d.slot = eslot;
             d.nt = 1;
             d.pair[0] = lane;
         }
-        if (blockIdx.x == 0 && lane == 0) table->n = nu;
+        if (lane == 0) table->n = nu;
     }
-    __syncthreads();
 
     const int g = lane >> lsp, sl = lane & (SP - 1);
     const int q = blockIdx.x * RGn + wv * (kWave >> lsp) + g;
@@ -777,7 +786,8 @@ constexpr int kPlanTok = 4;
 
 template <int KP>
 __global__ __launch_bounds__(kPlanThreads) void k_dec_plan(FwdArgs a, DecTable* __restrict__ table) {
-    __shared__ int32_t s_e[kWave], s_occ[kWave], s_tot[kWave], s_lq[kWave];
+    __shared__ __attribute__((aligned(16))) int32_t s_e[kWave], s_occ[kWave];
+    __shared__ int32_t s_tot[kWave], s_lq[kWave];
     __shared__ int32_t s_part[kMaxTok][2][kWave];
     __shared__ int32_t s_g2s[kPlanThreads];   // E <= 512
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -797,36 +807,59 @@ __global__ __launch_bounds__(kPlanThreads) void k_dec_plan(FwdArgs a, DecTable* 
     float lsg = 0.0f;   // the shared-expert gate's logit
     if constexpr (KP > 0) lsg = l[E];
     const int g0 = a.g2s[min(tid, E - 1)];
+    int sel_e = -1;
+    float w = 0.0f;
     if constexpr (KP > 0) {
         if (wv < a.T) {   // wave t ranks token t
             const RouteRule rr{a.route_bias, a.route_mode, a.n_group, a.topk_group, a.route_scale};
-            int sel_e;
             float sel_v;
             wave_select<KP>(v, rr, E, k, sel_e, sel_v);
-            const float w = wave_weight<KP>(v, rr, E, k, sel_e, sel_v);
-            if (lane < k) {
-                s_e[wv * k + lane] = sel_e;
-                a.route_idx[wv * k + lane] = sel_e;
-                a.route_w[wv * k + lane] = w;
-            }
-            if (lane == 0 && a.route_sg) a.route_sg[wv] = 1.0f / (1.0f + expf(-lsg));
+            w = wave_weight<KP>(v, rr, E, k, sel_e, sel_v);
+            if (lane < k) s_e[wv * k + lane] = sel_e;
         }
     } else {
         if (tid < P) s_e[tid] = a.pexp[tid];
     }
     if (tid < E) s_g2s[tid] = g0;
+    const float sg = 1.0f / (1.0f + expf(-lsg));
+    // every load has landed here, on every path (vmcnt 0), so no wait below covers the stores
+    __builtin_amdgcn_s_waitcnt(0x0F70);
     __syncthreads();
+    // the routing is published after the barrier: global stores count in the same in-order
+    // counter as the loads, so stores issued before the wait for g0 would be waited for too
+    if constexpr (KP > 0) {
+        if (wv < a.T) {
+            if (lane < k) {
+                a.route_idx[wv * k + lane] = sel_e;
+                a.route_w[wv * k + lane] = w;
+            }
+            if (lane == 0 && a.route_sg) a.route_sg[wv] = sg;
+        }
+    }
     // pair p = lane (p < P) against the pairs q of chunk c = wave: q = 8 c .. 8 c + 7. Experts
     // are clamped (id E names the shared expert); idle pairs match nothing.
     const int emax = a.shared ? E : E - 1;
-    auto expert = [&](int q) { return q < P ? min(max(s_e[q], 0), emax) : -1 - q; };
-    const int e = expert(lane);
+    // (the reads are unconditional -- entries past P hold no pair and are masked after the
+    // read -- so each chunk's eight come in two 16-byte reads rather than eight waits)
+    auto expert_of = [&](int q, int v) { return q < P ? min(max(v, 0), emax) : -1 - q; };
+    auto chunk = [&](const int32_t* arr, int out[kMaxTok]) {
+        const int4 lo = *reinterpret_cast<const int4*>(arr + wv * kMaxTok);
+        const int4 hi = *reinterpret_cast<const int4*>(arr + wv * kMaxTok + 4);
+        out[0] = lo.x; out[1] = lo.y; out[2] = lo.z; out[3] = lo.w;
+        out[4] = hi.x; out[5] = hi.y; out[6] = hi.z; out[7] = hi.w;
+    };
+    static_assert(kMaxTok == 8, "two 16-byte reads a chunk");
+    const int e = expert_of(lane, s_e[lane]);
+    int ce[kMaxTok];
+    chunk(s_e, ce);
+#pragma unroll
+    for (int i = 0; i < kMaxTok; ++i) ce[i] = expert_of(wv * kMaxTok + i, ce[i]);
     {
         int occ = 0, tot = 0;
 #pragma unroll
         for (int i = 0; i < kMaxTok; ++i) {
             const int q = wv * kMaxTok + i;
-            const bool m = expert(q) == e;
+            const bool m = ce[i] == e;
             occ += (m && q < lane) ? 1 : 0;
             tot += m ? 1 : 0;
         }
@@ -845,13 +878,16 @@ __global__ __launch_bounds__(kPlanThreads) void k_dec_plan(FwdArgs a, DecTable* 
         s_tot[lane] = tot;   // all pairs of that expert
     }
     __syncthreads();
-    // the lane of the pair that leads this pair's entry: the (occ & ~7)-th pair of its expert
+    // the lane of the pair that leads this pair's entry: the (occ & ~(kPlanTok - 1))-th pair of
+    // its expert
     {
         const int occ0 = s_occ[lane] & ~(kPlanTok - 1);
+        int co[kMaxTok];
+        chunk(s_occ, co);
 #pragma unroll
         for (int i = 0; i < kMaxTok; ++i) {
             const int q = wv * kMaxTok + i;
-            if (expert(q) == e && s_occ[q] == occ0) s_lq[lane] = q;
+            if (ce[i] == e && co[i] == occ0) s_lq[lane] = q;
         }
     }
     __syncthreads();
