@@ -53,8 +53,17 @@ constexpr int kBucketWaveRun = kWave * kBucketPer;            // pairs per wave 
 constexpr int kBucketPass = kBucketThreads * kBucketPer;
 constexpr int kBucketListMax = 8192;                          // pairs an LDS list may hold
 
-__device__ __forceinline__ int bucket_expert(const int32_t* __restrict__ pexp, int p, int P, int E, int emax) {
-    return p < P ? min(max(pexp[p], 0), emax) : E;
+// The experts of a lane's pairs pb + 64 i (i < kBucketPer; id E for the shared expert's pairs
+// past the P routed ones). The loads are unconditional (index clamped into the routed pairs), so
+// a lane's sixteen are in flight together rather than one round trip each.
+__device__ __forceinline__ void bucket_experts(const int32_t* __restrict__ pexp, int pb, int P, int E, int emax,
+                                               int ex[kBucketPer]) {
+    if (P > 0) {   // uniform
+#pragma unroll
+        for (int i = 0; i < kBucketPer; ++i) ex[i] = pexp[min(pb + i * kWave, P - 1)];
+    }
+#pragma unroll
+    for (int i = 0; i < kBucketPer; ++i) ex[i] = pb + i * kWave < P ? min(max(ex[i], 0), emax) : E;
 }
 
 __global__ __launch_bounds__(kBucketThreads) void k_bucket(const int32_t* __restrict__ pexp, int P, int E,
@@ -86,8 +95,7 @@ __global__ __launch_bounds__(kBucketThreads) void k_bucket(const int32_t* __rest
     for (int p0 = 0; p0 < P_ext; p0 += kBucketPass) {
         const int pb = p0 + wv * kBucketWaveRun + lane;
         int ex[kBucketPer];
-#pragma unroll
-        for (int i = 0; i < kBucketPer; ++i) ex[i] = bucket_expert(pexp, min(pb + i * kWave, P_ext - 1), P, E, emax);
+        bucket_experts(pexp, pb, P, E, emax, ex);
 #pragma unroll
         for (int i = 0; i < kBucketPer; ++i)
             if (pb + i * kWave < P_ext) atomicAdd(&hist[ex[i]], 1);
@@ -181,11 +189,12 @@ __global__ __launch_bounds__(kBucketThreads) void k_bucket(const int32_t* __rest
         const int pb = p0 + wv * kBucketWaveRun + lane;
         uint64_t m[kBucketPer];
         int cnt = 0;
+        int ex[kBucketPer];
+        bucket_experts(pexp, pb, P, E, emax, ex);
 #pragma unroll
         for (int i = 0; i < kBucketPer; ++i) {
             const int p = pb + i * kWave;
-            const int ex = bucket_expert(pexp, min(p, P_ext - 1), P, E, emax);
-            m[i] = __ballot(p < P_ext && ex == e);
+            m[i] = __ballot(p < P_ext && ex[i] == e);
             cnt += __popcll(m[i]);
         }
         if (lane == 0) wsum[wv] = cnt;
