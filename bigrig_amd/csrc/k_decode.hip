@@ -1498,9 +1498,10 @@ hipError_t launch_mode(const FwdArgs& a, uint16_t* hbuf, DecTable* table, uint16
         // pairs share its launch (a pool's span calls against the whole step).
         pick_split(a.H / 64, a.T > 1 ? 2 : 1, SP, upl_);
         hipError_t err;
-        if (a.T == 1 && !a.ptok && upl_ <= 2 && a.E <= 256 && nu <= kWave) {
-            err = upl_ == 1 ? launch_gateup1<MODE, 1>(a, hbuf, table, nu, Imax, SP, s)
-                            : launch_gateup1<MODE, 2>(a, hbuf, table, nu, Imax, SP, s);
+        if (a.T == 1 && !a.ptok && upl_ <= 3 && a.E <= 256 && nu <= kWave) {
+            err = upl_ == 1   ? launch_gateup1<MODE, 1>(a, hbuf, table, nu, Imax, SP, s)
+                  : upl_ == 2 ? launch_gateup1<MODE, 2>(a, hbuf, table, nu, Imax, SP, s)
+                              : launch_gateup1<MODE, 3>(a, hbuf, table, nu, Imax, SP, s);
         } else if (per_entry) {
             err = [&]() -> hipError_t { BRX_UPL_CASES(launch_gateupT, a, hbuf, table, nu, Imax, SP, s); }();
         } else {
