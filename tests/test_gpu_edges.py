@@ -1,4 +1,5 @@
-"""Edge cases of the path on the GPU, through the C-ABI: empty inputs, router ties, the largest
+"""Edge cases of the path on the GPU, through the C-ABI: empty inputs, router ties (also across a
+lane's registers and at the top-k boundary), -inf logits, the largest
 expert count the library takes (512, the in-kernel ranking's widest case), and top-1 routing.
 
 Bars as elsewhere: routing indices bit-exact against the oracle (ties to the lower expert id,
@@ -126,4 +127,49 @@ def test_top1_routing(gpu, T):
     ref, _ = oracle.moe_forward(spec, lay.experts, x, idx, w)
     r = oracle.rel_l2(F.bf16_bits_to_f32(bits(out)), F.bf16_bits_to_f32(ref))
     assert r < TOL, f"rel L2 {r:.3e}"
+    pool.close()
+
+
+@pytest.mark.parametrize("case", ["ties", "neg_inf"])
+def test_router_ties_across_registers_and_infinities(gpu, case):
+    """Exact logits from a one-hot token: ties between experts held in different registers of
+    one lane (6 and 70 at E = 128) and at the top-k boundary go to the lower id, and -inf ranks
+    below every number (taken lowest id first when fewer than k logits are finite), in the
+    in-kernel ranking and the chunk router alike; the expected order is written out by hand."""
+    import torch
+    spec = small(QWEN3_30B_A3B, hidden=512, inter=256, n_experts=128, top_k=8)
+    lay = make_layer(spec, seed=94)
+    col = 5
+    lg = np.full(spec.n_experts, -np.inf, np.float32)
+    if case == "ties":
+        for e, v in ((70, 2.0), (6, 2.0), (100, 2.0), (3, 1.5), (127, 0.0), (64, 0.0), (0, 0.0),
+                     (90, 0.0), (10, -1.0), (11, -1.0)):
+            lg[e] = v
+        want = [6, 70, 100, 3, 0, 64, 90, 127]
+    else:
+        for e, v in ((70, 2.0), (6, 2.0), (3, 1.5), (64, 0.0), (0, 0.0)):
+            lg[e] = v
+        want = [6, 70, 3, 0, 64, 1, 2, 4]
+    r = F.bf16_bits_to_f32(lay.router).copy()
+    r[:, col] = lg
+    lay.router = F.f32_to_bf16_bits(r)
+    _, sw, pool, _ = build_gpu_layer(lay, gpu)
+    pool.g2s_device(torch.cuda.current_stream().cuda_stream)
+    router = to_dev_bits(lay.router, gpu)
+    x = np.zeros((1, spec.hidden), np.uint16)
+    x[0, col] = 0x3F80   # bf16 1.0: logit e is the router's entry (e, col) exactly
+    _, idx, wref, _ = oracle.router(x, lay.router, False, None, spec.top_k, spec.route_mode)
+    assert list(idx[0]) == want
+    gi = torch.full((1, spec.top_k), -1, dtype=torch.int32, device=gpu)
+    gw = torch.zeros((1, spec.top_k), dtype=torch.float32, device=gpu)
+    ops.moe_block(spec, pool, to_dev_bits(x, gpu), router, out_idx=gi, out_w=gw,
+                  flags=ops.path_flag(1, spec.top_k))
+    i2, w2, _ = ops.router_topk(spec, to_dev_bits(x, gpu), router)
+    torch.cuda.synchronize()
+    assert list(gi.cpu().numpy()[0]) == want
+    assert list(i2.cpu().numpy()[0]) == want
+    np.testing.assert_allclose(gw.cpu().numpy(), wref, rtol=1e-6, atol=0)
+    np.testing.assert_allclose(w2.cpu().numpy(), wref, rtol=1e-6, atol=0)
+    if case == "neg_inf":
+        assert np.all(wref[0, 5:] == 0.0)
     pool.close()
