@@ -1,6 +1,6 @@
 """Edge cases of the path on the GPU, through the C-ABI: empty inputs, router ties (also across a
-lane's registers and at the top-k boundary), -inf logits, the largest
-expert count the library takes (512, the in-kernel ranking's widest case), and top-1 routing.
+lane's registers and at the top-k boundary), -inf logits, the largest expert count the library
+takes (512, the in-kernel ranking's widest case), and top-1 routing.
 
 Bars as elsewhere: routing indices bit-exact against the oracle (ties to the lower expert id,
 the rule of the reference's argsort over -logits, pool.py:333), outputs within 1e-2 relative
