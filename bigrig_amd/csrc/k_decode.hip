@@ -927,18 +927,28 @@ __global__ __launch_bounds__(kPlanThreads) void k_dec_plan(FwdArgs a, DecTable* 
 // The (entry, token group, row block) of per-entry block b: blocks u * nrb + rb with u < n take
 // entry u's first kPlanTok pairs; past the n entries, the next groups of the last entry (the
 // shared expert, which takes every token). Returns the row block, or -1 for a block with no
-// work; u, t0 (its first pair's index in the entry) and nt (its pair count) are set otherwise.
-__device__ __forceinline__ int entry_group(const DecTable* table, int b, int nrb, int& u, int& t0, int& nt) {
+// work; u, t0 (its first pair's index in the entry), nt (its pair count) and slot (entry u's slot
+// code) are set otherwise. The header of row b / nrb's entry is read together with n: that is
+// the block's entry for every block but the shared expert's later token groups, which read
+// entry n - 1's once n is known.
+__device__ __forceinline__ int entry_group(const DecTable* table, int b, int nrb, int& u, int& t0, int& nt,
+                                           int& slot) {
     const int n = table->n;
     u = b / nrb;
     const int rb = b - u * nrb;
-    int c = 0;
+    const int2 h0 = *reinterpret_cast<const int2*>(&table->ent[min(u, kMaxU - 1)]);   // (slot, nt)
+    int c = 0, nt_all = h0.y;
+    slot = h0.x;
     if (u >= n) {
         c = u - n + 1;
         u = n - 1;
+        if (u >= 0 && u < kMaxU) {
+            slot = table->ent[u].slot;
+            nt_all = table->ent[u].nt;
+        }
     }
     if (u < 0 || u >= kMaxU) return -1;
-    const int nall = min(max(table->ent[u].nt, 0), kMaxTok);
+    const int nall = min(max(nt_all, 0), kMaxTok);
     t0 = c * kPlanTok;
     nt = min(kPlanTok, nall - t0);
     return nt > 0 ? rb : -1;
@@ -958,10 +968,11 @@ __global__ __launch_bounds__(kThreads) void k_dec_gateupT(FwdArgs a, uint16_t* _
     const int lane = threadIdx.x & 63, tid = threadIdx.x;
     const int H = a.H, U = H / 64;
     int u, t0, nt;
-    const int rb = entry_group(table, blockIdx.x, nrb, u, t0, nt);
+    int eslot;
+    const int rb = entry_group(table, blockIdx.x, nrb, u, t0, nt, eslot);
     if (rb < 0) return;   // uniform
     const DecEntry& en = table->ent[u];
-    const int slot = clamp_code(a, en.slot);
+    const int slot = clamp_code(a, eslot);
     const int PT = a.P + (a.auto_shared ? a.T : 0);
     const bool sh = slot == -1;
     const int inter = sh ? a.I_sh : a.I;
@@ -1030,10 +1041,11 @@ __global__ __launch_bounds__(kThreads) void k_dec_downT(FwdArgs a, const uint16_
     const int lane = threadIdx.x & 63, tid = threadIdx.x;
     const int H = a.H;
     int u, t0, nt;
-    const int rb = entry_group(table, blockIdx.x, nrb, u, t0, nt);
+    int eslot;
+    const int rb = entry_group(table, blockIdx.x, nrb, u, t0, nt, eslot);
     if (rb < 0) return;   // uniform
     const DecEntry& en = table->ent[u];
-    const int slot = clamp_code(a, en.slot);
+    const int slot = clamp_code(a, eslot);
     const int PT = a.P + (a.auto_shared ? a.T : 0);
     const Layout& L = slot == -1 ? a.lay_sh : a.lay;
     const int K = L.p[2].n_in, U = K / 64;
