@@ -927,16 +927,21 @@ __global__ __launch_bounds__(kPlanThreads) void k_dec_plan(FwdArgs a, DecTable* 
 // The (entry, token group, row block) of per-entry block b: blocks u * nrb + rb with u < n take
 // entry u's first kPlanTok pairs; past the n entries, the next groups of the last entry (the
 // shared expert, which takes every token). Returns the row block, or -1 for a block with no
-// work; u, t0 (its first pair's index in the entry), nt (its pair count) and slot (entry u's slot
-// code) are set otherwise. The header of row b / nrb's entry is read together with n: that is
-// the block's entry for every block but the shared expert's later token groups, which read
-// entry n - 1's once n is known.
+// work; u, t0 (its first pair's index in the entry), nt (its pair count), slot (entry u's slot
+// code) and, for threads below kPlanTok, pair (the entry's pair t0 + thread) are set otherwise.
+// Row b / nrb's entry is read together with n -- that is the block's entry for every block but
+// the shared expert's later token groups, which read entry n - 1 once n is known -- and before
+// any weight load, so the pairs (and the token rows staged from them) do not wait behind the
+// weights: loads complete in issue order.
 __device__ __forceinline__ int entry_group(const DecTable* table, int b, int nrb, int& u, int& t0, int& nt,
-                                           int& slot) {
+                                           int& slot, int& pair) {
+    const int tid = threadIdx.x;
     const int n = table->n;
     u = b / nrb;
     const int rb = b - u * nrb;
-    const int2 h0 = *reinterpret_cast<const int2*>(&table->ent[min(u, kMaxU - 1)]);   // (slot, nt)
+    const int u0 = min(u, kMaxU - 1);
+    const int2 h0 = *reinterpret_cast<const int2*>(&table->ent[u0]);   // (slot, nt)
+    pair = tid < kPlanTok ? table->ent[u0].pair[tid] : 0;
     int c = 0, nt_all = h0.y;
     slot = h0.x;
     if (u >= n) {
@@ -945,6 +950,7 @@ __device__ __forceinline__ int entry_group(const DecTable* table, int b, int nrb
         if (u >= 0 && u < kMaxU) {
             slot = table->ent[u].slot;
             nt_all = table->ent[u].nt;
+            pair = tid < kPlanTok ? table->ent[u].pair[min(c * kPlanTok + tid, kMaxTok - 1)] : 0;
         }
     }
     if (u < 0 || u >= kMaxU) return -1;
@@ -967,11 +973,11 @@ __global__ __launch_bounds__(kThreads) void k_dec_gateupT(FwdArgs a, uint16_t* _
     const int SP = 1 << lsp;
     const int lane = threadIdx.x & 63, tid = threadIdx.x;
     const int H = a.H, U = H / 64;
+    __shared__ int32_t s_pair[kPlanTok];
     int u, t0, nt;
-    int eslot;
-    const int rb = entry_group(table, blockIdx.x, nrb, u, t0, nt, eslot);
+    int eslot, epair;
+    const int rb = entry_group(table, blockIdx.x, nrb, u, t0, nt, eslot, epair);
     if (rb < 0) return;   // uniform
-    const DecEntry& en = table->ent[u];
     const int slot = clamp_code(a, eslot);
     const int PT = a.P + (a.auto_shared ? a.T : 0);
     const bool sh = slot == -1;
@@ -995,7 +1001,8 @@ __global__ __launch_bounds__(kThreads) void k_dec_gateupT(FwdArgs a, uint16_t* _
     }
     // the entry's token rows, staged while the weights are in flight
     if (tid < nt) {
-        const int pair = min(max(en.pair[t0 + tid], 0), PT - 1);
+        const int pair = min(max(epair, 0), PT - 1);
+        s_pair[tid] = pair;
         s_tok[tid] = pair < a.P ? pair_tok(a, pair) : pair - a.P;
     }
     __syncthreads();
@@ -1004,7 +1011,7 @@ __global__ __launch_bounds__(kThreads) void k_dec_gateupT(FwdArgs a, uint16_t* _
     stage_dense<MODE>(a.x, H, nt, [&](int i) { return s_tok[i]; }, xs, xsum);
     __syncthreads();
     for (int i = 0; i < nt; ++i) {
-        const int pair = min(max(en.pair[t0 + i], 0), PT - 1);
+        const int pair = s_pair[i];
         float pg = 0.f, pu = 0.f;
 #pragma unroll
         for (int j = 0; j < UPL; ++j) {
@@ -1041,10 +1048,9 @@ __global__ __launch_bounds__(kThreads) void k_dec_downT(FwdArgs a, const uint16_
     const int lane = threadIdx.x & 63, tid = threadIdx.x;
     const int H = a.H;
     int u, t0, nt;
-    int eslot;
-    const int rb = entry_group(table, blockIdx.x, nrb, u, t0, nt, eslot);
+    int eslot, epair;
+    const int rb = entry_group(table, blockIdx.x, nrb, u, t0, nt, eslot, epair);
     if (rb < 0) return;   // uniform
-    const DecEntry& en = table->ent[u];
     const int slot = clamp_code(a, eslot);
     const int PT = a.P + (a.auto_shared ? a.T : 0);
     const Layout& L = slot == -1 ? a.lay_sh : a.lay;
@@ -1059,7 +1065,7 @@ __global__ __launch_bounds__(kThreads) void k_dec_downT(FwdArgs a, const uint16_
     Units<MODE, UPL> ud;
     units_load<MODE, UPL>(base, L.p[2], row, sl, SP, ud);
     const float bd = L.p[2].bias >= 0 ? bf2f(reinterpret_cast<const uint16_t*>(base + L.p[2].bias)[row]) : 0.f;
-    if (tid < nt) s_pair[tid] = min(max(en.pair[t0 + tid], 0), PT - 1);
+    if (tid < nt) s_pair[tid] = min(max(epair, 0), PT - 1);
     __syncthreads();
     // h rows are staged at their full width (hstride / 64 units); the entry reads its U
     const int Us = hstride / 64;
