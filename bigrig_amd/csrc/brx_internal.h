@@ -435,11 +435,17 @@ template <int kPer>
 __device__ __forceinline__ void route_values(const float v[kPer], const RouteRule& rr, int E, float c[kPer]) {
     const int lane = threadIdx.x & (kWave - 1);
     const bool sig = route_sigmoid(rr.mode);
+    // the selection bias: one branch around all kPer loads (uniform), so they are in flight
+    // together rather than one round trip each
+    float bv[kPer];
 #pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-        const int e = min(lane + kWave * i, E - 1);
-        c[i] = sig ? sigmoid_f(v[i]) + (rr.bias ? rr.bias[e] : 0.0f) : v[i];
+    for (int i = 0; i < kPer; ++i) bv[i] = 0.0f;
+    if (sig && rr.bias) {
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) bv[i] = rr.bias[min(lane + kWave * i, E - 1)];
     }
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) c[i] = sig ? sigmoid_f(v[i]) + bv[i] : v[i];
     if (rr.n_group <= 1) return;
     const int G = E / rr.n_group;
     float gs = -__builtin_inff();          // lane g: group g's score
