@@ -756,7 +756,15 @@ __global__ __launch_bounds__(kThreads) void k_combine(const uint16_t* __restrict
             acc[2 * i + 1] = fmaf(wj, bf2f(q[i] >> 16), acc[2 * i + 1]);
         }
     };
-    for (int j0 = 0; j0 < k; j0 += KB) {
+    // the shared expert's row and gate are requested with the first routed rows (it is added
+    // last, in the same order as before, but its round trip is not a second one)
+    // (the load is unconditional -- from routed row 0 when there is no shared expert, and then
+    // unused -- so no branch holds it back)
+    const bool has_sh = y_shared && sg;   // uniform
+    const uint16_t* shrow = has_sh ? y_shared + (int64_t)t * H + n : y_routed + (int64_t)t * k * H + n;
+    const VT vsh = *reinterpret_cast<const VT*>(shrow);
+    const float wsh = has_sh ? sg[t] : 0.f;
+    auto batch = [&](int j0) __attribute__((always_inline)) {
         VT v[KB];
         float wj[KB];
 #pragma unroll
@@ -768,8 +776,12 @@ __global__ __launch_bounds__(kThreads) void k_combine(const uint16_t* __restrict
 #pragma unroll
         for (int u = 0; u < KB; ++u)
             if (j0 + u < k) add(wj[u], v[u]);
-    }
-    if (y_shared && sg) add(sg[t], *reinterpret_cast<const VT*>(y_shared + (int64_t)t * H + n));
+    };
+    // the first KB rows outside the loop: straight-line code after the shared row's load, so
+    // nothing makes them wait for it
+    batch(0);
+    for (int j0 = KB; j0 < k; j0 += KB) batch(j0);
+    if (has_sh) add(wsh, vsh);
     uint32_t o[NW];
 #pragma unroll
     for (int i = 0; i < NW; ++i) o[i] = f2bf(acc[2 * i]) | (f2bf(acc[2 * i + 1]) << 16);
