@@ -135,8 +135,9 @@ __device__ __forceinline__ void route_load(const FwdArgs& a, RouteRegs<kPer>& rg
 #pragma unroll
         for (int i = 0; i < kPer; ++i) {
             const int e = lane + kWave * i;
-            const float v = l[min(e, E - 1)];   // clamped, branch-free
-            rg.v[tt][i] = e < E ? v : 0.0f;
+            // clamped and used as loaded (a select here would wait for the load): lanes past E
+            // hold a copy of the last logit, which every ranking and weight step masks out
+            rg.v[tt][i] = l[min(e, E - 1)];
         }
     }
 }
@@ -657,19 +658,20 @@ __global__ __launch_bounds__(kThreads) void k_dec_gateup1(FwdArgs a, uint16_t* _
     uint8_t* xs = lds;
     float* xsum = reinterpret_cast<float*>(lds + (size_t)U * kXU);
     // one round trip: the routing (logits or the given pairs), the slot table (wave 0) and x
-    const int ng = (E + kWave - 1) / kWave;
-    int g2s[kG];
-    if (wv == 0) {
+    // (every wave issues these loads, only wave 0 uses them: no branch around a load, so none is
+    // waited for before x is requested; the table registers past E repeat its last entry and
+    // are never selected)
+    constexpr int kGn = KP > 0 ? KP : kG;   // KP * 64 >= E
+    int g2s[kGn];
 #pragma unroll
-        for (int i = 0; i < kG; ++i) g2s[i] = i < ng ? a.g2s[min(lane + kWave * i, E - 1)] : -1;
-    }
+    for (int i = 0; i < kGn; ++i) g2s[i] = a.g2s[min(lane + kWave * i, E - 1)];
     int pe = 0;
     if constexpr (KP == 0) pe = a.pexp[min(lane, P - 1)];
     RouteRegs<(KP > 0 ? KP : 1)> rg;
     float lsg = 0.0f;   // the shared-expert gate's logit (block 0 publishes its sigmoid)
     if constexpr (KP > 0) {
-        if (wv == 0) route_load<KP>(a, rg);
-        if (wv == 0 && blockIdx.x == 0 && a.route_sg) lsg = a.logits[E];
+        route_load<KP>(a, rg);
+        lsg = a.logits[E];
     }
     StageRegs st;
     auto tok_row = [](int i) { return i; };
@@ -701,7 +703,7 @@ __global__ __launch_bounds__(kThreads) void k_dec_gateup1(FwdArgs a, uint16_t* _
         const int ec = min(max(e, 0), E - 1);
         int v = -1;
 #pragma unroll
-        for (int i = 0; i < kG; ++i) {
+        for (int i = 0; i < kGn; ++i) {
             const int t = __shfl(g2s[i], ec & (kWave - 1), kWave);
             if (i == (ec >> 6)) v = t;
         }
@@ -800,8 +802,7 @@ __global__ __launch_bounds__(kPlanThreads) void k_dec_plan(FwdArgs a, DecTable* 
 #pragma unroll
         for (int i = 0; i < KP; ++i) {
             const int e = lane + kWave * i;
-            const float x = l[min(e, E - 1)];   // clamped, branch-free
-            v[i] = e < E ? x : 0.0f;
+            v[i] = l[min(e, E - 1)];   // clamped, used as loaded (lanes past E are masked later)
         }
     }
     float lsg = 0.0f;   // the shared-expert gate's logit
