@@ -381,53 +381,75 @@ __device__ __forceinline__ void stage_store(int K, int nrows, int base, const St
     }
 }
 
-// The same staging with the pieces of all rows numbered densely (piece g of the block is row
-// g / (8U), unit (g / 8) % U, piece g % 8) and handed to the threads kStageB at a time, so rows
-// shorter than the block (h rows of 8-16 units) still take one round trip per kStageB * kThreads
-// pieces. The 8 pieces of a unit stay on 8 consecutive lanes.
-template <int MODE, int NB = kStageB, typename RowOf>
-__device__ __forceinline__ void stage_dense(const uint16_t* __restrict__ src, int K, int nrows, RowOf row_of,
-                                            uint8_t* xs, float* sums) {
+// One pass of stage_dense, split so a caller can issue other loads between the two halves:
+// dense_issue requests the pieces [base, base + NB * kThreads) into registers, dense_store
+// writes them (and the unit sums) to LDS.
+template <int NB>
+struct DenseRegs {
+    uint4 v[NB];
+    int gi[NB];
+};
+template <int NB, typename RowOf>
+__device__ __forceinline__ void dense_issue(const uint16_t* __restrict__ src, int K, int nrows, RowOf row_of,
+                                            int base, DenseRegs<NB>& d) {
+    const int pcs = (K / 64) * 8;
+    const int total = nrows * pcs;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        const int g = min(base + b * kThreads + (int)threadIdx.x, total - 1);
+        d.gi[b] = g;
+        const int r = g / pcs, pi = g - r * pcs;
+        const int off = row_of(r) * K + (pi >> 3) * 64 + (pi & 7) * 8;
+        d.v[b] = *reinterpret_cast<const uint4*>(src + off);
+    }
+}
+template <int MODE, int NB>
+__device__ __forceinline__ void dense_store(int K, int nrows, int base, const DenseRegs<NB>& d, uint8_t* xs,
+                                            float* sums) {
     const int U = K / 64;
     const int pcs = U * 8;
     const int total = nrows * pcs;
-    for (int base = 0; base < total; base += NB * kThreads) {
-        uint4 v[NB];
-        int gi[NB];
 #pragma unroll
-        for (int b = 0; b < NB; ++b) {
-            const int g = min(base + b * kThreads + (int)threadIdx.x, total - 1);
-            gi[b] = g;
-            const int r = g / pcs, pi = g - r * pcs;
-            const int off = row_of(r) * K + (pi >> 3) * 64 + (pi & 7) * 8;
-            v[b] = *reinterpret_cast<const uint4*>(src + off);
+    for (int b = 0; b < NB; ++b) {
+        if (base + b * kThreads >= total) break;   // uniform
+        const bool ok = base + b * kThreads + (int)threadIdx.x < total;
+        const int g = d.gi[b];
+        const int r = g / pcs, pi = g - r * pcs;
+        const int un = pi >> 3, q = pi & 7;
+        uint32_t in[4] = {d.v[b].x, d.v[b].y, d.v[b].z, d.v[b].w}, o[4];
+        float part = 0.0f;
+        if constexpr (kAffine<MODE>) {
+            perm8(in, o);
+#pragma unroll
+            for (int z = 0; z < 4; ++z)
+                part = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, in[z]),
+                                                       __builtin_bit_cast(bf16x2_t, 0x3F803F80u), part, false);
+        } else {
+#pragma unroll
+            for (int z = 0; z < 4; ++z) o[z] = in[z];
         }
-#pragma unroll
-        for (int b = 0; b < NB; ++b) {
-            if (base + b * kThreads >= total) break;   // uniform
-            const bool ok = base + b * kThreads + (int)threadIdx.x < total;
-            const int g = gi[b];
-            const int r = g / pcs, pi = g - r * pcs;
-            const int un = pi >> 3, q = pi & 7;
-            uint32_t in[4] = {v[b].x, v[b].y, v[b].z, v[b].w}, o[4];
-            float part = 0.0f;
-            if constexpr (kAffine<MODE>) {
-                perm8(in, o);
-#pragma unroll
-                for (int z = 0; z < 4; ++z)
-                    part = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, in[z]),
-                                                           __builtin_bit_cast(bf16x2_t, 0x3F803F80u), part, false);
-            } else {
-#pragma unroll
-                for (int z = 0; z < 4; ++z) o[z] = in[z];
-            }
-            if (ok)
-                *reinterpret_cast<uint4*>(xs + ((int64_t)r * U + un) * kXU + q * 16) = make_uint4(o[0], o[1], o[2], o[3]);
-            if constexpr (kAffine<MODE>) {
-                part = sum8_dpp(part);
-                if (ok && q == 0) sums[r * U + un] = part;
-            }
+        if (ok)
+            *reinterpret_cast<uint4*>(xs + ((int64_t)r * U + un) * kXU + q * 16) = make_uint4(o[0], o[1], o[2], o[3]);
+        if constexpr (kAffine<MODE>) {
+            part = sum8_dpp(part);
+            if (ok && q == 0) sums[r * U + un] = part;
         }
+    }
+}
+
+// The same staging with the pieces of all rows numbered densely (piece g of the block is row
+// g / (8U), unit (g / 8) % U, piece g % 8) and handed to the threads kStageB at a time, so rows
+// shorter than the block (h rows of 8-16 units) still take one round trip per kStageB * kThreads
+// pieces. The 8 pieces of a unit stay on 8 consecutive lanes. `first` > 0 skips the pieces a
+// caller already staged.
+template <int MODE, int NB = kStageB, typename RowOf>
+__device__ __forceinline__ void stage_dense(const uint16_t* __restrict__ src, int K, int nrows, RowOf row_of,
+                                            uint8_t* xs, float* sums, int first = 0) {
+    const int total = nrows * (K / 64) * 8;
+    for (int base = first; base < total; base += NB * kThreads) {
+        DenseRegs<NB> d;
+        dense_issue<NB>(src, K, nrows, row_of, base, d);
+        dense_store<MODE, NB>(K, nrows, base, d, xs, sums);
     }
 }
 
@@ -1315,8 +1337,15 @@ __global__ __launch_bounds__(kThreads) void k_dec_down_fit(FwdArgs a, const uint
     const int g = lane >> lsp, sl = lane & (SP - 1);
     const int items = nu * RBD;
 
-    for (int it0 = 0; it0 < items; it0 += kWaves * RW) {
-        if (it0 > 0 && it0 >= table->n * RBD) break;   // passes past the step's entries: no work
+    // every pair's h rows: the first pass requested with the first items' table rows, stored to
+    // LDS once those items' weights are requested
+    auto ident = [](int i) { return i; };
+    DenseRegs<kStageB> hrows;
+    dense_issue<kStageB>(hbuf, hstride, PT, ident, 0, hrows);
+    // the pass body; the first pass runs outside the loop, as straight-line code after the h
+    // loads, so nothing copies (and so waits for) the h registers before the weights are
+    // requested
+    auto pass = [&](int it0, bool first) __attribute__((always_inline)) {
         const int it = it0 + (tid >> 6) * RW + g;
         const bool in_range = it < items;
         const int u = min(it >> lrbd, nu - 1);
@@ -1324,9 +1353,6 @@ __global__ __launch_bounds__(kThreads) void k_dec_down_fit(FwdArgs a, const uint
         // the item's table row: header and pair ids, three 16-byte loads
         const uint4* ep = reinterpret_cast<const uint4*>(&table->ent[u]);
         const uint4 hd = ep[0], p0 = ep[1], p1 = ep[2];
-        if (it0 == 0) {   // h rows of every pair, in the same round trip
-            stage_dense<MODE>(hbuf, hstride, PT, [](int i) { return i; }, hs, hsum);
-        }
         const int nt = in_range ? (int)hd.y : 0;
         int slot = nt > 0 ? (int)hd.x : 0;
         slot = clamp_code(a, slot);
@@ -1334,7 +1360,17 @@ __global__ __launch_bounds__(kThreads) void k_dec_down_fit(FwdArgs a, const uint
         const int U = L.p[2].n_in / 64;
         Units<MODE, UPL> ud;
         units_load<MODE, UPL>(code_base(a, slot), L.p[2], min(n0 + r, H - 1), sl, SP, ud);
-        if (it0 == 0) __syncthreads();
+        if (first) {
+            // (an empty asm on the loaded registers keeps the store's arithmetic here, after the
+            // weight requests, rather than hoisted next to the loads)
+#pragma unroll
+            for (int q = 0; q < kStageB; ++q)
+                asm volatile("" : "+v"(hrows.v[q].x), "+v"(hrows.v[q].y), "+v"(hrows.v[q].z),
+                             "+v"(hrows.v[q].w));
+            dense_store<MODE, kStageB>(hstride, PT, 0, hrows, hs, hsum);
+            stage_dense<MODE>(hbuf, hstride, PT, ident, hs, hsum, kStageB * kThreads);
+            __syncthreads();
+        }
         const int pr[kMaxTok] = {(int)p0.x, (int)p0.y, (int)p0.z, (int)p0.w,
                                  (int)p1.x, (int)p1.y, (int)p1.z, (int)p1.w};
         // the SP lanes of one item share nt; lanes past the items have nt = 0 and only take
@@ -1358,6 +1394,11 @@ __global__ __launch_bounds__(kThreads) void k_dec_down_fit(FwdArgs a, const uint
             p = group_sum(p, SP);
             if (sl == 0 && i < nt && n0 + r < H) ys[hr * RBD + r] = p;
         }
+    };
+    pass(0, true);
+    for (int it0 = kWaves * RW; it0 < items; it0 += kWaves * RW) {
+        if (it0 >= table->n * RBD) break;   // passes past the step's entries: no work
+        pass(it0, false);
     }
     __syncthreads();
     dec_down_epilogue(a, ys, RBD, lrbd, n0);
