@@ -41,9 +41,26 @@ __global__ __launch_bounds__(kRouterThreads) void k_router_tiled(
     const int nt = min(TT, T - t0);
     const int nch = H / 8;
     const uint4* x4 = reinterpret_cast<const uint4*>(x);
-    for (int i = tid; i < TT * nch; i += kRouterThreads) {
-        const int t = i / nch, c = i - t * nch;
-        xs4[i] = t < nt ? x4[(int64_t)(t0 + t) * nch + c] : make_uint4(0, 0, 0, 0);
+    // kSt chunks a thread in flight at once (token rows clamped into the tile, so every load is
+    // unconditional), then the stores: a load and its store per iteration would make each of the
+    // TT * nch / kRouterThreads chunks a round trip of its own
+    {
+        constexpr int kSt = 16;
+        const int nall = TT * nch;
+        for (int i0 = 0; i0 < nall; i0 += kSt * kRouterThreads) {
+            uint4 v[kSt];
+#pragma unroll
+            for (int b = 0; b < kSt; ++b) {
+                const int i = min(i0 + b * kRouterThreads + tid, nall - 1);
+                const int t = i / nch, c = i - t * nch;
+                v[b] = x4[(int64_t)(t0 + min(t, nt - 1)) * nch + c];
+            }
+#pragma unroll
+            for (int b = 0; b < kSt; ++b) {
+                const int i = i0 + b * kRouterThreads + tid;
+                if (i < nall) xs4[i] = i / nch < nt ? v[b] : make_uint4(0, 0, 0, 0);
+            }
+        }
     }
     __syncthreads();
     const int rows = E + (sgw ? 1 : 0);
