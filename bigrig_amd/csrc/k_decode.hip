@@ -799,10 +799,11 @@ __global__ __launch_bounds__(kThreads) void k_dec_gateup1(FwdArgs a, uint16_t* _
 // ------------------------------------------------------------------ several tokens
 // k_dec_plan: one block ranks every token's top-k once (wave t takes token t; with the pairs
 // given, they are read instead) and plans the step: the pairs routed to one expert are merged,
-// in pair order, into entries of at most 8 pairs, numbered in order of their first pair (so an
-// expert is read once for all the step's tokens that chose it); the shared expert, when the
-// layer has one, is the last entry and takes every token. It writes the entry table and the
-// routing (indices, weights, shared-expert gate) that the gate/up and down kernels read.
+// in pair order, into entries of at most kPlanTok pairs, numbered in order of their first pair
+// (so an expert is read by one entry per kPlanTok of the step's tokens that chose it); the
+// shared expert, when the layer has one, is the last entry and takes every token. It writes the
+// entry table and the routing (indices, weights, shared-expert gate) that the gate/up and down
+// kernels read.
 constexpr int kPlanThreads = kWave * kMaxTok;
 // pairs per entry the plan forms: an expert chosen by more tokens is read by more entries, so
 // the blocks of a popular expert do no more than 4 tokens' dot products each
