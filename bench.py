@@ -27,7 +27,8 @@ Also reported on the same line:
                 previous layer computes (PCIe-inclusive)
   policy_replay the eviction-policy trace replay (host C++, libbrx_replay.so) against the
                 Python restatement, requests/s on the shipped Qwen3 routing trace
-  cpu_baseline  the C restatement (oracle/) on the host cores, on a bounded sample
+  cpu_baseline  the fp32 dequant-on-the-fly CPU layer (oracle/cpu_baseline.c, OpenMP) on
+                the host cores, on a bounded sample
 """
 from __future__ import annotations
 
@@ -617,8 +618,10 @@ def replay_bench() -> dict:
 
 
 def cpu_bench(args, st: "Stack"):
-    """The oracle's C restatement (OpenMP) on a bounded sample: decode tokens through two
-    layers until cpu_seconds of work, scaled to the 48-layer stack."""
+    """The CPU baseline (oracle/cpu_baseline.c: router, fp32 dequant-on-the-fly GEMVs and the
+    combine, OpenMP over output rows) on a bounded sample: decode tokens through two layers of
+    the same stack, read from the pinned host copies of their experts, until cpu_seconds of
+    work, scaled to the 48-layer stack."""
     import numpy as np
     import torch
 
@@ -626,10 +629,9 @@ def cpu_bench(args, st: "Stack"):
     spec = st.spec
     oracle.build(force=False)
     nlay = 2
-    experts, routers, biases = [], [], []
+    blobs, routers, biases = [], [], []
     for l in range(nlay):
-        blob = st.host.tensor(l).numpy()
-        experts.append([blob[e].tobytes() for e in range(spec.n_experts)])
+        blobs.append(st.host.tensor(l))          # pinned [E, bytes_per_expert] uint8
         routers.append(st.routers[l].view(torch.int16).cpu().numpy().view(np.uint16))
         biases.append(st.biases[l].cpu().numpy())
     xs = [st.xbank[l].view(torch.int16).cpu().numpy().view(np.uint16) for l in range(nlay)]
@@ -638,10 +640,8 @@ def cpu_bench(args, st: "Stack"):
     n, t0 = 0, time.perf_counter()
     while True:
         for l in range(nlay):
-            x = xs[l][n % G:n % G + 1]
-            _, idx, w, _ = oracle.router(x, routers[l], False, biases[l], spec.top_k,
-                                         spec.route_mode)
-            oracle.moe_forward(spec, experts[l], x, idx, w, nthreads=cores)
+            oracle.cpu_baseline_decode(spec, xs[l][n % G], routers[l], biases[l],
+                                       blobs[l].data_ptr(), blobs[l].shape[1], nthreads=cores)
         n += 1
         el = time.perf_counter() - t0
         if el >= args.cpu_seconds:
@@ -649,8 +649,8 @@ def cpu_bench(args, st: "Stack"):
     per_layer_tok = el / (n * nlay)
     return {"value": 1.0 / (per_layer_tok * 48), "unit": "tokens/s", "cores": cores,
             "kind": "port",
-            "sample": f"{n} decode tokens x {nlay} layers of the same stack (router + 8 experts + "
-                      f"combine per layer-token, OpenMP over (token, expert) rows), "
+            "sample": f"{n} decode tokens x {nlay} layers of the same stack (router, 8 experts as "
+                      f"fp32 dequant-on-the-fly GEMVs, combine; OpenMP over output rows), "
                       f"{el:.1f}s, scaled to 48 layers"}
 
 

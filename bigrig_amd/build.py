@@ -2,13 +2,15 @@
 host-only trace-replay library libbrx_replay.so with g++.
 
     python -m bigrig_amd.build            # compile bigrig_amd/libbrx.so and libbrx_replay.so
+    python -m bigrig_amd.build --incremental   # recompile only sources changed since their object
 
 The library is one hipcc invocation over every `csrc/*.hip` file. Packed FP32 instructions are
 disabled for device code (`-Xclang -target-feature -Xclang -packed-fp32-ops`); the host pass
 warns that it does not know that feature, which is harmless. MFMA accumulators are allocated in
 ordinary VGPRs (`-mllvm -amdgpu-mfma-vgpr-form=1`): with them in AGPRs the register allocator
-rotated the prefill GEMM's accumulators between loop iterations, costing ~190 register copies
-per K step.
+rotated the 128-row prefill GEMM's accumulators between loop iterations, costing ~190 register
+copies per K step. The sources in AGPR_SOURCES hold more accumulators than VGPRs can and are
+built without that option.
 """
 from __future__ import annotations
 
@@ -46,24 +48,39 @@ def _run(cmd, verbose: bool, what: str) -> None:
         print(out)
 
 
-def build(verbose: bool = False) -> str:
+# Sources whose MFMA accumulators do not fit in ordinary VGPRs (256-row GEMM tiles: 256
+# accumulators a lane): built without the VGPR-form option, so they live in AGPRs.
+AGPR_SOURCES = {"k_pf_big.hip"}
+
+
+def build(verbose: bool = False, incremental: bool = False) -> str:
     """Compile every csrc/*.hip to an object in parallel (each file carries its own device code
-    object; kernels are only launched from the file that defines them), then link."""
+    object; kernels are only launched from the file that defines them), then link. With
+    `incremental`, objects newer than their source and every header are kept."""
     from concurrent.futures import ThreadPoolExecutor
     srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
     if not srcs:
         raise RuntimeError(f"no HIP sources under {CSRC}")
     objdir = os.path.join(PKG, "_build")
     os.makedirs(objdir, exist_ok=True)
-    flags = [f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
-             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-             "-mllvm", "-amdgpu-mfma-vgpr-form=1",
-             "-Wno-unused-command-line-argument", "-I", INCLUDE, "-I", CSRC]
+    base = [f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
+            "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+            "-Wno-unused-command-line-argument", "-I", INCLUDE, "-I", CSRC]
+    vgpr_form = ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]
     objs = [os.path.join(objdir, os.path.basename(s)[:-4] + ".o") for s in srcs]
+    headers = glob.glob(os.path.join(CSRC, "*.h")) + glob.glob(os.path.join(INCLUDE, "*.h"))
+    newest_h = max((os.path.getmtime(h) for h in headers), default=0.0)
+
+    def stale(s, o):
+        return (not incremental or not os.path.exists(o) or
+                os.path.getmtime(o) < max(os.path.getmtime(s), newest_h))
+
     jobs = min(len(srcs), max(1, min(16, os.cpu_count() or 1)))
     with ThreadPoolExecutor(jobs) as ex:
-        futs = [ex.submit(_run, [hipcc(), *flags, "-c", s, "-o", o], verbose, f"hipcc {s}")
-                for s, o in zip(srcs, objs)]
+        futs = [ex.submit(_run, [hipcc(), *base,
+                                 *([] if os.path.basename(s) in AGPR_SOURCES else vgpr_form),
+                                 "-c", s, "-o", o], verbose, f"hipcc {s}")
+                for s, o in zip(srcs, objs) if stale(s, o)]
         for f in futs:
             f.result()
     tmp = LIB + ".tmp"
@@ -92,4 +109,4 @@ def build_replay(verbose: bool = False) -> str:
 
 
 if __name__ == "__main__":
-    print(build(verbose="-q" not in sys.argv))
+    print(build(verbose="-q" not in sys.argv, incremental="--incremental" in sys.argv))

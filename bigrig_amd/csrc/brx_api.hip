@@ -58,7 +58,8 @@ int check_desc(const brx_layer_desc* d) {
     if (d->inter <= 0 || d->inter % 64)
         return fail(BRX_EINVAL, "inter %d must be a positive multiple of 64", d->inter);
     // the decode kernels stage 8 token rows of x (and h rows) in LDS and split a weight row over
-    // at most 256 lanes x 4 units; the router loops over any width
+    // at most 256 lanes x 4 units; the router loops over any width (its LDS token tiles serve
+    // widths up to 5120, wider layers take its register path)
     if (d->hidden > kMaxWidth || d->inter > kMaxWidth || d->shared_inter > kMaxWidth)
         return fail(BRX_EINVAL, "hidden %d, inter %d and shared_inter %d must be at most %d", d->hidden,
                     d->inter, d->shared_inter, kMaxWidth);

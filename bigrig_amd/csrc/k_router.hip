@@ -17,6 +17,7 @@ namespace {
 
 constexpr int kRouterThreads = 256;
 constexpr int kSmallT = 64;  // up to this many tokens: one wave per (row, 4 tokens); above: token tiles
+constexpr size_t kMaxBlockLds = 160 * 1024;   // LDS one gfx950 block may allocate
 
 // ---------------------------------------------------------------- many tokens
 // k_router_tiled: a block takes a tile of TT tokens (staged in LDS as bf16) and a group of
@@ -333,7 +334,10 @@ hipError_t launch_router(const brx_layer_desc& d, const void* x, const void* w_r
                          float* out_w, float* out_sg, float* ws_logits, hipStream_t s) {
     if (T <= 0) return hipSuccess;
     const bool f32 = d.router_dtype == BRX_DT_F32;
-    if (T <= kSmallT) {
+    // the tiled kernel stages 16 token rows of x in LDS, 32 * H bytes: within a block's 160 KB up
+    // to H = 5120. Wider layers route every token tile with the small-T kernel (the same per-lane
+    // chains and butterfly, so the same bits).
+    if (T <= kSmallT || (size_t)32 * d.hidden > kMaxBlockLds) {
         hipError_t e = launch_router_logits(d, x, w_router, bias, sgw, T, ws_logits, s);
         if (e != hipSuccess) return e;
         return topk_launch(d, T, sgw ? 1 : 0, ws_logits, bias, out_idx, out_w, out_sg, s);

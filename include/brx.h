@@ -130,7 +130,11 @@ int brx_pool_destroy(brx_pool* p);
 int brx_pool_capacity(const brx_pool* p);
 /* Device address of slot `slot` (the expert's bytes, blob layout). */
 int brx_pool_slot_ptr(brx_pool* p, int slot, void** out);
-/* Device address of the int32 expert->slot table [n_experts] kernels read. */
+/* Device address of the int32 expert->slot table [n_experts] kernels read. The table is
+ * read-only for the caller: change it only through brx_pool_set_g2s (or, on a host-backed pool,
+ * brx_pool_publish_async / brx_pool_admit_async). The pool's count of resident entries, which
+ * brx_moe_block_forward checks before it launches anything, follows those calls only; a table
+ * edited through this pointer leaves it stale. */
 int brx_pool_g2s_ptr(brx_pool* p, int32_t** out);
 
 /* Copy one expert's packed bytes from pinned host memory into slot `slot`, asynchronously on

@@ -26,23 +26,36 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(BUILD, "liboracle.so")
 SRC = os.path.join(HERE, "moe_oracle.c")
+# the CPU baseline bench.py times (not the oracle: see cpu_baseline.c)
+CPB_LIB = os.path.join(BUILD, "libcpu_baseline.so")
+CPB_SRC = os.path.join(HERE, "cpu_baseline.c")
 
 _lib = None
+_cpb = None
+
+
+def _gcc(src: str, out: str, flags: list, force: bool) -> str:
+    if not force and os.path.exists(out) and os.path.getmtime(out) >= os.path.getmtime(src):
+        return out
+    tmp = out + ".tmp"
+    cmd = ["gcc", *flags, "-fopenmp", "-fPIC", "-shared", src, "-o", tmp, "-lm"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"build of {os.path.basename(src)} failed:\n{r.stdout}{r.stderr}")
+    os.replace(tmp, out)
+    return out
 
 
 def build(force: bool = True) -> str:
-    """gcc -O3 -fopenmp the C restatement. -ffp-contract=off keeps fmaf() the only fused op."""
+    """gcc -O3 -fopenmp the C restatement (-ffp-contract=off keeps fmaf() the only fused op),
+    and the CPU baseline (vectorized: reassociation allowed, it is timed, not compared bit for
+    bit)."""
     os.makedirs(BUILD, exist_ok=True)
-    if not force and os.path.exists(LIB) and os.path.getmtime(LIB) >= os.path.getmtime(SRC):
-        return LIB
-    tmp = LIB + ".tmp"
-    cmd = ["gcc", "-O3", "-march=x86-64-v3", "-ffp-contract=off", "-fno-fast-math", "-fopenmp",
-           "-fPIC", "-shared", SRC, "-o", tmp, "-lm"]
-    r = subprocess.run(cmd, capture_output=True, text=True)
-    if r.returncode != 0:
-        raise RuntimeError(f"oracle build failed:\n{r.stdout}{r.stderr}")
-    os.replace(tmp, LIB)
-    return LIB
+    # reassociation (vectorized sums) without -ffast-math, whose startup code would switch the
+    # whole process to flush-to-zero when the library loads
+    _gcc(CPB_SRC, CPB_LIB, ["-O3", "-march=x86-64-v3", "-fassociative-math", "-fno-signed-zeros",
+                            "-fno-trapping-math", "-fno-math-errno"], force)
+    return _gcc(SRC, LIB, ["-O3", "-march=x86-64-v3", "-ffp-contract=off", "-fno-fast-math"], force)
 
 
 class OrcLayer(C.Structure):
@@ -161,6 +174,44 @@ def sort_pairs(idx, E: int):
 
 def num_threads() -> int:
     return int(lib().orc_num_threads())
+
+
+# ------------------------------------------------------------------ CPU baseline (timed only)
+def _cpb_lib():
+    global _cpb
+    if _cpb is None:
+        if not os.path.exists(CPB_LIB):
+            build(force=False)
+        _cpb = C.CDLL(CPB_LIB)
+        vp = C.c_void_p
+        _cpb.cpb_decode_layer.argtypes = [vp, vp, vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
+                                          C.c_int, vp, C.c_int64, vp, C.c_int]
+        _cpb.cpb_decode_layer.restype = C.c_int
+    return _cpb
+
+
+def cpu_baseline_decode(spec, x_bits, router_bits, bias, experts_ptr: int, stride: int,
+                        nthreads: int = 0) -> np.ndarray:
+    """One decode token through one layer on the host with cpu_baseline.c (fp32 dequant-on-the-
+    fly GEMVs, OpenMP): out [H] bf16 bits. `experts_ptr` is the host address of the layer's
+    [E, stride] expert bytes. Only 4-bit affine group-64 SwiGLU layers without biases."""
+    q = spec.quant
+    if (q.mode != "affine" or q.bits != 4 or q.group_size != 64 or spec.has_bias or
+            spec.act != "swiglu" or spec.route_mode not in (0, 1) or
+            spec.router_dtype != "bfloat16"):
+        raise ValueError("the CPU baseline runs 4-bit affine g64 SwiGLU layers with a bf16 "
+                         "softmax router only")
+    x = np.ascontiguousarray(x_bits, dtype=np.uint16).reshape(-1)
+    wr = np.ascontiguousarray(router_bits, dtype=np.uint16)
+    b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+    out = np.zeros(spec.hidden, np.uint16)
+    rc = _cpb_lib().cpb_decode_layer(_p(x), _p(wr), _p(b), spec.hidden, spec.inter,
+                                     spec.n_experts, spec.top_k, int(spec.route_mode == 1),
+                                     int(q.scale_dtype == "float16"), experts_ptr, stride,
+                                     _p(out), nthreads)
+    if rc != 0:
+        raise ValueError("cpb_decode_layer rejected its arguments")
+    return out
 
 
 # ------------------------------------------------------------------ float64 truth (numpy)

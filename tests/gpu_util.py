@@ -48,3 +48,36 @@ def build_gpu_layer(layer, dev, capacity: int | None = None, warm: bool = True, 
     sgw = None if layer.sgate_w is None else to_dev_bits(layer.sgate_w, dev)
     moe = MoELayer(spec, router, sw, router_bias=bias, shared_gate_w=sgw)
     return moe, sw, pool, store
+
+
+def tile_edge_tokens(idx: np.ndarray, n_experts: int, block: int = 64) -> list[int]:
+    """Tokens to compare a prefill chunk on: for every expert the chunk hits, the tokens of the
+    first and last row of each `block`-row run of its bucket (its pairs in pair order t * k + j,
+    the stable order the bucketing keeps), and of the bucket's last row.
+
+    The grouped GEMM cuts each bucket into M tiles that start at multiples of 64 rows, so with
+    block = 64 every tile's first and last row, of every expert, is among the compared rows:
+    a tile variant or an expert whose rows go wrong cannot hide between sampled tokens."""
+    T, k = idx.shape
+    flat = np.asarray(idx).reshape(-1)
+    toks = set()
+    for e in range(n_experts):
+        p = np.flatnonzero(flat == e)
+        n = len(p)
+        if n == 0:
+            continue
+        rows = {n - 1}
+        for r0 in range(0, n, block):
+            rows.add(r0)
+            rows.add(min(r0 + block - 1, n - 1))
+        toks.update(int(p[r]) // k for r in rows)
+    return sorted(toks)
+
+
+def per_token_rel_l2(got: np.ndarray, want: np.ndarray) -> np.ndarray:
+    """Relative L2 error of each row (token) of got against want."""
+    g = np.asarray(got, np.float64)
+    w = np.asarray(want, np.float64)
+    num = np.sqrt(((g - w) ** 2).sum(-1))
+    den = np.sqrt((w ** 2).sum(-1))
+    return num / np.maximum(den, 1e-30)

@@ -142,15 +142,18 @@ def test_top_k_16_block(gpu, T):
     pool.close()
 
 
-@pytest.mark.parametrize("T", [1, 8, 40, 80])
-def test_hidden_4096(gpu, T):
-    """Two router passes per lane (4096 > 3072): routing bit-exact, layer within tolerance."""
+@pytest.mark.parametrize("H,T", [(4096, 1), (4096, 8), (4096, 40), (4096, 80), (8192, 1), (8192, 8),
+                                 (8192, 80)])
+def test_wide_hidden(gpu, H, T):
+    """Several router passes per lane (4096 and 8192 > 3072): routing bit-exact, layer within
+    tolerance. At 8192 the prefill router's LDS token tiles (32 H bytes) would exceed a block's
+    160 KB, so its token tiles take the register path; the decode kernels stage 8 rows of 8192."""
     import torch
-    spec = small(QWEN3_30B_A3B, hidden=4096, inter=256, n_experts=16, top_k=4)
+    spec = small(QWEN3_30B_A3B, hidden=H, inter=256, n_experts=16, top_k=4)
     lay = make_layer(spec, seed=404, zipf=0.5)
     moe, sw, pool, _ = build_gpu_layer(lay, gpu)
     x = make_x(T, spec.hidden, seed=4040 + T)
-    print(f"[abi] hidden 4096 T={T}", flush=True)
+    print(f"[abi] hidden {H} T={T}", flush=True)
     gidx, gw, _ = moe.route(to_dev_bits(x, gpu))
     out = moe(to_dev_bits(x, gpu))
     torch.cuda.synchronize()
