@@ -8,9 +8,8 @@ The library is one hipcc invocation over every `csrc/*.hip` file. Packed FP32 in
 disabled for device code (`-Xclang -target-feature -Xclang -packed-fp32-ops`); the host pass
 warns that it does not know that feature, which is harmless. MFMA accumulators are allocated in
 ordinary VGPRs (`-mllvm -amdgpu-mfma-vgpr-form=1`): with them in AGPRs the register allocator
-rotated the 128-row prefill GEMM's accumulators between loop iterations, costing ~190 register
-copies per K step. The sources in AGPR_SOURCES hold more accumulators than VGPRs can and are
-built without that option.
+rotated the prefill GEMM's accumulators between loop iterations, costing ~190 register copies
+per K step.
 """
 from __future__ import annotations
 
@@ -48,11 +47,6 @@ def _run(cmd, verbose: bool, what: str) -> None:
         print(out)
 
 
-# Sources whose MFMA accumulators do not fit in ordinary VGPRs (256-row GEMM tiles: 256
-# accumulators a lane): built without the VGPR-form option, so they live in AGPRs.
-AGPR_SOURCES = {"k_pf_big.hip"}
-
-
 def build(verbose: bool = False, incremental: bool = False) -> str:
     """Compile every csrc/*.hip to an object in parallel (each file carries its own device code
     object; kernels are only launched from the file that defines them), then link. With
@@ -63,10 +57,10 @@ def build(verbose: bool = False, incremental: bool = False) -> str:
         raise RuntimeError(f"no HIP sources under {CSRC}")
     objdir = os.path.join(PKG, "_build")
     os.makedirs(objdir, exist_ok=True)
-    base = [f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
-            "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-            "-Wno-unused-command-line-argument", "-I", INCLUDE, "-I", CSRC]
-    vgpr_form = ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]
+    flags = [f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
+             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+             "-mllvm", "-amdgpu-mfma-vgpr-form=1",
+             "-Wno-unused-command-line-argument", "-I", INCLUDE, "-I", CSRC]
     objs = [os.path.join(objdir, os.path.basename(s)[:-4] + ".o") for s in srcs]
     headers = glob.glob(os.path.join(CSRC, "*.h")) + glob.glob(os.path.join(INCLUDE, "*.h"))
     newest_h = max((os.path.getmtime(h) for h in headers), default=0.0)
@@ -77,9 +71,7 @@ def build(verbose: bool = False, incremental: bool = False) -> str:
 
     jobs = min(len(srcs), max(1, min(16, os.cpu_count() or 1)))
     with ThreadPoolExecutor(jobs) as ex:
-        futs = [ex.submit(_run, [hipcc(), *base,
-                                 *([] if os.path.basename(s) in AGPR_SOURCES else vgpr_form),
-                                 "-c", s, "-o", o], verbose, f"hipcc {s}")
+        futs = [ex.submit(_run, [hipcc(), *flags, "-c", s, "-o", o], verbose, f"hipcc {s}")
                 for s, o in zip(srcs, objs) if stale(s, o)]
         for f in futs:
             f.result()

@@ -343,6 +343,133 @@ __device__ __forceinline__ bf16x8_t dq8(uint32_t w, float s24, float b, float sc
     return __builtin_bit_cast(bf16x8_t, u32x4_t{o[0], o[1], o[2], o[3]});
 }
 
+// The activation of one output element with the rule fixed at compile time (act_apply's
+// arithmetic for that rule, so the same bits).
+template <int ACT>
+__device__ __forceinline__ float act_fixed(float g, float u, float alpha, float limit) {
+    if constexpr (ACT == BRX_ACT_SWIGLU) return silu_mul(g, u);
+    else if constexpr (ACT == BRX_ACT_SILU_MLP) return x_sigmoid(g, 1.0f);
+    else {
+        g = fminf(g, limit);
+        u = fminf(fmaxf(u, -limit), limit);
+        return x_sigmoid(g, alpha) * (u + 1.0f);
+    }
+}
+
+// The gate/up epilogue of one activation rule: act(gate + bias, up + bias) (or SiLU(fc1 + bias))
+// of every accumulator into the LDS tile T (row stride TS elements), NaN for an absent expert.
+// A gated tile's wave holds 32 features: fragment 0 their gate rows, fragment 1 their up rows;
+// a two-layer expert's fragment nj holds 32 fc1 features of its own. Element i of a 32 x 32
+// fragment is row 8 (i / 4) + 4 kh + i % 4, column l32.
+template <int MR, int ACT>
+__device__ __forceinline__ void pf_store_h(const FwdArgs& a, const Layout& L, const uint8_t* base, int inter,
+                                           bool absent, int nt, const f32x16_t (&acc)[MR][kNJ], uint16_t* T,
+                                           int wv, int kh, int l32) {
+    const float nan = absent_nan();
+    if constexpr (ACT == BRX_ACT_SILU_MLP) {
+        constexpr int TS = kBlockN + 8;
+#pragma unroll
+        for (int nj = 0; nj < kNJ; ++nj) {
+            const int fl = nj * 128 + wv * 32 + l32;
+            const int f = min(nt * kBlockN + fl, inter - 1);
+            const float bg = L.p[0].bias >= 0 ? bf2f(reinterpret_cast<const uint16_t*>(base + L.p[0].bias)[f]) : 0.f;
+#pragma unroll
+            for (int mi = 0; mi < MR; ++mi) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    float h = act_fixed<ACT>(acc[mi][nj][i] + bg, 0.f, a.alpha, a.limit);
+                    h = absent ? nan : h;
+                    T[(mi * 32 + 8 * (i >> 2) + 4 * kh + (i & 3)) * TS + fl] = __builtin_bit_cast(uint16_t, (__bf16)h);
+                }
+            }
+        }
+    } else {
+        constexpr int TS = kBlockN / 2 + 8;
+        const int fl = wv * (kWaveN / 2) + l32;
+        const int f = min(nt * (kBlockN / 2) + fl, inter - 1);
+        float bg = 0.f, bu = 0.f;
+        if (L.p[0].bias >= 0) {
+            bg = bf2f(reinterpret_cast<const uint16_t*>(base + L.p[0].bias)[f]);
+            bu = bf2f(reinterpret_cast<const uint16_t*>(base + L.p[1].bias)[f]);
+        }
+#pragma unroll
+        for (int mi = 0; mi < MR; ++mi) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                float h = act_fixed<ACT>(acc[mi][0][i] + bg, acc[mi][1][i] + bu, a.alpha, a.limit);
+                h = absent ? nan : h;
+                T[(mi * 32 + 8 * (i >> 2) + 4 * kh + (i & 3)) * TS + fl] = __builtin_bit_cast(uint16_t, (__bf16)h);
+            }
+        }
+    }
+}
+
+// The epilogue of a GEMM tile: MR x kNJ fragments of fp32 accumulators per wave go through LDS
+// (`ring`, free once the caller has waited for every copy into it and synchronised) so the
+// global stores are 16-byte chunks of contiguous row segments. KIND 0: the activation (one code
+// path per rule, chosen once per tile) stored as bf16 h rows at their bucketed positions; KIND 1:
+// + bias, each pair's row stored at its (token, k) position (dst_s). An absent expert's h rows
+// are NaN.
+template <int KIND, int MR>
+__device__ __forceinline__ void pf_store(const FwdArgs& a, const Layout& L, const uint8_t* base, bool mlp, int inter,
+                                         int slot, int nt, int m0, int rows, const f32x16_t (&acc)[MR][kNJ],
+                                         uint8_t* ring, const int32_t* dst_s, uint16_t* __restrict__ hbuf,
+                                         int hstride, uint16_t* __restrict__ y_routed,
+                                         uint16_t* __restrict__ y_shared) {
+    constexpr int MF = MR * 2;
+    const int H = a.H;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int kh = lane >> 5, l32 = lane & 31;
+    uint16_t* T = reinterpret_cast<uint16_t*>(ring);
+    if constexpr (KIND == 0) {
+        const bool absent = slot == kAbsentCode;
+        if (mlp)
+            pf_store_h<MR, BRX_ACT_SILU_MLP>(a, L, base, inter, absent, nt, acc, T, wv, kh, l32);
+        else if (a.act == BRX_ACT_SWIGLU_CLAMPED)
+            pf_store_h<MR, BRX_ACT_SWIGLU_CLAMPED>(a, L, base, inter, absent, nt, acc, T, wv, kh, l32);
+        else
+            pf_store_h<MR, BRX_ACT_SWIGLU>(a, L, base, inter, absent, nt, acc, T, wv, kh, l32);
+        lds_barrier();
+        // a two-layer expert's tile holds kBlockN features, a gated one's kBlockN / 2
+        const int fpb = mlp ? kBlockN : kBlockN / 2;
+        const int TS = fpb + 8;
+        const int CH = fpb / 8;
+        for (int c = tid; c < MF * 16 * CH; c += kGemmThreads) {
+            const int r = c / CH, f0 = nt * fpb + (c % CH) * 8;
+            if (r < rows && f0 < inter)
+                *reinterpret_cast<u32x4_t*>(hbuf + (int64_t)(m0 + r) * hstride + f0) =
+                    *reinterpret_cast<const u32x4_t*>(T + r * TS + (c % CH) * 8);
+        }
+    } else {
+        constexpr int TS = kBlockN + 8;
+        constexpr int CH = kBlockN / 8;
+#pragma unroll
+        for (int nj = 0; nj < kNJ; ++nj) {
+            const int nl = wv * kWaveN + nj * 32 + l32;
+            float bd = 0.f;
+            if (L.p[2].bias >= 0)
+                bd = bf2f(reinterpret_cast<const uint16_t*>(base + L.p[2].bias)[min(nt * kBlockN + nl, H - 1)]);
+#pragma unroll
+            for (int mi = 0; mi < MR; ++mi) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i)
+                    T[(mi * 32 + 8 * (i >> 2) + 4 * kh + (i & 3)) * TS + nl] =
+                        __builtin_bit_cast(uint16_t, (__bf16)(acc[mi][nj][i] + bd));
+            }
+        }
+        lds_barrier();
+        for (int c = tid; c < MF * 16 * CH; c += kGemmThreads) {
+            const int r = c / CH, n0 = nt * kBlockN + (c % CH) * 8;
+            if (r < rows && n0 < H) {
+                const int d = dst_s[r];
+                uint16_t* dst = d >= 0 ? y_routed + (int64_t)d * H + n0 : y_shared + (int64_t)(-2 - d) * H + n0;
+                *reinterpret_cast<u32x4_t*>(dst) = *reinterpret_cast<const u32x4_t*>(T + r * TS + (c % CH) * 8);
+            }
+        }
+    }
+}
+
 template <int MODE, bool F16, int KIND, int MF>
 __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restrict__ order,
                                         uint16_t* __restrict__ hbuf, int hstride,
@@ -563,9 +690,14 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
     // prologue: stages 0 .. NS - 2 in flight; wait for stages 0 and 1; B(0) kk 0 dequantized.
     // The B registers rotate through NS sets: stage t's words sit in set t % NS, so the loop
     // is unrolled NS times to keep every set index a constant.
+    // (the empty asm with a memory clobber keeps each stage's copies into LDS after the previous
+    // stage's: the wait counts them in issue order and the compiler cannot see their targets)
     BReg bq[NS];
 #pragma unroll
-    for (int t = 0; t < NS - 1; ++t) issue(t, bq[t]);
+    for (int t = 0; t < NS - 1; ++t) {
+        issue(t, bq[t]);
+        asm volatile("" ::: "memory");
+    }
     dma_wait_barrier<loads_after(NS, NV0, NV1, 0)>();
     bf16x8_t bop0[kNJ], bop1[kNJ];
     bf16x8_t a0[MR], a1[MR];
@@ -613,90 +745,8 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
     // landed and every wave is done reading it) so that the global stores are 16-byte chunks
     // of contiguous row segments
     dma_wait_barrier<0>();
-    uint16_t* T = reinterpret_cast<uint16_t*>(ring);
-    if (mlp) {
-        // 256 fc1 features: fragment nj holds features 128 nj + 32 wv + l32 of the block
-        constexpr int TS = kBlockN + 8;
-        constexpr int CH = kBlockN / 8;
-#pragma unroll
-        for (int nj = 0; nj < kNJ; ++nj) {
-            const int fl = nj * 128 + wv * 32 + l32;
-            const int f = min(nt * kBlockN + fl, inter - 1);
-            const float bg = L.p[0].bias >= 0 ? bf2f(reinterpret_cast<const uint16_t*>(base + L.p[0].bias)[f]) : 0.f;
-#pragma unroll
-            for (int mi = 0; mi < MR; ++mi) {
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const float h = slot == kAbsentCode ? absent_nan()
-                                                        : act_apply(a.act, acc[mi][nj][i] + bg, 0.f, a.alpha, a.limit);
-                    T[(mi * 32 + 8 * (i >> 2) + 4 * kh + (i & 3)) * TS + fl] = __builtin_bit_cast(uint16_t, (__bf16)h);
-                }
-            }
-        }
-        lds_barrier();
-        for (int c = tid; c < MF * 16 * CH; c += kGemmThreads) {
-            const int r = c / CH, f0 = nt * kBlockN + (c % CH) * 8;
-            if (r < rows && f0 < inter)
-                *reinterpret_cast<u32x4_t*>(hbuf + (int64_t)(m0 + r) * hstride + f0) =
-                    *reinterpret_cast<const u32x4_t*>(T + r * TS + (c % CH) * 8);
-        }
-    } else if constexpr (KIND == 0) {
-        constexpr int TS = kBlockN / 2 + 8;                // LDS row stride (elements)
-        constexpr int CH = kBlockN / 2 / 8;                // 16-byte chunks per row
-        // fragment 0 holds gate, fragment 1 the up rows of the same 32 features; element i of
-        // a 32 x 32 fragment is row 8 (i / 4) + 4 kh + i % 4, column l32
-        {
-            const int fl = wv * (kWaveN / 2) + l32;
-            const int f = min(nt * (kBlockN / 2) + fl, inter - 1);
-            float bg = 0.f, bu = 0.f;
-            if (L.p[0].bias >= 0) {
-                bg = bf2f(reinterpret_cast<const uint16_t*>(base + L.p[0].bias)[f]);
-                bu = bf2f(reinterpret_cast<const uint16_t*>(base + L.p[1].bias)[f]);
-            }
-#pragma unroll
-            for (int mi = 0; mi < MR; ++mi) {
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const float h = slot == kAbsentCode
-                        ? absent_nan() : act_apply(a.act, acc[mi][0][i] + bg, acc[mi][1][i] + bu, a.alpha, a.limit);
-                    T[(mi * 32 + 8 * (i >> 2) + 4 * kh + (i & 3)) * TS + fl] = __builtin_bit_cast(uint16_t, (__bf16)h);
-                }
-            }
-        }
-        lds_barrier();
-        for (int c = tid; c < MF * 16 * CH; c += kGemmThreads) {
-            const int r = c / CH, f0 = nt * (kBlockN / 2) + (c % CH) * 8;
-            if (r < rows && f0 < inter)
-                *reinterpret_cast<u32x4_t*>(hbuf + (int64_t)(m0 + r) * hstride + f0) =
-                    *reinterpret_cast<const u32x4_t*>(T + r * TS + (c % CH) * 8);
-        }
-    } else {
-        constexpr int TS = kBlockN + 8;
-        constexpr int CH = kBlockN / 8;
-#pragma unroll
-        for (int nj = 0; nj < kNJ; ++nj) {
-            const int nl = wv * kWaveN + nj * 32 + l32;
-            float bd = 0.f;
-            if (L.p[2].bias >= 0)
-                bd = bf2f(reinterpret_cast<const uint16_t*>(base + L.p[2].bias)[min(nt * kBlockN + nl, H - 1)]);
-#pragma unroll
-            for (int mi = 0; mi < MR; ++mi) {
-#pragma unroll
-                for (int i = 0; i < 16; ++i)
-                    T[(mi * 32 + 8 * (i >> 2) + 4 * kh + (i & 3)) * TS + nl] =
-                        __builtin_bit_cast(uint16_t, (__bf16)(acc[mi][nj][i] + bd));
-            }
-        }
-        lds_barrier();
-        for (int c = tid; c < MF * 16 * CH; c += kGemmThreads) {
-            const int r = c / CH, n0 = nt * kBlockN + (c % CH) * 8;
-            if (r < rows && n0 < H) {
-                const int d = dst_s[r];
-                uint16_t* dst = d >= 0 ? y_routed + (int64_t)d * H + n0 : y_shared + (int64_t)(-2 - d) * H + n0;
-                *reinterpret_cast<u32x4_t*>(dst) = *reinterpret_cast<const u32x4_t*>(T + r * TS + (c % CH) * 8);
-            }
-        }
-    }
+    pf_store<KIND, MR>(a, L, base, mlp, inter, slot, nt, m0, rows, acc, ring, dst_s, hbuf, hstride, y_routed,
+                       y_shared);
 }
 
 template <int MODE, bool F16, int KIND>
