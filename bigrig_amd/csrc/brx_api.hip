@@ -68,9 +68,15 @@ int check_desc(const brx_layer_desc* d) {
     if (d->top_k < 1 || d->top_k > d->n_experts || d->top_k > 64)
         return fail(BRX_EINVAL, "top_k %d outside [1, min(n_experts, 64)]", d->top_k);
     if (d->quant_mode == BRX_QUANT_AFFINE) {
-        if ((d->bits != 4 && d->bits != 3) || d->group_size != 64)
-            return fail(BRX_EINVAL, "affine kernels take 4- or 3-bit weights in groups of 64 (got %d-bit g%d)",
-                        d->bits, d->group_size);
+        // the reference's per-layer precision candidates (bigrig_engine/precision.py:58): 2, 3 and
+        // 4 bits in groups of 64 or 128, 6 and 8 bits in groups of 64 (MLX also writes 6- and 8-bit
+        // g128, which the kernels take as well)
+        if (kernel_mode(BRX_QUANT_AFFINE, d->bits) < 0 || (d->group_size != 64 && d->group_size != 128))
+            return fail(BRX_EINVAL, "affine kernels take 2-, 3-, 4-, 6- or 8-bit weights in groups of 64 or 128 "
+                        "(got %d-bit g%d)", d->bits, d->group_size);
+        if (d->hidden % d->group_size || d->inter % d->group_size || d->shared_inter % d->group_size)
+            return fail(BRX_EINVAL, "hidden %d, inter %d and shared_inter %d must be multiples of the group size %d",
+                        d->hidden, d->inter, d->shared_inter, d->group_size);
         if (d->scale_dtype != BRX_SCALE_BF16 && d->scale_dtype != BRX_SCALE_F16)
             return fail(BRX_EINVAL, "scale_dtype %d unknown", d->scale_dtype);
     } else if (d->quant_mode == BRX_QUANT_MXFP4) {
@@ -485,7 +491,8 @@ static FwdArgs make_args(const brx_layer_desc* d, brx_pool* p, const void* x, in
     a.lay_sh = d->shared_inter ? make_layout(*d, d->shared_inter) : p->lay;
     a.T = T; a.H = d->hidden; a.I = d->inter; a.I_sh = shared_expert ? d->shared_inter : 0;
     a.E = d->n_experts; a.k = d->top_k;
-    a.quant_mode = (d->quant_mode == BRX_QUANT_AFFINE && d->bits == 3) ? kModeAffine3 : d->quant_mode;
+    a.quant_mode = kernel_mode(d->quant_mode, d->bits);
+    a.gshift = d->quant_mode == BRX_QUANT_AFFINE && d->group_size == 128 ? 1 : 0;
     a.scale_f16 = d->scale_dtype == BRX_SCALE_F16; a.has_bias = d->has_bias;
     a.act = d->act; a.alpha = d->alpha; a.limit = d->limit;
     a.out = (uint16_t*)out;

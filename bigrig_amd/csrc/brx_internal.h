@@ -12,24 +12,32 @@ constexpr int kWave = 64;
 constexpr int kMaxTableEdits = 32;   // table entries one brx_pool_publish_async launch sets
 constexpr int kMaxWidth = 8192;      // largest hidden / intermediate width the kernels take
 
-// Kernel weight modes: the public quant modes, plus 3-bit affine (BRX_QUANT_AFFINE with 3 bits:
-// a group of 64 codes is 24 bytes, 8 codes per 3 bytes, least significant bits first).
+// Kernel weight modes: MXFP4, and one mode per affine code width (4-bit affine keeps the public
+// BRX_QUANT_AFFINE value). Every affine width stores a row as one continuous stream of codes,
+// least significant bits first (code k at bits [bits k, bits k + bits) of the row's bytes), so
+// 64 codes -- a decode unit, a 64-K prefill stage -- are 8 * bits bytes, and a run of 8 codes
+// (a "piece") is `bits` bytes. Scale groups hold 64 or 128 codes (gshift 0 or 1).
+constexpr int kModeAffine4 = BRX_QUANT_AFFINE;
 constexpr int kModeAffine3 = 2;
+constexpr int kModeAffine2 = 3;
+constexpr int kModeAffine6 = 4;
+constexpr int kModeAffine8 = 5;
 template <int MODE>
-constexpr bool kAffine = MODE != BRX_QUANT_MXFP4;   // scale + bias per group of 64
+constexpr bool kAffine = MODE != BRX_QUANT_MXFP4;   // scale + bias per group
+template <int MODE>
+constexpr int kBits = MODE == kModeAffine2 ? 2 : MODE == kModeAffine3 ? 3 : MODE == kModeAffine6 ? 6
+                    : MODE == kModeAffine8 ? 8 : 4;
 
-// The 24 bits of 3-byte group m (codes 8m .. 8m + 7) of a 3-bit affine group held in six
-// little-endian words (only the low 24 bits of the result are meaningful).
-__device__ __forceinline__ uint32_t group24(const uint32_t w[6], int m) {
-    switch (m & 7) {
-        case 0: return w[0];
-        case 1: return __builtin_amdgcn_alignbit(w[1], w[0], 24);
-        case 2: return __builtin_amdgcn_alignbit(w[2], w[1], 16);
-        case 3: return w[2] >> 8;
-        case 4: return w[3];
-        case 5: return __builtin_amdgcn_alignbit(w[4], w[3], 24);
-        case 6: return __builtin_amdgcn_alignbit(w[5], w[4], 16);
-        default: return w[5] >> 8;
+// The kernel mode of a descriptor's quantization (-1: none takes it).
+inline int kernel_mode(int quant_mode, int bits) {
+    if (quant_mode == BRX_QUANT_MXFP4) return bits == 4 ? BRX_QUANT_MXFP4 : -1;
+    switch (bits) {
+        case 2: return kModeAffine2;
+        case 3: return kModeAffine3;
+        case 4: return kModeAffine4;
+        case 6: return kModeAffine6;
+        case 8: return kModeAffine8;
+        default: return -1;
     }
 }
 
@@ -38,6 +46,37 @@ __device__ __forceinline__ uint32_t pair3(uint32_t g, int i) {
     const uint32_t t = g >> (3 * i);
     return (t & 0x7u) | ((t << 4) & 0x70000u);
 }
+
+// Codes 8m + i (low 16 bits) and 8m + i + 4 (high 16 bits) of piece m of a run of little-endian
+// words `w` holding whole pieces of BITS-bit codes (i < 4; m and i compile-time after
+// unrolling). Two codes a 32-bit value, so one AND/OR turns both into operands.
+__device__ __forceinline__ uint32_t bits_at(const uint32_t* w, int b, int n) {
+    // n <= 24 bits starting at bit b of `w` (in the low bits; the rest is garbage)
+    const int wi = b >> 5, sh = b & 31;
+    return sh + n <= 32 ? w[wi] >> sh : __builtin_amdgcn_alignbit(w[wi + 1], w[wi], sh);
+}
+template <int BITS>
+__device__ __forceinline__ uint32_t piece_pair(const uint32_t* w, int m, int i) {
+    if constexpr (BITS == 4) {
+        return (w[m] >> (4 * i)) & 0x000F000Fu;
+    } else if constexpr (BITS == 3) {
+        return pair3(bits_at(w, 24 * m, 24), i);
+    } else if constexpr (BITS == 2) {
+        // the piece is 16 bits: its low byte holds codes 0..3, its high byte codes 4..7
+        const uint32_t v = w[m >> 1] >> (16 * (m & 1));
+        const uint32_t sp = (v & 0xFFu) | ((v & 0xFF00u) << 8);
+        return (sp >> (2 * i)) & 0x00030003u;
+    } else if constexpr (BITS == 8) {
+        // byte i of each of the piece's two words
+        return ((w[2 * m] >> (8 * i)) & 0xFFu) | (((w[2 * m + 1] >> (8 * i)) & 0xFFu) << 16);
+    } else {
+        static_assert(BITS == 6, "affine widths are 2, 3, 4, 6 and 8 bits");
+        // codes 0..3 and 4..7 of the piece as two runs of 24 bits
+        const uint32_t lo = bits_at(w, 48 * m, 24), hi = bits_at(w, 48 * m + 24, 24);
+        return ((lo >> (6 * i)) & 0x3Fu) | (((hi >> (6 * i)) & 0x3Fu) << 16);
+    }
+}
+
 
 // ------------------------------------------------------------------ layout (host + device)
 struct Proj {
@@ -116,10 +155,11 @@ struct FwdArgs {
     int32_t capacity;
     int32_t auto_shared;        // token mode: every token also runs the shared expert
     int32_t T, H, I, I_sh, E, k;
-    int32_t quant_mode, scale_f16, has_bias, act;   // quant_mode: a kernel mode (kModeAffine3 for 3 bits)
+    int32_t quant_mode, scale_f16, has_bias, act;   // quant_mode: a kernel mode (kModeAffine*, MXFP4)
     float alpha, limit;
     int32_t yrows;              // rows of yun
-    int16_t route_mode;
+    int8_t route_mode;
+    int8_t gshift;              // affine scale groups of 64 << gshift codes (0 or 1)
     uint8_t n_group, topk_group;   // group-limited routing (1, 1: none); at most 64
     float route_scale;          // multiplies every routing weight
 };
@@ -557,26 +597,25 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
-// sum_{i} (128 + q_i) * x_i over the 8 codes of a 3-byte group `g` (3-bit affine), with the
-// activations paired as for dot8_q4.
-__device__ __forceinline__ float dot8_q3(uint32_t g, const uint32_t* xp, float acc) {
+// sum_i c_i x_i over the 8 codes of piece m of `w` (BITS-bit affine), accumulated into acc.
+// xp[i] packs (x_i, x_{i+4}) as bf16x2. Below 8 bits c = 128 + q: the code pair of piece_pair
+// OR'd with 0x43004300 is the bf16 pair (128 + q_i, 128 + q_{i+4}) exactly (q < 128 fills the 7
+// mantissa bits of 128). 8-bit codes do not fit there and take c = q: each code is converted to
+// fp32 (exact) and its upper half kept, exact in bf16 since q has at most 8 significant bits.
+template <int BITS>
+constexpr float kCodeOffset = BITS == 8 ? 0.0f : 128.0f;
+template <int BITS>
+__device__ __forceinline__ float dot8(const uint32_t* w, int m, const uint32_t* xp, float acc) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const uint32_t qp = pair3(g, i) | 0x43004300u;
-        acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, qp),
-                                              __builtin_bit_cast(bf16x2_t, xp[i]), acc, false);
-    }
-    return acc;
-}
-
-// sum_{i} (128 + q_i) * x_i over the 8 nibbles of `wd`, accumulated into acc.
-// xp[i] packs (x_{i}, x_{i+4}) as bf16x2: nibble i and nibble i+4 of the word land in the
-// low and high halves of ((wd >> 4i) & 0x000F000F) | 0x43004300, which is the bf16 pair
-// (128 + q_i, 128 + q_{i+4}) exactly.
-__device__ __forceinline__ float dot8_q4(uint32_t wd, const uint32_t* xp, float acc) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        uint32_t qp = ((wd >> (4 * i)) & 0x000F000Fu) | 0x43004300u;
+        uint32_t qp;
+        if constexpr (BITS == 8) {
+            const float c0 = (float)((w[2 * m] >> (8 * i)) & 0xFFu);
+            const float c1 = (float)((w[2 * m + 1] >> (8 * i)) & 0xFFu);
+            qp = (__float_as_uint(c0) >> 16) | (__float_as_uint(c1) & 0xFFFF0000u);
+        } else {
+            qp = piece_pair<BITS>(w, m, i) | 0x43004300u;
+        }
         acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, qp),
                                               __builtin_bit_cast(bf16x2_t, xp[i]), acc, false);
     }
@@ -584,7 +623,7 @@ __device__ __forceinline__ float dot8_q4(uint32_t wd, const uint32_t* xp, float 
 }
 
 // Permute 8 natural-order bf16 (4 words: (x0,x1),(x2,x3),(x4,x5),(x6,x7)) into the pair
-// order dot8_q4 expects: (x0,x4),(x1,x5),(x2,x6),(x3,x7).
+// order dot8 expects: (x0,x4),(x1,x5),(x2,x6),(x3,x7).
 __device__ __forceinline__ void perm8(const uint32_t in[4], uint32_t out[4]) {
     out[0] = (in[0] & 0xFFFFu) | (in[2] << 16);
     out[1] = (in[0] >> 16) | (in[2] & 0xFFFF0000u);
@@ -620,6 +659,7 @@ struct TableEdits {
 };
 hipError_t launch_table_set(int32_t* g2s, const TableEdits& ed, hipStream_t s);
 hipError_t launch_decode(const FwdArgs& a, void* ws, int phases, hipStream_t s);
+hipError_t launch_decode_wide(const FwdArgs& a, void* ws, int phases, hipStream_t s);   // 2, 6, 8 bits
 hipError_t launch_prefill(const FwdArgs& a, void* ws, size_t ws_bytes, int phases, hipStream_t s);
 size_t prefill_workspace_bytes(const FwdArgs& a);
 size_t decode_workspace_bytes(const FwdArgs& a);

@@ -7,10 +7,11 @@ namespace brx {
 namespace {
 
 // Code k of a row sits at bits [bits k, bits k + bits) of the row's bytes, least significant
-// bit first (a 3-bit code may straddle two bytes).
+// bit first (a 3- or 6-bit code may straddle two bytes); affine scale groups hold `group` codes.
 template <int MODE>
 __global__ __launch_bounds__(256) void k_dequant(const uint8_t* __restrict__ base, Proj P,
-                                                 int scale_f16, int bits, float* __restrict__ out) {
+                                                 int scale_f16, int bits, int group,
+                                                 float* __restrict__ out) {
     const int row = blockIdx.x;
     const int n_in = P.n_in;
     const uint8_t* wrow = base + P.w + (int64_t)row * (n_in * bits / 8);
@@ -21,9 +22,9 @@ __global__ __launch_bounds__(256) void k_dequant(const uint8_t* __restrict__ bas
         const uint32_t q = (two >> (bit & 7)) & ((1u << bits) - 1u);
         float v;
         if constexpr (MODE == BRX_QUANT_AFFINE) {
-            const int G = n_in / 64;
-            float s = load_scale(base + P.s, (int64_t)row * G + k / 64, scale_f16);
-            float b = load_scale(base + P.b, (int64_t)row * G + k / 64, scale_f16);
+            const int G = n_in / group;
+            float s = load_scale(base + P.s, (int64_t)row * G + k / group, scale_f16);
+            float b = load_scale(base + P.b, (int64_t)row * G + k / group, scale_f16);
             v = fmaf(s, (float)q, b);
         } else {
             const int G = n_in / 32;
@@ -52,10 +53,10 @@ hipError_t launch_dequant(const brx_layer_desc& d, const Layout& L, const uint8_
     const Proj& P = L.p[proj];
     if (d.quant_mode == BRX_QUANT_AFFINE)
         hipLaunchKernelGGL(k_dequant<BRX_QUANT_AFFINE>, dim3(P.n_out), dim3(256), 0, s, expert, P,
-                           d.scale_dtype == BRX_SCALE_F16 ? 1 : 0, d.bits, out);
+                           d.scale_dtype == BRX_SCALE_F16 ? 1 : 0, d.bits, d.group_size, out);
     else
         hipLaunchKernelGGL(k_dequant<BRX_QUANT_MXFP4>, dim3(P.n_out), dim3(256), 0, s, expert, P, 0,
-                           4, out);
+                           4, 32, out);
     return hipGetLastError();
 }
 

@@ -19,8 +19,9 @@
 //              bucketed order.  KIND 1 (down):
 //              A = h rows, B = down weights of 256 output columns; the epilogue stores each
 //              pair's bf16 row at its (token, k) position.  A is staged through LDS, B is
-//              dequantized from 4-bit straight into MFMA operand registers; fp32 accumulators
-//              (details at the kernel).
+//              dequantized from its packed codes (affine 2-8 bits, MXFP4) straight into MFMA
+//              operand registers; fp32 accumulators (details at the kernel). M tiles are 128
+//              rows (64 for 6- and 8-bit codes).
 //   k_combine  out[t] = sum_j w[t,j] * y[t,j] (+ shared_gate[t] * y_shared[t]), k-ordered.
 // Every output element is one MFMA accumulation over K in a fixed K order, so a row's value
 // does not depend on which other pairs share its tile.
@@ -311,37 +312,50 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint3
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
 }
 
-// Dequantize one 32-bit word (8 weights, natural K order) into a bf16x8 MFMA operand.
+// Dequantize piece kk (8 weights, natural K order) of a lane's words `w` into a bf16x8 MFMA
+// operand.
 //   affine: w = s q + b with one fp32 rounding, then rounded to bf16 (v_cvt_pk_bf16_f32).
-//     Each nibble q is read as the fp16 subnormal q 2^-24 (the nibble alone in a 16-bit half,
-//     exact when widened to fp32) and v_fma_mix_f32 forms fma(q 2^-24, s 2^24, b): the product
-//     is exactly s q, so the result is the same fl(s q + b) as fmaf(s, q, b). `s24` is s 2^24
-//     (exact for any scale below 2^104). A mask of 0x000F000F takes two nibbles at once, so a
-//     word costs 7 extractions, 8 fma_mix and 4 packs. 3-bit codes arrive as a 24-bit group
-//     (8 codes, 3 bits each) and are paired the same way (code i and code 4 + i).
+//     Each code q is read as the fp16 subnormal q 2^-24 (the code alone in a 16-bit half, exact
+//     when widened to fp32: q < 1024) and v_fma_mix_f32 forms fma(q 2^-24, s 2^24, b): the
+//     product is exactly s q, so the result is the same fl(s q + b) as fmaf(s, q, b). `s24` is
+//     s 2^24 (exact for any scale below 2^104). piece_pair puts codes i and 4 + i in the two
+//     halves of one register, so a 4-bit piece costs 7 extractions, 8 fma_mix and 4 packs.
 //   MXFP4: the hardware converts two e2m1 codes with the e8m0 scale, exact in bf16.
 template <int MODE>
-__device__ __forceinline__ bf16x8_t dq8(uint32_t w, float s24, float b, float sc) {
+__device__ __forceinline__ bf16x8_t dq8(const uint32_t* w, int kk, float s24, float b, float sc) {
     uint32_t o[4];
     if constexpr (kAffine<MODE>) {
         float v[8];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             // codes i (low half) and 4 + i (high half)
-            const uint32_t t = MODE == kModeAffine3 ? pair3(w, i) : (w >> (4 * i)) & 0x000F000Fu;
+            const uint32_t t = piece_pair<kBits<MODE>>(w, kk, i);
             v[i] = __builtin_fmaf((float)__builtin_bit_cast(_Float16, (uint16_t)(t & 0xFFFFu)), s24, b);
             v[4 + i] = __builtin_fmaf((float)__builtin_bit_cast(_Float16, (uint16_t)(t >> 16)), s24, b);
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j) o[j] = pk_bf16(v[2 * j], v[2 * j + 1]);
     } else {
-        o[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 0));
-        o[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 1));
-        o[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 2));
-        o[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 3));
+        const uint32_t q = w[kk];
+        o[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q, sc, 0));
+        o[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q, sc, 1));
+        o[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q, sc, 2));
+        o[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q, sc, 3));
     }
     return __builtin_bit_cast(bf16x8_t, u32x4_t{o[0], o[1], o[2], o[3]});
 }
+
+// B words a lane holds per stage (half of a row's 64-code stage segment: 32 codes), and the
+// loads that bring them in (16-byte loads, plus one 8-byte load for 6 bits; one 8- or 12-byte
+// load for 2 and 3 bits).
+template <int MODE>
+constexpr int kBW = kBits<MODE>;
+template <int MODE>
+constexpr int kBLoads = kBits<MODE> >= 6 ? 2 : 1;
+// M tile height: 128 rows, or 64 for 6- and 8-bit codes, whose B words (48 and 64 registers
+// over the ring) leave no room for the accumulators of a 128-row tile at two blocks per CU
+template <int MODE>
+constexpr int kTileRows = kBits<MODE> >= 6 ? 64 : 128;
 
 // The activation of one output element with the rule fixed at compile time (act_apply's
 // arithmetic for that rule, so the same bits).
@@ -482,8 +496,9 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
     constexpr int SS = SA + kStS;                       // stage bytes in the ring
     // loads per wave of an odd stage (A copies, B loads) and of an even stage (+ the scale copies
     // of it and the next stage)
-    constexpr int NV1 = NA + kNJ;
+    constexpr int NV1 = NA + kNJ * kBLoads<MODE>;
     constexpr int NV0 = NV1 + (kAffine<MODE> ? 2 : 1);
+    constexpr int B = kBits<MODE>;
     const bool sh = e >= a.E;
     const int inter = sh ? a.I_sh : a.I;
     const int H = a.H;
@@ -515,10 +530,11 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
         }
     }
     // ---- B: the block's 256 weight rows (KIND 0: gate rows of features nt * 128 + [0, 128),
-    // then the up rows of the same features; KIND 1: down rows nt * 256 + [0, 256)), 32 bytes
-    // of each per stage. A lane loads its own operands straight into registers: the 16-byte
-    // half kh of the stage segment of row brow[nj] (fragment nj, column l32), so one load
-    // instruction reads 32 rows x 32 contiguous bytes. Rows past the matrix repeat its last row.
+    // then the up rows of the same features; KIND 1: down rows nt * 256 + [0, 256)), 8 B bytes
+    // of each per stage (64 codes). A lane loads its own operands straight into registers: the
+    // half kh (4 B bytes) of the stage segment of row brow[nj] (fragment nj, column l32), so one
+    // load instruction reads 32 rows x 8 B contiguous bytes. Rows past the matrix repeat its
+    // last row.
     const __amdgpu_buffer_rsrc_t rb_rsrc = make_rsrc(base, (uint32_t)L.bytes);
     // a two-layer expert (fc1 / fc2): the block's 256 first-projection rows are 256 fc1
     // features, all from matrix 0, instead of 128 gate and the same 128 up features
@@ -533,24 +549,23 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
     for (int nj = 0; nj < kNJ; ++nj) {
         brow[nj] = KIND == 0 ? nj * 128 + wv * 32 + l32 : wv * 64 + nj * 32 + l32;
         const int pj = KIND == 0 ? (mlp ? 0 : nj) : 2;
-        vbw[nj] = MODE == kModeAffine3
-            ? (uint32_t)L.p[pj].w + (uint32_t)mat_row(brow[nj]) * (uint32_t)(K * 3 / 8) + kh * 12
-            : (uint32_t)L.p[pj].w + (uint32_t)mat_row(brow[nj]) * (uint32_t)(K / 2) + kh * 16;
+        vbw[nj] = (uint32_t)L.p[pj].w + (uint32_t)mat_row(brow[nj]) * (uint32_t)(K * B / 8) + kh * (4 * B);
     }
     // ---- scales: wave wv copies those of rows 64 wv + lane (one 16-bit value per row and
-    // stage: affine scale and bias; MXFP4 the e8m0 bytes of the stage's two groups) into a
-    // 32-bit LDS slot per row
+    // stage: affine scale and bias of the stage's group -- groups of 128 codes span two stages,
+    // gs = 1; MXFP4 the e8m0 bytes of the stage's two groups) into a 32-bit LDS slot per row
+    const int gs = kAffine<MODE> ? a.gshift : 0;
     const int p_w = KIND == 0 ? (mlp ? 0 : (wv >= 2 ? 1 : 0)) : 2;  // matrix of the rows this wave copies
     const int so = (int)L.p[p_w].s, bo = (int)L.p[p_w].b;
     const uint32_t vsc = kAffine<MODE>
-        ? (uint32_t)mat_row(wv * 64 + lane) * (uint32_t)(K / 64) * 2
+        ? (uint32_t)mat_row(wv * 64 + lane) * (uint32_t)((K / 64) >> gs) * 2
         : (uint32_t)mat_row(wv * 64 + lane) * (uint32_t)(K / 32);
-    // the scales of two stages are one 4-byte copy when every scale row and array of the
-    // block's matrices is 4-byte aligned (affine: K / 64 even; MXFP4: K a multiple of 128);
-    // otherwise each stage copies its own 2 bytes (the waits below assume the paired count,
-    // which then makes them wait for one or two more copies than they need)
+    // the scales of two stages are one 4-byte copy when they are two groups and every scale row
+    // and array of the block's matrices is 4-byte aligned (affine: K / 64 even; MXFP4: K a
+    // multiple of 128); otherwise each stage copies its own 2 bytes (the waits below assume the
+    // paired count, which then makes them wait for one or two more copies than they need)
     const int rb = K / 32;   // scale bytes per row (affine: K / 64 16-bit values; MXFP4: K / 32 bytes)
-    bool spair = (rb & 3) == 0;
+    bool spair = (rb & 3) == 0 && gs == 0;
 #pragma unroll
     for (int pj = 0; pj < 3; ++pj)
         if (KIND == 0 ? (pj == 0 || (pj == 1 && !mlp)) : pj == 2)
@@ -566,9 +581,9 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
         }
     }
 
-    // the lane's B words of one stage (fragment nj: words kk = 0..3 of its 16-byte half)
+    // the lane's B words of one stage (fragment nj: the B words of its half, 8 codes a piece)
     struct BReg {
-        u32x4_t w[kNJ];
+        uint32_t w[kNJ][kBW<MODE>];
     };
     // issue every load of stage s: A and scale copies into ring slot s % NS, B into `br`
     auto issue = [&](int s, BReg& br) __attribute__((always_inline)) {
@@ -593,19 +608,32 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
             }
         } else {
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rb_rsrc, (LDS_PTR)(st + SA + wv * 256), 2, vsc,
-                                                     so + g * 2, 0, 0);
+                                                     so + (g >> gs) * 2, 0, 0);
             if constexpr (kAffine<MODE>)
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(rb_rsrc, (LDS_PTR)(st + SA + 1024 + wv * 256), 2,
-                                                         vsc, bo + g * 2, 0, 0);
+                                                         vsc, bo + (g >> gs) * 2, 0, 0);
         }
+        // the lane's half of the stage segment: 4 B bytes (kBLoads loads per fragment)
 #pragma unroll
         for (int nj = 0; nj < kNJ; ++nj) {
-            if constexpr (MODE == kModeAffine3) {
-                // 3-bit: the lane's half of the stage segment is 12 bytes (4 groups of 8 codes)
-                const u32x3_t w3 = __builtin_amdgcn_raw_buffer_load_b96(rb_rsrc, vbw[nj], g * 24, 0);
-                br.w[nj] = u32x4_t{w3[0], w3[1], w3[2], 0u};
+            uint32_t* q = br.w[nj];
+            const int go = g * (8 * B);
+            if constexpr (B == 2) {
+                const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(rb_rsrc, vbw[nj], go, 0);
+                q[0] = v[0]; q[1] = v[1];
+            } else if constexpr (B == 3) {
+                const u32x3_t v = __builtin_amdgcn_raw_buffer_load_b96(rb_rsrc, vbw[nj], go, 0);
+                q[0] = v[0]; q[1] = v[1]; q[2] = v[2];
             } else {
-                br.w[nj] = __builtin_amdgcn_raw_buffer_load_b128(rb_rsrc, vbw[nj], g * 32, 0);
+                const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rb_rsrc, vbw[nj], go, 0);
+                q[0] = v[0]; q[1] = v[1]; q[2] = v[2]; q[3] = v[3];
+                if constexpr (B == 6) {
+                    const u32x2_t u = __builtin_amdgcn_raw_buffer_load_b64(rb_rsrc, vbw[nj], go + 16, 0);
+                    q[4] = u[0]; q[5] = u[1];
+                } else if constexpr (B == 8) {
+                    const u32x4_t u = __builtin_amdgcn_raw_buffer_load_b128(rb_rsrc, vbw[nj], go + 16, 0);
+                    q[4] = u[0]; q[5] = u[1]; q[6] = u[2]; q[7] = u[3];
+                }
             }
         }
     };
@@ -643,21 +671,12 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
             }
         }
     };
-    // word kk of the lane's stage half, dequantized into MFMA operands
+    // piece kk of the lane's stage half, dequantized into MFMA operands
     auto deq = [&](bf16x8_t (&bop)[kNJ], const BReg& bw, const SReg& f, int kk) __attribute__((always_inline)) {
 #pragma unroll
         for (int nj = 0; nj < kNJ; ++nj) {
             const float sv = f.s[nj], bv = f.b[nj], sc = f.s[nj];
-            uint32_t wk = bw.w[nj][kk];
-            if constexpr (MODE == kModeAffine3) {
-                // the 24-bit group kk of the lane's 12 bytes
-                const u32x4_t& q = bw.w[nj];
-                wk = kk == 0 ? q[0]
-                   : kk == 1 ? __builtin_amdgcn_alignbit(q[1], q[0], 24)
-                   : kk == 2 ? __builtin_amdgcn_alignbit(q[2], q[1], 16)
-                             : q[2] >> 8;
-            }
-            bop[nj] = dq8<MODE>(wk, sv, bv, sc);
+            bop[nj] = dq8<MODE>(bw.w[nj], kk, sv, bv, sc);
         }
     };
 
@@ -772,9 +791,9 @@ void k_pf_gemm(FwdArgs a, const int32_t* __restrict__ order, const int32_t* __re
     }
     if (rows <= 32)
         pf_tile<MODE, F16, KIND, 2>(a, order, hbuf, hstride, y_routed, y_shared, ring, dst_s, e, m0, rows, ti.w, nt);
-    else if (rows <= 64)
+    else if (kTileRows<MODE> == 64 || rows <= 64)
         pf_tile<MODE, F16, KIND, 4>(a, order, hbuf, hstride, y_routed, y_shared, ring, dst_s, e, m0, rows, ti.w, nt);
-    else
+    else if constexpr (kTileRows<MODE> == 128)
         pf_tile<MODE, F16, KIND, 8>(a, order, hbuf, hstride, y_routed, y_shared, ring, dst_s, e, m0, rows, ti.w, nt);
 }
 
@@ -852,14 +871,18 @@ struct PfWs {
 
 inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
+// The M tile height of a kernel mode (kTileRows on the host).
+inline int tile_rows(int mode) { return mode == kModeAffine6 || mode == kModeAffine8 ? 64 : kBM; }
+
 PfWs carve(const FwdArgs& a, void* ws) {
     const int P = a.P;
     const int T_sh = a.auto_shared ? a.T : 0;
     const int P_ext = P + T_sh;
     const int E_ext = a.E + (a.shared ? 1 : 0);
     const int Imax = a.I > a.I_sh ? a.I : a.I_sh;
-    // at most ceil(P_ext / kBM) full tiles plus one partial tile per expert
-    const int mt_max = (P_ext + kBM - 1) / kBM + E_ext;
+    // at most ceil(P_ext / BM) full tiles plus one partial tile per expert
+    const int BM = tile_rows(a.quant_mode);
+    const int mt_max = (P_ext + BM - 1) / BM + E_ext;
     PfWs w{};
     w.mt_pad = (mt_max + kXcd - 1) / kXcd * kXcd;
     size_t off = 0;
@@ -942,18 +965,22 @@ hipError_t launch_prefill(const FwdArgs& a, void* ws, size_t ws_bytes, int phase
     uint16_t* y_routed = a.yun ? a.yun : w.y_routed;
     hipError_t err = hipSuccess;
     if (phases & 1) {
-        err = launch_bucket(a.pexp, P, a.E, E_ext, T_sh, kBM, a.g2s, a.capacity, a.host != nullptr, a.err, w.order, w.offsets,
+        err = launch_bucket(a.pexp, P, a.E, E_ext, T_sh, tile_rows(a.quant_mode), a.g2s, a.capacity, a.host != nullptr, a.err, w.order, w.offsets,
                             w.tile_start, w.tinfo, s);
         if (err != hipSuccess) return err;
     }
-    if (a.quant_mode == kModeAffine3)
-        err = a.scale_f16 ? launch_gemm<kModeAffine3, true>(a, w, E_ext, Imax, y_routed, phases, s)
-                          : launch_gemm<kModeAffine3, false>(a, w, E_ext, Imax, y_routed, phases, s);
-    else if (a.quant_mode == BRX_QUANT_AFFINE)
-        err = a.scale_f16 ? launch_gemm<BRX_QUANT_AFFINE, true>(a, w, E_ext, Imax, y_routed, phases, s)
-                          : launch_gemm<BRX_QUANT_AFFINE, false>(a, w, E_ext, Imax, y_routed, phases, s);
-    else
-        err = launch_gemm<BRX_QUANT_MXFP4, false>(a, w, E_ext, Imax, y_routed, phases, s);
+#define BRX_GEMM(M) (a.scale_f16 ? launch_gemm<M, true>(a, w, E_ext, Imax, y_routed, phases, s) \
+                                 : launch_gemm<M, false>(a, w, E_ext, Imax, y_routed, phases, s))
+    switch (a.quant_mode) {
+        case kModeAffine4: err = BRX_GEMM(kModeAffine4); break;
+        case kModeAffine3: err = BRX_GEMM(kModeAffine3); break;
+        case kModeAffine2: err = BRX_GEMM(kModeAffine2); break;
+        case kModeAffine6: err = BRX_GEMM(kModeAffine6); break;
+        case kModeAffine8: err = BRX_GEMM(kModeAffine8); break;
+        case BRX_QUANT_MXFP4: err = launch_gemm<BRX_QUANT_MXFP4, false>(a, w, E_ext, Imax, y_routed, phases, s); break;
+        default: err = hipErrorInvalidValue;
+    }
+#undef BRX_GEMM
     if (err != hipSuccess) return err;
     if ((phases & 2) && a.out)
         err = launch_combine(y_routed, a.auto_shared ? w.y_shared : nullptr, a.w, a.sgate, a.T, a.k,

@@ -77,7 +77,8 @@ def test_expert_layout_matches_formats(spec):
 
 
 BAD = [("hidden", 100, "hidden"), ("inter", 0, "inter"), ("n_experts", 513, "n_experts"),
-       ("top_k", 0, "top_k"), ("bits", 5, "affine"), ("group_size", 128, "affine"),
+       ("top_k", 0, "top_k"), ("bits", 5, "affine"), ("bits", 7, "affine"), ("group_size", 32, "affine"),
+       ("group_size", 256, "affine"),
        ("quant_mode", 7, "quant_mode"), ("act", 5, "act"), ("route_mode", 5, "route_mode"),
        ("n_group", 65, "n_group"), ("n_group", 3, "divide"), ("n_group", 4, "topk_group 0 outside"),
        ("route_scale", -1.0, "route_scale"), ("router_dtype", 9, "router_dtype"), ("shared_inter", 96, "shared_inter"),
@@ -99,6 +100,41 @@ def test_descriptor_validation(field, value, msg):
     assert lib.brx_sort_pairs(C.byref(d), None, 1, None, None, None) == L.BRX_EINVAL
     h = C.c_void_p()
     assert lib.brx_pool_create(C.byref(d), 4, C.byref(h)) == L.BRX_EINVAL and not h.value
+
+
+# the reference's per-layer precision candidates (bigrig_engine/precision.py:58), plus 6- and
+# 8-bit at group 128 (MLX writes those too)
+WIDTHS = [(2, 128), (2, 64), (3, 128), (3, 64), (4, 128), (4, 64), (6, 64), (8, 64), (6, 128), (8, 128)]
+
+
+@pytest.mark.parametrize("bits,group", WIDTHS, ids=[f"{b}bit-g{g}" for b, g in WIDTHS])
+def test_every_affine_width_is_accepted_with_the_packed_layout(bits, group):
+    """Each width validates and its expert layout is the one formats packs (weight words of
+    32 / bits codes or byte-aligned runs, then K / group scales and biases per row)."""
+    from dataclasses import replace
+    lib = L.load()
+    for fp16 in (False, True):
+        spec = replace(QWEN3_30B_A3B, quant=F.QuantSpec(bits, group, "affine", "float16" if fp16 else "bfloat16"))
+        d = spec.desc()
+        out = L.ExpertLayout()
+        L.check(lib.brx_expert_layout_get(C.byref(d), 0, C.byref(out)))
+        offs = F.spec_offsets(spec.expert_spec())
+        assert out.bytes_per_expert == F.spec_bytes(spec.expert_spec())
+        for p, proj in enumerate(F.PROJECTIONS):
+            assert out.weight[p] == offs[(proj, "weight")]
+            assert out.scales[p] == offs[(proj, "scales")]
+            assert out.biases[p] == offs[(proj, "biases")]
+
+
+def test_group_of_128_needs_widths_it_divides():
+    lib = L.load()
+    for field in ("hidden", "inter", "shared_inter"):
+        d = E256_SHARED.desc()
+        d.group_size = 128
+        setattr(d, field, 704)          # a multiple of 64, not of 128
+        out = L.ExpertLayout()
+        assert lib.brx_expert_layout_get(C.byref(d), 0, C.byref(out)) == L.BRX_EINVAL
+        assert "multiples of the group size" in lib.brx_last_error().decode()
 
 
 def test_calls_before_init_fail_cleanly():
