@@ -68,7 +68,7 @@ def parse():
     ap.add_argument("--pool-capacity", type=int, default=32)
     ap.add_argument("--pool-tokens", type=int, default=64)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--skip", default="", help="comma list of: prefill,pool,layered,replay,cpu,graph,report")
+    ap.add_argument("--skip", default="", help="comma list of: prefill,pool,layered,replay,cpu,graph,report,widths")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB (--steps times): the "
                          "known-size reference for scaling HBM byte counters")
@@ -529,6 +529,37 @@ def config_report(args):
     return rep
 
 
+# affine widths of the reference's per-layer precision candidates (bigrig_engine/precision.py:58)
+WIDTHS = [(2, 128), (2, 64), (3, 128), (3, 64), (4, 128), (4, 64), (6, 64), (8, 64)]
+
+
+def widths_report():
+    """The Qwen3-30B-A3B-shaped layer (Zipf(1.1) router bias, all experts resident) at every
+    affine width and group size: 8 layers (1.4-5.4 GB, beyond the last-level cache), decode at
+    batch 1 (64 steps, fresh inputs) and 2048-token prefill chunks (4-bit g64 is the headline
+    layer, measured here in the same way as the others)."""
+    from dataclasses import replace
+
+    import torch
+
+    from bigrig_amd import formats as F
+    from bigrig_amd.spec import QWEN3_30B_A3B
+    rep = {}
+    for b_, g_ in WIDTHS:
+        spec = replace(QWEN3_30B_A3B, quant=F.QuantSpec(b_, g_))
+        st = Stack(spec, 8, bank=64)
+        dec = decode_report(st, 1, steps=64)
+        pf = prefill_report(st, 2048, reps=3)
+        rep[f"{b_}bit_g{g_}"] = {
+            "bytes_per_expert": spec.bytes_per_expert,
+            "decode_us_per_layer": dec["us_per_layer"], "decode_hbm_frac": dec["hbm_frac"],
+            "prefill_us_per_layer": pf["us_per_layer"], "prefill_mfma_frac": pf["mfma_frac"]}
+        log(f"width {b_}-bit g{g_}: decode {dec['us_per_layer']} us, prefill {pf['us_per_layer']} us per layer")
+        del st
+        torch.cuda.empty_cache()
+    return rep
+
+
 def pool_bench(args, st: "Stack", host_served: bool = False, capacities=None):
     """Bounded pool end to end: C of E experts per layer resident, misses copied from pinned
     host memory. Synchronous: one routing read-back per layer, misses admitted before the layer
@@ -718,6 +749,13 @@ def main():
         del st
         torch.cuda.empty_cache()
         report = config_report(args)
+    widths = None
+    if "widths" not in skip:
+        log("affine widths")
+        if "report" in skip:
+            del st
+            torch.cuda.empty_cache()
+        widths = widths_report()
     # HBM bytes per launch of the timed kernel, from the committed FETCH_SIZE / WRITE_SIZE
     # profile; only counters taken on this kernel are reported
     traffic = None
@@ -787,6 +825,8 @@ def main():
         }
     if report is not None:
         rec["report"] = report
+    if widths is not None:
+        rec["widths"] = widths
     if pool is not None:
         def rnd(d):
             return {k2: (rnd(v) if isinstance(v, dict) else round(v, 4) if isinstance(v, float)
