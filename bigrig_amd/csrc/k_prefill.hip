@@ -484,7 +484,44 @@ __device__ __forceinline__ void pf_store(const FwdArgs& a, const Layout& L, cons
     }
 }
 
-template <int MODE, bool F16, int KIND, int MF>
+// How a block copies its rows' scales into LDS: per row and stage one 16-bit affine scale and
+// bias, or MXFP4's two e8m0 bytes. One copy ("unit") per row is 4 bytes holding stages 2u and
+// 2u + 1 when every scale row and array of the block's matrices is 4-byte aligned and a group
+// is one stage (affine groups of 64: K / 64 even; MXFP4: K a multiple of 128), else 2 bytes: the
+// value of stage u, or of group u spanning stages 2u and 2u + 1 (affine groups of 128). A
+// 16-bit copy into LDS fills a 32-bit slot, zero-extended.
+struct ScalePlan {
+    bool pair;
+    int gs;         // stage -> group shift (1: groups of 128)
+    int nu;         // units per row
+    int pitch;      // scale-table slots per row: nu rounded up to odd, so 32 rows read conflict-free
+    int rowbytes;   // bytes of one row of a scale array
+};
+template <int MODE, int KIND>
+__device__ __forceinline__ ScalePlan scale_plan(const FwdArgs& a, const Layout& L, int K, bool mlp) {
+    ScalePlan p;
+    p.gs = kAffine<MODE> ? a.gshift : 0;
+    p.rowbytes = kAffine<MODE> ? ((K / 64) >> p.gs) * 2 : K / 32;
+    bool pair = (p.rowbytes & 3) == 0 && p.gs == 0;
+#pragma unroll
+    for (int pj = 0; pj < 3; ++pj)
+        if (KIND == 0 ? (pj == 0 || (pj == 1 && !mlp)) : pj == 2)
+            pair = pair && ((L.p[pj].s & 3) == 0) && (!kAffine<MODE> || (L.p[pj].b & 3) == 0);
+    p.pair = pair;
+    p.nu = p.rowbytes / (pair ? 4 : 2);
+    p.pitch = p.nu | 1;
+    return p;
+}
+
+// LDS bytes of a tile of MF x 16 rows: its A ring, plus the scale table when it has one
+// (256 rows x pitch slots for each scale array; the per-stage copies sit in the ring otherwise).
+template <int MODE>
+__host__ __device__ constexpr int tile_lds(int MF, bool tbl, int pitch) {
+    return tbl ? kNS * MF * 16 * kBK * 2 + (kAffine<MODE> ? 2 : 1) * 256 * pitch * 4
+               : kNS * (MF * 16 * kBK * 2 + kStS);
+}
+
+template <int MODE, bool F16, int KIND, int MF, bool TBL>
 __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restrict__ order,
                                         uint16_t* __restrict__ hbuf, int hstride,
                                         uint16_t* __restrict__ y_routed, uint16_t* __restrict__ y_shared,
@@ -493,11 +530,11 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
     constexpr int NA = MF * 16 * 8 / 64 / kGemmWaves;   // A copies per wave per stage
     constexpr int NS = kNS;                             // stages in the ring
     constexpr int SA = MF * 16 * kBK * 2;               // A bytes per stage
-    constexpr int SS = SA + kStS;                       // stage bytes in the ring
+    constexpr int SS = TBL ? SA : SA + kStS;            // stage bytes in the ring
     // loads per wave of an odd stage (A copies, B loads) and of an even stage (+ the scale copies
-    // of it and the next stage)
+    // of it and the next stage, unless the tile reads its scales from the table)
     constexpr int NV1 = NA + kNJ * kBLoads<MODE>;
-    constexpr int NV0 = NV1 + (kAffine<MODE> ? 2 : 1);
+    constexpr int NV0 = NV1 + (TBL ? 0 : kAffine<MODE> ? 2 : 1);
     constexpr int B = kBits<MODE>;
     const bool sh = e >= a.E;
     const int inter = sh ? a.I_sh : a.I;
@@ -551,25 +588,20 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
         const int pj = KIND == 0 ? (mlp ? 0 : nj) : 2;
         vbw[nj] = (uint32_t)L.p[pj].w + (uint32_t)mat_row(brow[nj]) * (uint32_t)(K * B / 8) + kh * (4 * B);
     }
-    // ---- scales: wave wv copies those of rows 64 wv + lane (one 16-bit value per row and
-    // stage: affine scale and bias of the stage's group -- groups of 128 codes span two stages,
-    // gs = 1; MXFP4 the e8m0 bytes of the stage's two groups) into a 32-bit LDS slot per row
-    const int gs = kAffine<MODE> ? a.gshift : 0;
+    // ---- scales (ScalePlan). Without the table, wave wv copies those of rows 64 wv + lane into
+    // a 32-bit slot per row of the stage's ring slot, one unit per stage pair (paired) or stage;
+    // the waits below assume the paired count, which unpaired makes them wait for one or two
+    // more copies than they need. With the table (TBL), every unit of every row is copied once,
+    // before the first stage, into [256 rows][pitch] slots after the A ring: lanes run along
+    // each row's contiguous scale array, so a copy instruction touches a few cache lines rather
+    // than one per lane, and no stage copies scales.
+    const ScalePlan sp = scale_plan<MODE, KIND>(a, L, K, mlp);
+    const int gs = sp.gs;
+    const bool spair = sp.pair;
     const int p_w = KIND == 0 ? (mlp ? 0 : (wv >= 2 ? 1 : 0)) : 2;  // matrix of the rows this wave copies
     const int so = (int)L.p[p_w].s, bo = (int)L.p[p_w].b;
-    const uint32_t vsc = kAffine<MODE>
-        ? (uint32_t)mat_row(wv * 64 + lane) * (uint32_t)((K / 64) >> gs) * 2
-        : (uint32_t)mat_row(wv * 64 + lane) * (uint32_t)(K / 32);
-    // the scales of two stages are one 4-byte copy when they are two groups and every scale row
-    // and array of the block's matrices is 4-byte aligned (affine: K / 64 even; MXFP4: K a
-    // multiple of 128); otherwise each stage copies its own 2 bytes (the waits below assume the
-    // paired count, which then makes them wait for one or two more copies than they need)
-    const int rb = K / 32;   // scale bytes per row (affine: K / 64 16-bit values; MXFP4: K / 32 bytes)
-    bool spair = (rb & 3) == 0 && gs == 0;
-#pragma unroll
-    for (int pj = 0; pj < 3; ++pj)
-        if (KIND == 0 ? (pj == 0 || (pj == 1 && !mlp)) : pj == 2)
-            spair = spair && ((L.p[pj].s & 3) == 0) && (!kAffine<MODE> || (L.p[pj].b & 3) == 0);
+    const uint32_t vsc = (uint32_t)mat_row(wv * 64 + lane) * (uint32_t)sp.rowbytes;
+    uint8_t* const tbl = ring + NS * SA;
     if constexpr (KIND == 1) {
         if (tid < kBM) {
             int d = -1;
@@ -595,9 +627,9 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
                                                      va[i], g * 128, 0, 0);
         // scales: paired, an even stage's slot holds its 16-bit scale (and bias) value in the
         // low half and the next stage's in the high half and an odd stage copies nothing;
-        // unpaired, every stage copies its own 16 bits (a 16-bit copy to LDS fills a 32-bit
-        // slot, zero-extended)
-        if (spair) {
+        // unpaired, every stage copies its own 16 bits
+        if constexpr (TBL) {
+        } else if (spair) {
             if ((s & 1) == 0) {
                 const int gp = g & ~1;
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(rb_rsrc, (LDS_PTR)(st + SA + wv * 256), 4, vsc,
@@ -655,14 +687,19 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
     auto fetch_s = [&](SReg& f, int s) __attribute__((always_inline)) {
         // paired scales of an odd stage: the high halves of the previous (even) stage's slots
         const bool hi = spair && (s & 1);
-        const uint8_t* ss = ring + ((hi ? s - 1 : s) % NS) * SS;
         const int sh = hi ? 16 : 0;
+        // per-stage copies: the slots of rows br in the stage's ring slot; the table: slot
+        // br * pitch + unit of each array (a stage past the last reads the last unit)
+        const uint8_t* ss = TBL ? tbl : ring + ((hi ? s - 1 : s) % NS) * SS + SA;
+        const int unit = TBL ? min(spair ? s >> 1 : s >> gs, sp.nu - 1) : 0;
+        const int rs = TBL ? sp.pitch : 1;          // slots between rows
+        const int ab = TBL ? 256 * sp.pitch * 4 : 1024;   // bytes between the scale and bias arrays
 #pragma unroll
         for (int nj = 0; nj < kNJ; ++nj) {
-            const int br = brow[nj];
-            const uint32_t sv = (*reinterpret_cast<const uint32_t*>(ss + SA + br * 4) >> sh) & 0xFFFFu;
+            const int br = brow[nj] * rs + unit;
+            const uint32_t sv = (*reinterpret_cast<const uint32_t*>(ss + br * 4) >> sh) & 0xFFFFu;
             if constexpr (kAffine<MODE>) {
-                const uint32_t bv = (*reinterpret_cast<const uint32_t*>(ss + SA + 1024 + br * 4) >> sh) & 0xFFFFu;
+                const uint32_t bv = (*reinterpret_cast<const uint32_t*>(ss + ab + br * 4) >> sh) & 0xFFFFu;
                 f.s[nj] = (F16 ? h2f(sv) : bf2f(sv)) * 16777216.0f;
                 f.b[nj] = F16 ? h2f(bv) : bf2f(bv);
             } else {
@@ -711,6 +748,37 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
     // is unrolled NS times to keep every set index a constant.
     // (the empty asm with a memory clobber keeps each stage's copies into LDS after the previous
     // stage's: the wait counts them in issue order and the compiler cannot see their targets)
+    if constexpr (TBL) {
+        // the scale table: slot q = c * 256 + tid of copy c holds unit q % pitch of row
+        // q / pitch (slot nu of an even nu is padding and repeats unit nu - 1); (r, u) advance by
+        // 256 slots a copy
+        const int pitch = sp.pitch, dr = 256 / pitch, du = 256 - dr * pitch;
+        int r = tid / pitch, u = tid - r * pitch;
+        uint8_t* const tb = tbl + 256 * pitch * 4;
+        for (int c = 0; c < pitch; ++c) {
+            const int pm = KIND == 0 ? (mlp ? 0 : (r >= 128 ? 1 : 0)) : 2;
+            const uint32_t vo = (uint32_t)mat_row(r) * (uint32_t)sp.rowbytes +
+                                (uint32_t)min(u, sp.nu - 1) * (spair ? 4u : 2u);
+            LDS_PTR ds = (LDS_PTR)(tbl + (c * 256 + wv * 64) * 4);
+            LDS_PTR db = (LDS_PTR)(tb + (c * 256 + wv * 64) * 4);
+            if (spair) {
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rb_rsrc, ds, 4, vo + (uint32_t)L.p[pm].s, 0, 0, 0);
+                if constexpr (kAffine<MODE>)
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(rb_rsrc, db, 4, vo + (uint32_t)L.p[pm].b, 0, 0, 0);
+            } else {
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rb_rsrc, ds, 2, vo + (uint32_t)L.p[pm].s, 0, 0, 0);
+                if constexpr (kAffine<MODE>)
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(rb_rsrc, db, 2, vo + (uint32_t)L.p[pm].b, 0, 0, 0);
+            }
+            u += du;
+            r += dr;
+            if (u >= pitch) {
+                u -= pitch;
+                ++r;
+            }
+        }
+        asm volatile("" ::: "memory");
+    }
     BReg bq[NS];
 #pragma unroll
     for (int t = 0; t < NS - 1; ++t) {
@@ -789,12 +857,26 @@ void k_pf_gemm(FwdArgs a, const int32_t* __restrict__ order, const int32_t* __re
     } else {
         if (nt * kBlockN >= a.H) return;
     }
-    if (rows <= 32)
-        pf_tile<MODE, F16, KIND, 2>(a, order, hbuf, hstride, y_routed, y_shared, ring, dst_s, e, m0, rows, ti.w, nt);
-    else if (kTileRows<MODE> == 64 || rows <= 64)
-        pf_tile<MODE, F16, KIND, 4>(a, order, hbuf, hstride, y_routed, y_shared, ring, dst_s, e, m0, rows, ti.w, nt);
-    else if constexpr (kTileRows<MODE> == 128)
-        pf_tile<MODE, F16, KIND, 8>(a, order, hbuf, hstride, y_routed, y_shared, ring, dst_s, e, m0, rows, ti.w, nt);
+    // 32- and 64-row tiles whose scales are copied 2 bytes a stage (unpaired) read them from a
+    // table copied once per tile when it fits beside their A ring: gpt-oss's 512-token prefill
+    // (MXFP4, 90-byte scale rows) 800 -> 705 us per layer. Paired layouts keep the per-stage
+    // copies (a table made the Qwen3-shape gate/up 2.5% slower), as do 128-row tiles, whose A
+    // ring leaves no room for it.
+    const bool sh = e >= a.E;
+    const int K = KIND == 0 ? a.H : (sh ? a.I_sh : a.I);
+    const ScalePlan sp = scale_plan<MODE, KIND>(a, sh ? a.lay_sh : a.lay, K, KIND == 0 && a.act == BRX_ACT_SILU_MLP);
+#define BRX_TILE(MF, TBL) \
+    pf_tile<MODE, F16, KIND, MF, TBL>(a, order, hbuf, hstride, y_routed, y_shared, ring, dst_s, e, m0, rows, ti.w, nt)
+    if (rows <= 32) {
+        if (!sp.pair && tile_lds<MODE>(2, true, sp.pitch) <= kNS * kStage) BRX_TILE(2, true);
+        else BRX_TILE(2, false);
+    } else if (kTileRows<MODE> == 64 || rows <= 64) {
+        if (!sp.pair && tile_lds<MODE>(4, true, sp.pitch) <= kNS * kStage) BRX_TILE(4, true);
+        else BRX_TILE(4, false);
+    } else if constexpr (kTileRows<MODE> == 128) {
+        BRX_TILE(8, false);
+    }
+#undef BRX_TILE
 }
 
 // ------------------------------------------------------------------ combine

@@ -116,11 +116,19 @@ def test_full_chunk_rows_independent_of_tiles(gpu, spec):
     small(E256_SHARED, hidden=512, inter=256, n_experts=16, top_k=4, shared_inter=256),
     small(QWEN3_30B_A3B, hidden=512, inter=256, n_experts=8, top_k=2,
           quant=F.QuantSpec(4, 64, "affine", "float16")),
-], ids=["silu-mlp", "mxfp4-clamped", "shared", "fp16-scales"])
+    # scale rows of 18 and 10 bytes: 2-byte scale copies, which 32- and 64-row tiles read from
+    # a per-tile table and 128-row tiles copy stage by stage
+    small(QWEN3_30B_A3B, hidden=576, inter=320, n_experts=8, top_k=2,
+          quant=F.QuantSpec(4, 32, "mxfp4"), has_bias=True, act="swiglu_clamped",
+          route="topk_softmax"),
+    small(QWEN3_30B_A3B, hidden=512, inter=384, n_experts=8, top_k=2,
+          quant=F.QuantSpec(2, 128, "affine")),
+], ids=["silu-mlp", "mxfp4-clamped", "shared", "fp16-scales", "mxfp4-unpaired", "2bit-g128"])
 def test_small_layer_rows_independent_of_tiles(gpu, spec):
     """Small layers with a strongly biased router, so one expert takes several full tiles (a
     partial last one too): two-layer experts, MXFP4 with biases and the clamped SwiGLU, a shared
-    expert (every token's shared pair) and fp16 scales."""
+    expert (every token's shared pair), fp16 scales, and layouts whose scales are copied 2 bytes
+    a stage (MXFP4 with 18-byte scale rows, 2-bit groups of 128)."""
     import torch
     T = 700
     lay = make_layer(spec, seed=77, zipf=4.0)
