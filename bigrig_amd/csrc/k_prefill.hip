@@ -273,7 +273,11 @@ constexpr int kStA = kBM * kBK * 2;          // stage bytes: A tile
 constexpr int kStS = kBlockN * 4 * 2;        // scale and bias per row, one 32-bit LDS slot each
 constexpr int kStage = kStA + kStS;
 static_assert(kNS % 2 == 0, "the paired scale copies follow stage parity through the unrolled ring");
-static_assert(8 * 16 * (kBlockN + 8) * 2 <= kNS * kStage, "the widest output tile must fit in the ring");
+// The block's LDS: the ring (A stages, per-stage scale slots or the scale table, then the output
+// tile) takes all of a CU's 160 KB that two blocks can share, less the down kernel's row list.
+constexpr int kRing = 80 * 1024 - kBM * 4;
+static_assert(kNS * kStage <= kRing, "the per-stage ring must fit");
+static_assert(8 * 16 * (kBlockN + 8) * 2 <= kRing, "the widest output tile must fit in the ring");
 
 typedef __attribute__((address_space(3))) void* LDS_PTR;
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
@@ -755,20 +759,26 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
         const int pitch = sp.pitch, dr = 256 / pitch, du = 256 - dr * pitch;
         int r = tid / pitch, u = tid - r * pitch;
         uint8_t* const tb = tbl + 256 * pitch * 4;
+        // the scale and bias arrays of rows 0..127 and 128..255 (gate / up for a gated expert),
+        // read once as uniform values: indexing the layout by a per-lane matrix number would
+        // read the kernel arguments per lane, a vector load the next copy would wait for
+        const int plo = KIND == 0 ? 0 : 2, phi = KIND == 0 ? (mlp ? 0 : 1) : 2;
+        const uint32_t s_lo = (uint32_t)L.p[plo].s, s_hi = (uint32_t)L.p[phi].s;
+        const uint32_t b_lo = (uint32_t)L.p[plo].b, b_hi = (uint32_t)L.p[phi].b;
         for (int c = 0; c < pitch; ++c) {
-            const int pm = KIND == 0 ? (mlp ? 0 : (r >= 128 ? 1 : 0)) : 2;
+            const bool up = r >= 128;
             const uint32_t vo = (uint32_t)mat_row(r) * (uint32_t)sp.rowbytes +
                                 (uint32_t)min(u, sp.nu - 1) * (spair ? 4u : 2u);
             LDS_PTR ds = (LDS_PTR)(tbl + (c * 256 + wv * 64) * 4);
             LDS_PTR db = (LDS_PTR)(tb + (c * 256 + wv * 64) * 4);
             if (spair) {
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rb_rsrc, ds, 4, vo + (uint32_t)L.p[pm].s, 0, 0, 0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rb_rsrc, ds, 4, vo + (up ? s_hi : s_lo), 0, 0, 0);
                 if constexpr (kAffine<MODE>)
-                    __builtin_amdgcn_raw_ptr_buffer_load_lds(rb_rsrc, db, 4, vo + (uint32_t)L.p[pm].b, 0, 0, 0);
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(rb_rsrc, db, 4, vo + (up ? b_hi : b_lo), 0, 0, 0);
             } else {
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rb_rsrc, ds, 2, vo + (uint32_t)L.p[pm].s, 0, 0, 0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rb_rsrc, ds, 2, vo + (up ? s_hi : s_lo), 0, 0, 0);
                 if constexpr (kAffine<MODE>)
-                    __builtin_amdgcn_raw_ptr_buffer_load_lds(rb_rsrc, db, 2, vo + (uint32_t)L.p[pm].b, 0, 0, 0);
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(rb_rsrc, db, 2, vo + (up ? b_hi : b_lo), 0, 0, 0);
             }
             u += du;
             r += dr;
@@ -841,7 +851,7 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2,
 void k_pf_gemm(FwdArgs a, const int32_t* __restrict__ order, const int32_t* __restrict__ tile_start,
                const int4* __restrict__ tinfo, int E_ext, int ntn, uint16_t* __restrict__ hbuf,
                int hstride, uint16_t* __restrict__ y_routed, uint16_t* __restrict__ y_shared) {
-    __shared__ __attribute__((aligned(16))) uint8_t ring[kNS * kStage];
+    __shared__ __attribute__((aligned(16))) uint8_t ring[kRing];
     __shared__ int32_t dst_s[KIND == 1 ? kBM : 1];
     const int blk = blockIdx.x;
     const int loc = blk / kXcd;
@@ -857,24 +867,23 @@ void k_pf_gemm(FwdArgs a, const int32_t* __restrict__ order, const int32_t* __re
     } else {
         if (nt * kBlockN >= a.H) return;
     }
-    // 32- and 64-row tiles whose scales are copied 2 bytes a stage (unpaired) read them from a
-    // table copied once per tile when it fits beside their A ring: gpt-oss's 512-token prefill
-    // (MXFP4, 90-byte scale rows) 800 -> 705 us per layer. Paired layouts keep the per-stage
-    // copies (a table made the Qwen3-shape gate/up 2.5% slower), as do 128-row tiles, whose A
-    // ring leaves no room for it.
+    // A tile reads its scales from a table copied once per tile when the table fits beside its
+    // A ring (gpt-oss's 512-token prefill 800 -> 615 us per layer, the Qwen3-shape gate/up
+    // 168 -> 160 us); otherwise (128-row tiles of wide K) each stage's scales come with the stage.
     const bool sh = e >= a.E;
     const int K = KIND == 0 ? a.H : (sh ? a.I_sh : a.I);
     const ScalePlan sp = scale_plan<MODE, KIND>(a, sh ? a.lay_sh : a.lay, K, KIND == 0 && a.act == BRX_ACT_SILU_MLP);
 #define BRX_TILE(MF, TBL) \
     pf_tile<MODE, F16, KIND, MF, TBL>(a, order, hbuf, hstride, y_routed, y_shared, ring, dst_s, e, m0, rows, ti.w, nt)
     if (rows <= 32) {
-        if (!sp.pair && tile_lds<MODE>(2, true, sp.pitch) <= kNS * kStage) BRX_TILE(2, true);
+        if (tile_lds<MODE>(2, true, sp.pitch) <= kRing) BRX_TILE(2, true);
         else BRX_TILE(2, false);
     } else if (kTileRows<MODE> == 64 || rows <= 64) {
-        if (!sp.pair && tile_lds<MODE>(4, true, sp.pitch) <= kNS * kStage) BRX_TILE(4, true);
+        if (tile_lds<MODE>(4, true, sp.pitch) <= kRing) BRX_TILE(4, true);
         else BRX_TILE(4, false);
     } else if constexpr (kTileRows<MODE> == 128) {
-        BRX_TILE(8, false);
+        if (tile_lds<MODE>(8, true, sp.pitch) <= kRing) BRX_TILE(8, true);
+        else BRX_TILE(8, false);
     }
 #undef BRX_TILE
 }
