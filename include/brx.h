@@ -68,8 +68,8 @@ typedef struct brx_layer_desc {
     int32_t n_experts;     /* E                                                             */
     int32_t top_k;         /* k                                                             */
     int32_t quant_mode;    /* BRX_QUANT_*                                                   */
-    int32_t bits;          /* affine: 4 or 3 (8 codes in 3 bytes, LSB first); mxfp4: 4      */
-    int32_t group_size;    /* 64 (affine) or 32 (mxfp4)                                     */
+    int32_t bits;          /* affine: 2, 3, 4, 6 or 8 (codes LSB first); mxfp4: 4           */
+    int32_t group_size;    /* 64 or 128 (affine) or 32 (mxfp4)                              */
     int32_t scale_dtype;   /* BRX_SCALE_* (affine)                                          */
     int32_t has_bias;      /* projections carry a `bias` [N] bf16 component (gpt-oss)       */
     int32_t act;           /* BRX_ACT_*                                                     */
