@@ -292,7 +292,9 @@ def layer_spec(man: CheckpointManifest, layer: int, **overrides):
     two_layer = not F.is_gated(e["spec"])
     first = e["spec"]["fc1" if two_layer else "gate_proj"]
     inter = int(first["weight"]["shape"][0])
-    hidden = int(first["weight"]["shape"][1]) * 32 // q.bits
+    # packed weights hold 32 / bits codes per uint32 word; bf16 weights are [n_out, n_in]
+    n_words = int(first["weight"]["shape"][1])
+    hidden = n_words if q.mode == "none" else n_words * 32 // q.bits
     kw = {"hidden": hidden, "inter": inter, "n_experts": int(e["n_experts"]),
           "top_k": int(man.top_k or 1), "quant": q, "has_bias": "bias" in first}
     kw.update(routing_from_config(man.config))

@@ -83,6 +83,12 @@ int check_desc(const brx_layer_desc* d) {
         if (d->bits != 4 || d->group_size != 32)
             return fail(BRX_EINVAL, "mxfp4 is 4-bit in groups of 32 (got %d-bit g%d)", d->bits,
                         d->group_size);
+    } else if (d->quant_mode == BRX_QUANT_NONE) {
+        // unquantized experts: bf16 weights with no scales (the mx.gather_mm branch,
+        // bigrig_engine/stream.py:1626-1628)
+        if (d->bits != 16 || d->group_size != 0)
+            return fail(BRX_EINVAL, "unquantized experts are bf16: bits 16, group_size 0 (got %d-bit g%d)",
+                        d->bits, d->group_size);
     } else {
         return fail(BRX_EINVAL, "quant_mode %d unknown", d->quant_mode);
     }

@@ -22,15 +22,19 @@ constexpr int kModeAffine3 = 2;
 constexpr int kModeAffine2 = 3;
 constexpr int kModeAffine6 = 4;
 constexpr int kModeAffine8 = 5;
+constexpr int kModeBf16 = 6;           // unquantized bf16 weights (BRX_QUANT_NONE)
 template <int MODE>
-constexpr bool kAffine = MODE != BRX_QUANT_MXFP4;   // scale + bias per group
+constexpr bool kAffine = MODE != BRX_QUANT_MXFP4 && MODE != kModeBf16;   // scale + bias per group
+template <int MODE>
+constexpr bool kScaled = MODE != kModeBf16;                           // any per-group scales
 template <int MODE>
 constexpr int kBits = MODE == kModeAffine2 ? 2 : MODE == kModeAffine3 ? 3 : MODE == kModeAffine6 ? 6
-                    : MODE == kModeAffine8 ? 8 : 4;
+                    : MODE == kModeAffine8 ? 8 : MODE == kModeBf16 ? 16 : 4;
 
 // The kernel mode of a descriptor's quantization (-1: none takes it).
 inline int kernel_mode(int quant_mode, int bits) {
     if (quant_mode == BRX_QUANT_MXFP4) return bits == 4 ? BRX_QUANT_MXFP4 : -1;
+    if (quant_mode == BRX_QUANT_NONE) return bits == 16 ? kModeBf16 : -1;
     switch (bits) {
         case 2: return kModeAffine2;
         case 3: return kModeAffine3;
@@ -104,12 +108,14 @@ inline Layout make_layout(const brx_layer_desc& d, int inter) {
         }
         int n_out = p < 2 ? inter : d.hidden;
         int n_in = p < 2 ? d.hidden : inter;
-        int64_t G = n_in / d.group_size;
+        int64_t G = d.group_size > 0 ? n_in / d.group_size : 0;
         L.p[p].n_out = n_out;
         L.p[p].n_in = n_in;
         L.p[p].w = (int32_t)pos;
         pos += (int64_t)n_out * n_in * d.bits / 8;
-        if (d.quant_mode == BRX_QUANT_AFFINE) {
+        if (d.quant_mode == BRX_QUANT_NONE) {          // unquantized bf16: the weight alone
+            L.p[p].s = L.p[p].b = -1;
+        } else if (d.quant_mode == BRX_QUANT_AFFINE) {
             L.p[p].s = (int32_t)pos; pos += (int64_t)n_out * G * 2;
             L.p[p].b = (int32_t)pos; pos += (int64_t)n_out * G * 2;
         } else {

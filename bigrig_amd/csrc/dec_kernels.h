@@ -195,7 +195,8 @@ struct PairIter {
 
 
 // ------------------------------------------------------------------ weight units
-// One unit is 64 codes of a row: 8 * bits bytes (32 for MXFP4, two 32-code groups).
+// One unit is 64 codes of a row: 8 * bits bytes (32 for MXFP4, two 32-code groups; 128 for
+// unquantized bf16 weights).
 template <int MODE, int UPL>
 struct Units {
     uint32_t w[UPL][2 * kBits<MODE>];
@@ -246,13 +247,16 @@ __device__ __forceinline__ void units_load(const uint8_t* base, const Proj& P, i
             u.s[j] = sp[un >> gs];
             u.b[j] = bp[un >> gs];
         }
-    } else {
+    } else if constexpr (kScaled<MODE>) {
         const uint16_t* sp = reinterpret_cast<const uint16_t*>(base + P.s + (int64_t)row * (2 * U));
 #pragma unroll
         for (int j = 0; j < UPL; ++j) {
             u.s[j] = sp[min(s + SP * j, U - 1)];
             u.b[j] = 0u;
         }
+    } else {
+#pragma unroll
+        for (int j = 0; j < UPL; ++j) u.s[j] = u.b[j] = 0u;
     }
 }
 
@@ -274,6 +278,19 @@ __device__ __forceinline__ float unit_dot(const Units<MODE, UPL>& u, int j, cons
         const float sc = scale_f16 ? h2f(u.s[j]) : bf2f(u.s[j]);
         const float bi = scale_f16 ? h2f(u.b[j]) : bf2f(u.b[j]);
         return fmaf(sc, acc, (bi - kCodeOffset<kBits<MODE>> * sc) * xsum);
+    } else if constexpr (MODE == kModeBf16) {
+        // unquantized: piece m is 4 words of 8 bf16 weights in natural order, x staged alike
+        float acc = 0.0f;
+#pragma unroll
+        for (int m = 0; m < 8; ++m) {
+            const uint4 xv = xu[m];
+            const uint32_t xp[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+            for (int z = 0; z < 4; ++z)
+                acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, wd[4 * m + z]),
+                                                      __builtin_bit_cast(bf16x2_t, xp[z]), acc, false);
+        }
+        return acc;
     } else {
         float a0 = 0.0f, a1 = 0.0f;
 #pragma unroll
@@ -1418,13 +1435,13 @@ __global__ __launch_bounds__(kThreads) void k_dec_down_fit(FwdArgs a, const uint
 }
 
 // (SP, UPL) for a row of U units: the fewest lane slots SP * UPL >= U, then the units per lane
-// nearest `pref` (UPL <= 4, SP a power of two <= 64).
-void pick_split(int U, int pref, int& SP, int& UPL) {
+// nearest `pref` (UPL <= max_upl, SP a power of two <= 64).
+void pick_split(int U, int pref, int& SP, int& UPL, int max_upl = 4) {
     int best = 1 << 30, bestd = 1 << 30;
     SP = 64;
     UPL = 1;
     for (int sp = 1; sp <= 64; sp <<= 1)
-        for (int upl = 1; upl <= 4; ++upl) {
+        for (int upl = 1; upl <= max_upl; ++upl) {
             if (sp * upl < U) continue;
             const int cost = sp * upl, dist = upl > pref ? upl - pref : pref - upl;
             if (cost < best || (cost == best && dist < bestd)) { best = cost; bestd = dist; SP = sp; UPL = upl; }
@@ -1542,12 +1559,21 @@ hipError_t launch_down(const FwdArgs& a, uint16_t* hbuf, DecTable* table, int nu
     return hipGetLastError();
 }
 
+// Units per lane a mode's kernels are built for: a bf16 unit is 128 bytes (32 registers), so
+// unquantized rows take at most two units a lane (SP up to 64 covers widths up to 8192).
+template <int MODE>
+constexpr int kMaxUpl = MODE == kModeBf16 ? 2 : 4;
+
 #define BRX_UPL_CASES(FN, ...)                                                   \
     do {                                                                         \
         if (upl_ == 1) return FN<MODE, 1>(__VA_ARGS__);                          \
-        if (upl_ == 2) return FN<MODE, 2>(__VA_ARGS__);                          \
-        if (upl_ == 3) return FN<MODE, 3>(__VA_ARGS__);                          \
-        return FN<MODE, 4>(__VA_ARGS__);                                         \
+        if constexpr (kMaxUpl<MODE> == 2) {                                      \
+            return FN<MODE, 2>(__VA_ARGS__);                                     \
+        } else {                                                                 \
+            if (upl_ == 2) return FN<MODE, 2>(__VA_ARGS__);                      \
+            if (upl_ == 3) return FN<MODE, 3>(__VA_ARGS__);                      \
+            return FN<MODE, 4>(__VA_ARGS__);                                     \
+        }                                                                        \
     } while (0)
 
 template <int MODE>
@@ -1569,12 +1595,16 @@ hipError_t launch_mode(const FwdArgs& a, uint16_t* hbuf, DecTable* table, uint16
         // x once for twice the rows. The split fixes each row's summation order, so both
         // several-token kernels take the same one: a step's rows do not depend on how many
         // pairs share its launch (a pool's span calls against the whole step).
-        pick_split(a.H / 64, a.T > 1 ? 2 : 1, SP, upl_);
+        pick_split(a.H / 64, a.T > 1 && kMaxUpl<MODE> > 2 ? 2 : 1, SP, upl_, kMaxUpl<MODE>);
         hipError_t err;
         if (a.T == 1 && !a.ptok && upl_ <= 3 && a.E <= 256 && nu <= kWave) {
-            err = upl_ == 1   ? launch_gateup1<MODE, 1>(a, hbuf, table, nu, Imax, SP, s)
-                  : upl_ == 2 ? launch_gateup1<MODE, 2>(a, hbuf, table, nu, Imax, SP, s)
-                              : launch_gateup1<MODE, 3>(a, hbuf, table, nu, Imax, SP, s);
+            if constexpr (kMaxUpl<MODE> == 2)
+                err = upl_ == 1 ? launch_gateup1<MODE, 1>(a, hbuf, table, nu, Imax, SP, s)
+                                : launch_gateup1<MODE, 2>(a, hbuf, table, nu, Imax, SP, s);
+            else
+                err = upl_ == 1   ? launch_gateup1<MODE, 1>(a, hbuf, table, nu, Imax, SP, s)
+                      : upl_ == 2 ? launch_gateup1<MODE, 2>(a, hbuf, table, nu, Imax, SP, s)
+                                  : launch_gateup1<MODE, 3>(a, hbuf, table, nu, Imax, SP, s);
         } else if (per_entry) {
             err = [&]() -> hipError_t { BRX_UPL_CASES(launch_gateupT, a, hbuf, table, nu, Imax, SP, s); }();
         } else {
@@ -1586,7 +1616,7 @@ hipError_t launch_mode(const FwdArgs& a, uint16_t* hbuf, DecTable* table, uint16
         int SP, upl_;
         hipError_t err;
         // (the same split for both down kernels, as for gate/up)
-        pick_split(Imax / 64, 3, SP, upl_);
+        pick_split(Imax / 64, kMaxUpl<MODE> > 2 ? 3 : 1, SP, upl_, kMaxUpl<MODE>);
         // several tokens whose h rows are too many for every block to stage them all: one block
         // per (entry, rows), then the combine; otherwise every block stages every pair's h rows
         // and combines in its epilogue

@@ -1,5 +1,5 @@
 // Decode launches for 4-bit affine, MXFP4 and 3-bit affine weights, and the dispatch over every
-// weight mode (the 2-, 6- and 8-bit affine modes are compiled in k_decode_wide.hip).
+// weight mode (2-, 6- and 8-bit affine and bf16 weights are compiled in k_decode_wide.hip).
 #include "dec_kernels.h"
 
 namespace brx {

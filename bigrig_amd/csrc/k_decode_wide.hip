@@ -1,5 +1,5 @@
-// Decode launches for 2-, 6- and 8-bit affine weights (the kernels of dec_kernels.h; a
-// translation unit of its own so the modes compile in parallel).
+// Decode launches for 2-, 6- and 8-bit affine and unquantized bf16 weights (the kernels of
+// dec_kernels.h; a translation unit of its own so the modes compile in parallel).
 #include "dec_kernels.h"
 
 namespace brx {
@@ -13,6 +13,8 @@ hipError_t launch_decode_wide(const FwdArgs& a, void* ws, int phases, hipStream_
             return launch_mode<kModeAffine6>(a, w.hbuf, w.table, w.y_routed, w.y_shared, phases, s);
         case kModeAffine8:
             return launch_mode<kModeAffine8>(a, w.hbuf, w.table, w.y_routed, w.y_shared, phases, s);
+        case kModeBf16:
+            return launch_mode<kModeBf16>(a, w.hbuf, w.table, w.y_routed, w.y_shared, phases, s);
         default:
             return hipErrorInvalidValue;
     }

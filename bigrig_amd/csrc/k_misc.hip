@@ -1,6 +1,6 @@
 // fp32 dequantization of one projection (test hook; replaces mx.dequantize,
 // bigrig_engine/precision.py:186-189). w = s*q + b for affine (s*q exact in fp32, one
-// rounding), w = e2m1(q) * 2^(e-127) for mxfp4.
+// rounding), w = e2m1(q) * 2^(e-127) for mxfp4, the bf16 weight for unquantized experts.
 #include "brx_internal.h"
 
 namespace brx {
@@ -15,6 +15,11 @@ __global__ __launch_bounds__(256) void k_dequant(const uint8_t* __restrict__ bas
     const int row = blockIdx.x;
     const int n_in = P.n_in;
     const uint8_t* wrow = base + P.w + (int64_t)row * (n_in * bits / 8);
+    if constexpr (MODE == BRX_QUANT_NONE) {    // unquantized: the bf16 weights themselves
+        for (int k = threadIdx.x; k < n_in; k += blockDim.x)
+            out[(int64_t)row * n_in + k] = bf2f(reinterpret_cast<const uint16_t*>(wrow)[k]);
+        return;
+    }
     for (int k = threadIdx.x; k < n_in; k += blockDim.x) {
         const int bit = k * bits;
         uint32_t two = wrow[bit >> 3];
@@ -54,6 +59,9 @@ hipError_t launch_dequant(const brx_layer_desc& d, const Layout& L, const uint8_
     if (d.quant_mode == BRX_QUANT_AFFINE)
         hipLaunchKernelGGL(k_dequant<BRX_QUANT_AFFINE>, dim3(P.n_out), dim3(256), 0, s, expert, P,
                            d.scale_dtype == BRX_SCALE_F16 ? 1 : 0, d.bits, d.group_size, out);
+    else if (d.quant_mode == BRX_QUANT_NONE)
+        hipLaunchKernelGGL(k_dequant<BRX_QUANT_NONE>, dim3(P.n_out), dim3(256), 0, s, expert, P, 0,
+                           16, 0, out);
     else
         hipLaunchKernelGGL(k_dequant<BRX_QUANT_MXFP4>, dim3(P.n_out), dim3(256), 0, s, expert, P, 0,
                            4, 32, out);

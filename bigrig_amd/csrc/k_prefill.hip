@@ -19,9 +19,9 @@
 //              bucketed order.  KIND 1 (down):
 //              A = h rows, B = down weights of 256 output columns; the epilogue stores each
 //              pair's bf16 row at its (token, k) position.  A is staged through LDS, B is
-//              dequantized from its packed codes (affine 2-8 bits, MXFP4) straight into MFMA
+//              dequantized from its packed codes (affine 2-8 bits, MXFP4; bf16 as loaded) into MFMA
 //              operand registers; fp32 accumulators (details at the kernel). M tiles are 128
-//              rows (64 for 6- and 8-bit codes).
+//              rows (64 for 6- and 8-bit codes and bf16 weights).
 //   k_combine  out[t] = sum_j w[t,j] * y[t,j] (+ shared_gate[t] * y_shared[t]), k-ordered.
 // Every output element is one MFMA accumulation over K in a fixed K order, so a row's value
 // does not depend on which other pairs share its tile.
@@ -325,6 +325,7 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint3
 //     s 2^24 (exact for any scale below 2^104). piece_pair puts codes i and 4 + i in the two
 //     halves of one register, so a 4-bit piece costs 7 extractions, 8 fma_mix and 4 packs.
 //   MXFP4: the hardware converts two e2m1 codes with the e8m0 scale, exact in bf16.
+//   Unquantized bf16 weights are the operand as loaded.
 template <int MODE>
 __device__ __forceinline__ bf16x8_t dq8(const uint32_t* w, int kk, float s24, float b, float sc) {
     uint32_t o[4];
@@ -339,6 +340,10 @@ __device__ __forceinline__ bf16x8_t dq8(const uint32_t* w, int kk, float s24, fl
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j) o[j] = pk_bf16(v[2 * j], v[2 * j + 1]);
+    } else if constexpr (MODE == kModeBf16) {
+        // unquantized: the piece is 8 bf16 weights, 4 words in natural K order
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[j] = w[4 * kk + j];
     } else {
         const uint32_t q = w[kk];
         o[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q, sc, 0));
@@ -351,13 +356,14 @@ __device__ __forceinline__ bf16x8_t dq8(const uint32_t* w, int kk, float s24, fl
 
 // B words a lane holds per stage (half of a row's 64-code stage segment: 32 codes), and the
 // loads that bring them in (16-byte loads, plus one 8-byte load for 6 bits; one 8- or 12-byte
-// load for 2 and 3 bits).
+// load for 2 and 3 bits; four 16-byte loads for bf16 weights).
 template <int MODE>
 constexpr int kBW = kBits<MODE>;
 template <int MODE>
-constexpr int kBLoads = kBits<MODE> >= 6 ? 2 : 1;
-// M tile height: 128 rows, or 64 for 6- and 8-bit codes, whose B words (48 and 64 registers
-// over the ring) leave no room for the accumulators of a 128-row tile at two blocks per CU
+constexpr int kBLoads = kBits<MODE> == 16 ? 4 : kBits<MODE> >= 6 ? 2 : 1;
+// M tile height: 128 rows, or 64 for 6- and 8-bit codes and bf16 weights, whose B words (48, 64
+// and 128 registers over the ring) leave no room for the accumulators of a 128-row tile at two
+// blocks per CU
 template <int MODE>
 constexpr int kTileRows = kBits<MODE> >= 6 ? 64 : 128;
 
@@ -538,7 +544,7 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
     // loads per wave of an odd stage (A copies, B loads) and of an even stage (+ the scale copies
     // of it and the next stage, unless the tile reads its scales from the table)
     constexpr int NV1 = NA + kNJ * kBLoads<MODE>;
-    constexpr int NV0 = NV1 + (TBL ? 0 : kAffine<MODE> ? 2 : 1);
+    constexpr int NV0 = NV1 + ((TBL || !kScaled<MODE>) ? 0 : kAffine<MODE> ? 2 : 1);
     constexpr int B = kBits<MODE>;
     const bool sh = e >= a.E;
     const int inter = sh ? a.I_sh : a.I;
@@ -632,7 +638,7 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
         // scales: paired, an even stage's slot holds its 16-bit scale (and bias) value in the
         // low half and the next stage's in the high half and an odd stage copies nothing;
         // unpaired, every stage copies its own 16 bits
-        if constexpr (TBL) {
+        if constexpr (TBL || !kScaled<MODE>) {
         } else if (spair) {
             if ((s & 1) == 0) {
                 const int gp = g & ~1;
@@ -666,9 +672,12 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
                 if constexpr (B == 6) {
                     const u32x2_t u = __builtin_amdgcn_raw_buffer_load_b64(rb_rsrc, vbw[nj], go + 16, 0);
                     q[4] = u[0]; q[5] = u[1];
-                } else if constexpr (B == 8) {
-                    const u32x4_t u = __builtin_amdgcn_raw_buffer_load_b128(rb_rsrc, vbw[nj], go + 16, 0);
-                    q[4] = u[0]; q[5] = u[1]; q[6] = u[2]; q[7] = u[3];
+                } else if constexpr (B >= 8) {
+#pragma unroll
+                    for (int l = 1; l < B / 4; ++l) {
+                        const u32x4_t u = __builtin_amdgcn_raw_buffer_load_b128(rb_rsrc, vbw[nj], go + 16 * l, 0);
+                        q[4 * l] = u[0]; q[4 * l + 1] = u[1]; q[4 * l + 2] = u[2]; q[4 * l + 3] = u[3];
+                    }
                 }
             }
         }
@@ -706,6 +715,8 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
                 const uint32_t bv = (*reinterpret_cast<const uint32_t*>(ss + ab + br * 4) >> sh) & 0xFFFFu;
                 f.s[nj] = (F16 ? h2f(sv) : bf2f(sv)) * 16777216.0f;
                 f.b[nj] = F16 ? h2f(bv) : bf2f(bv);
+            } else if constexpr (!kScaled<MODE>) {
+                f.s[nj] = f.b[nj] = 0.f;      // no scales: the slot read above is not used
             } else {
                 f.s[nj] = e8m0_f32((sv >> (8 * kh)) & 0xFFu);
                 f.b[nj] = 0.f;
@@ -875,7 +886,10 @@ void k_pf_gemm(FwdArgs a, const int32_t* __restrict__ order, const int32_t* __re
     const ScalePlan sp = scale_plan<MODE, KIND>(a, sh ? a.lay_sh : a.lay, K, KIND == 0 && a.act == BRX_ACT_SILU_MLP);
 #define BRX_TILE(MF, TBL) \
     pf_tile<MODE, F16, KIND, MF, TBL>(a, order, hbuf, hstride, y_routed, y_shared, ring, dst_s, e, m0, rows, ti.w, nt)
-    if (rows <= 32) {
+    if constexpr (!kScaled<MODE>) {       // bf16 weights: no scales to copy
+        if (rows <= 32) BRX_TILE(2, false);
+        else BRX_TILE(4, false);
+    } else if (rows <= 32) {
         if (tile_lds<MODE>(2, true, sp.pitch) <= kRing) BRX_TILE(2, true);
         else BRX_TILE(2, false);
     } else if (kTileRows<MODE> == 64 || rows <= 64) {
@@ -963,7 +977,9 @@ struct PfWs {
 inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 // The M tile height of a kernel mode (kTileRows on the host).
-inline int tile_rows(int mode) { return mode == kModeAffine6 || mode == kModeAffine8 ? 64 : kBM; }
+inline int tile_rows(int mode) {
+    return mode == kModeAffine6 || mode == kModeAffine8 || mode == kModeBf16 ? 64 : kBM;
+}
 
 PfWs carve(const FwdArgs& a, void* ws) {
     const int P = a.P;
@@ -1069,6 +1085,7 @@ hipError_t launch_prefill(const FwdArgs& a, void* ws, size_t ws_bytes, int phase
         case kModeAffine6: err = BRX_GEMM(kModeAffine6); break;
         case kModeAffine8: err = BRX_GEMM(kModeAffine8); break;
         case BRX_QUANT_MXFP4: err = launch_gemm<BRX_QUANT_MXFP4, false>(a, w, E_ext, Imax, y_routed, phases, s); break;
+        case kModeBf16: err = launch_gemm<kModeBf16, false>(a, w, E_ext, Imax, y_routed, phases, s); break;
         default: err = hipErrorInvalidValue;
     }
 #undef BRX_GEMM

@@ -71,12 +71,14 @@ class QuantSpec:
     (`entry["quant"]`, stream.py:145-149)."""
     bits: int = 4
     group_size: int = 64
-    mode: str = "affine"          # "affine" | "mxfp4"
+    mode: str = "affine"          # "affine" | "mxfp4" | "none" (unquantized bf16 weights)
     scale_dtype: str = "bfloat16"  # affine only: "bfloat16" | "float16"
 
     def __post_init__(self):
-        if self.mode not in ("affine", "mxfp4"):
+        if self.mode not in ("affine", "mxfp4", "none"):
             raise ValueError(f"unknown quant mode {self.mode!r}")
+        if self.mode == "none" and (self.bits != 16 or self.group_size != 0):
+            raise ValueError("unquantized experts are bf16: bits 16, no scale groups")
         if self.mode == "mxfp4" and (self.bits != 4 or self.group_size != 32):
             raise ValueError("mxfp4 is 4-bit with 32-element scale groups")
         if self.mode == "affine" and self.bits not in (2, 3, 4, 5, 6, 8):
@@ -91,7 +93,16 @@ def bytes_per_param(bits: int, group_size: int) -> float:
 
 def projection_spec(n_out: int, n_in: int, q: QuantSpec, has_bias: bool = False) -> dict:
     """{component: {shape, dtype, nbytes}} of one projection W [n_out, n_in], in COMPONENTS
-    order, as the manifest records it (stream.py:133-138)."""
+    order, as the manifest records it (stream.py:133-138). Unquantized (mode "none"): the bf16
+    weight alone (+ bias), no scales -- the tensors an unquantized checkpoint carries
+    (direct.py:110-142)."""
+    if q.mode == "none":
+        spec = {"weight": {"shape": [n_out, n_in], "dtype": "bfloat16"}}
+        if has_bias:
+            spec["bias"] = {"shape": [n_out], "dtype": "bfloat16"}
+        for c in spec.values():
+            c["nbytes"] = int(np.prod(c["shape"])) * DTYPE_SIZE[c["dtype"]]
+        return spec
     if n_in % q.group_size:
         raise ValueError(f"input dim {n_in} is not a multiple of group size {q.group_size}")
     if (n_in * q.bits) % 32:
@@ -316,6 +327,8 @@ def dequantize_mxfp4(wq, scales) -> np.ndarray:
 # --------------------------------------------------------------------------- expert factory
 def dequantize_projection(arrays: dict, proj: str, q: QuantSpec) -> np.ndarray:
     """fp32 dequantized weight [n_out, n_in] of one projection from split_expert() arrays."""
+    if q.mode == "none":
+        return bf16_bits_to_f32(arrays[(proj, "weight")])
     if q.mode == "affine":
         return dequantize_affine(arrays[(proj, "weight")], arrays[(proj, "scales")],
                                  arrays[(proj, "biases")], q.group_size, q.bits, q.scale_dtype)
@@ -331,7 +344,9 @@ def make_expert(rng: np.random.Generator, hidden: int, inter: int, q: QuantSpec,
     for proj in spec:
         n_out, n_in = (inter, hidden) if proj in ("gate_proj", "up_proj", "fc1") else (hidden, inter)
         w = (rng.standard_normal((n_out, n_in), dtype=np.float32) * std).astype(np.float32)
-        if q.mode == "affine":
+        if q.mode == "none":
+            arrays[(proj, "weight")] = f32_to_bf16_bits(w)
+        elif q.mode == "affine":
             wq, s, b = quantize_affine(w, q.group_size, q.bits, q.scale_dtype)
             arrays[(proj, "weight")], arrays[(proj, "scales")], arrays[(proj, "biases")] = wq, s, b
         else:
@@ -380,10 +395,14 @@ class Manifest:
         return d
 
     def quant(self, layer) -> QuantSpec:
+        """The layer's quant record; without one, the tensors decide (direct.py:110-142): no
+        `scales` beside the weights is an unquantized (bf16) layer."""
         e = self.layers[str(layer)]
-        qd = e.get("quant") or {"bits": 4, "group_size": 64, "mode": "affine"}
         spec = e["spec"]
         first = next(iter(spec.values()))
+        if not e.get("quant") and not any("scales" in comps for comps in spec.values()):
+            return QuantSpec(16, 0, "none")
+        qd = e.get("quant") or {"bits": 4, "group_size": 64, "mode": "affine"}
         sd = first.get("scales", {}).get("dtype", "bfloat16")
         if qd.get("mode", "affine") != "affine":
             sd = "bfloat16"
@@ -421,8 +440,9 @@ def pack_blob(path: str, layers: dict, top_k: int | None = None) -> Manifest:
         for li in sorted(layers):
             spec, q, experts = layers[li]
             per = spec_bytes(spec)
-            entry = {"n_experts": len(experts), "spec": spec, "bytes_per_expert": per,
-                     "quant": {"group_size": q.group_size, "bits": q.bits, "mode": q.mode}}
+            entry = {"n_experts": len(experts), "spec": spec, "bytes_per_expert": per}
+            if q.mode != "none":    # an unquantized layer carries no quant record (stream.py:145-149)
+                entry["quant"] = {"group_size": q.group_size, "bits": q.bits, "mode": q.mode}
             man.layers[str(li)] = entry
             for e, b in enumerate(experts):
                 if len(b) != per:

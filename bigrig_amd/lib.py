@@ -13,7 +13,7 @@ from .build import LIB
 
 # ------------------------------------------------------------------ constants (brx.h)
 BRX_OK, BRX_EINVAL, BRX_ESTATE, BRX_EHIP, BRX_ENOMEM, BRX_ERANGE = 0, -1, -2, -3, -4, -5
-QUANT_AFFINE, QUANT_MXFP4 = 0, 1
+QUANT_AFFINE, QUANT_MXFP4, QUANT_NONE = 0, 1, 2
 SCALE_BF16, SCALE_F16 = 0, 1
 ACT_SWIGLU, ACT_SWIGLU_CLAMPED = 0, 1
 ROUTE_SOFTMAX_TOPK, ROUTE_SOFTMAX_TOPK_RENORM, ROUTE_TOPK_SOFTMAX = 0, 1, 2

@@ -10,6 +10,7 @@ _ROUTES = {"softmax_topk": 0, "softmax_topk_renorm": 1, "topk_softmax": 2, "sigm
            "sigmoid_topk_renorm": 4}
 _ACTS = {"swiglu": 0, "swiglu_clamped": 1, "silu_mlp": 2}
 _RDT = {"float32": 0, "bfloat16": 1}
+_QMODES = {"affine": 0, "mxfp4": 1, "none": 2}   # BRX_QUANT_*
 MAX_WIDTH = 8192   # largest hidden / intermediate width libbrx takes
 
 
@@ -100,7 +101,7 @@ class LayerSpec:
         from .lib import LayerDesc
         q = self.quant
         return LayerDesc(self.hidden, self.inter, self.n_experts, self.top_k,
-                         0 if q.mode == "affine" else 1, q.bits, q.group_size,
+                         _QMODES[q.mode], q.bits, q.group_size,
                          1 if q.scale_dtype == "float16" else 0, int(self.has_bias),
                          _ACTS[self.act], self.alpha, self.limit, self.route_mode,
                          _RDT[self.router_dtype], self.shared_inter, self.n_group,
@@ -115,6 +116,10 @@ QWEN3_30B_A3B = LayerSpec(2048, 768, 128, 8, route="softmax_topk_renorm")
 # data/blobs/Qwen3-30B-A3B-3bit.experts.manifest.json, 2,064,384 bytes per expert)
 QWEN3_30B_A3B_3BIT = LayerSpec(2048, 768, 128, 8, route="softmax_topk_renorm",
                                quant=F.QuantSpec(3, 64, "affine", "bfloat16"))
+# unquantized bf16 experts (Qwen3-30B-A3B-bf16, the checkpoint the reference's reader names for
+# the no-quant case, direct.py:110-142): 9,437,184 bytes per expert
+QWEN3_30B_A3B_BF16 = LayerSpec(2048, 768, 128, 8, route="softmax_topk_renorm",
+                               quant=F.QuantSpec(16, 0, "none"))
 E256_SHARED = LayerSpec(2048, 512, 256, 8, route="softmax_topk_renorm", shared_inter=512)
 GPT_OSS_120B = LayerSpec(2880, 2880, 128, 4, quant=F.QuantSpec(4, 32, "mxfp4"), has_bias=True,
                          act="swiglu_clamped", route="topk_softmax")

@@ -95,7 +95,9 @@ def make_layer_experts(spec: LayerSpec, seed: int, std: float = 0.02, device="cu
     for proj in spec.expert_spec(shared):
         n_out, n_in = (inter, spec.hidden) if proj in ("gate_proj", "up_proj", "fc1") else (spec.hidden, inter)
         w = torch.randn((E, n_out, n_in), generator=gen, device=device, dtype=torch.float32) * std
-        if spec.quant.mode == "affine":
+        if spec.quant.mode == "none":
+            parts.append(_bytes(w.to(torch.bfloat16), E))
+        elif spec.quant.mode == "affine":
             wq, s, b = quantize_affine_torch(w, spec.quant.group_size, spec.quant.bits)
             if spec.quant.scale_dtype == "float16":
                 s, b = s.float().half(), b.float().half()

@@ -39,7 +39,7 @@ enum {
 };
 
 /* quant_mode */
-enum { BRX_QUANT_AFFINE = 0, BRX_QUANT_MXFP4 = 1 };
+enum { BRX_QUANT_AFFINE = 0, BRX_QUANT_MXFP4 = 1, BRX_QUANT_NONE = 2 };   /* NONE: bf16 weights */
 /* scale_dtype (affine only) */
 enum { BRX_SCALE_BF16 = 0, BRX_SCALE_F16 = 1 };
 /* act: the expert's activation (stream.py:1164-1169) */
@@ -68,8 +68,8 @@ typedef struct brx_layer_desc {
     int32_t n_experts;     /* E                                                             */
     int32_t top_k;         /* k                                                             */
     int32_t quant_mode;    /* BRX_QUANT_*                                                   */
-    int32_t bits;          /* affine: 2, 3, 4, 6 or 8 (codes LSB first); mxfp4: 4           */
-    int32_t group_size;    /* 64 or 128 (affine) or 32 (mxfp4)                              */
+    int32_t bits;          /* affine: 2, 3, 4, 6 or 8 (codes LSB first); mxfp4: 4; none: 16 */
+    int32_t group_size;    /* 64 or 128 (affine), 32 (mxfp4), 0 (none)                      */
     int32_t scale_dtype;   /* BRX_SCALE_* (affine)                                          */
     int32_t has_bias;      /* projections carry a `bias` [N] bf16 component (gpt-oss)       */
     int32_t act;           /* BRX_ACT_*                                                     */

@@ -92,7 +92,9 @@ def _p(a):
 def orc_layer(spec) -> OrcLayer:
     """OrcLayer from a bigrig_amd.layer.LayerSpec-like object."""
     q = spec.quant
-    return OrcLayer(spec.hidden, spec.inter, 0 if q.mode == "affine" else 1, q.bits, q.group_size,
+    # unquantized (bf16) weights: mode 2; the group size only sets the oracle's summation chunks
+    return OrcLayer(spec.hidden, spec.inter, {"affine": 0, "mxfp4": 1, "none": 2}[q.mode], q.bits,
+                    q.group_size or 64,
                     1 if q.scale_dtype == "float16" else 0, int(spec.has_bias),
                     {"swiglu": 0, "swiglu_clamped": 1, "silu_mlp": 2}[spec.act], spec.alpha,
                     spec.limit)

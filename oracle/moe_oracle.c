@@ -245,7 +245,9 @@ void orc_offsets(const orc_layer* L, int inter, orc_off* o) {
         proj_dims(L, inter, p, &n_out, &n_in);
         int64_t G = n_in / L->gs;
         o->w[p] = pos; pos += (int64_t)n_out * n_in * L->bits / 8;
-        if (L->quant_mode == 0) {
+        if (L->quant_mode == 2) {            /* unquantized bf16: the weight alone */
+            o->s[p] = o->b[p] = -1;
+        } else if (L->quant_mode == 0) {
             o->s[p] = pos; pos += (int64_t)n_out * G * 2;
             o->b[p] = pos; pos += (int64_t)n_out * G * 2;
         } else {
@@ -277,9 +279,16 @@ static inline uint32_t qcode(const uint8_t* wrow, int k, int bits) {
 
 static inline int64_t row_bytes(const orc_layer* L, int n_in) { return (int64_t)n_in * L->bits / 8; }
 
-/* fp32 dequantized projection p: out [n_out, n_in]. */
+/* The layer's quantization is one this restatement takes: affine 2-8 bits, MXFP4 (4 bits), or
+ * unquantized bf16 (mode 2, 16 bits). */
+static int orc_quant_ok(const orc_layer* L) {
+    if (L->quant_mode == 2) return L->bits == 16;
+    return L->bits >= 2 && L->bits <= 8 && (L->quant_mode == 0 || L->bits == 4);
+}
+
+/* fp32 dequantized projection p: out [n_out, n_in] (unquantized: the bf16 values). */
 int orc_dequant(const orc_layer* L, const uint8_t* expert, int inter, int p, float* out) {
-    if (L->bits < 2 || L->bits > 8 || (L->quant_mode != 0 && L->bits != 4)) return -1;
+    if (!orc_quant_ok(L)) return -1;
     orc_off o;
     orc_offsets(L, inter, &o);
     if (o.w[p] < 0) return -1;
@@ -288,6 +297,14 @@ int orc_dequant(const orc_layer* L, const uint8_t* expert, int inter, int p, flo
     int G = n_in / L->gs;
     for (int n = 0; n < n_out; ++n) {
         const uint8_t* wrow = expert + o.w[p] + (int64_t)n * row_bytes(L, n_in);
+        if (L->quant_mode == 2) {
+            for (int k = 0; k < n_in; ++k) {
+                uint16_t v;
+                memcpy(&v, wrow + 2 * k, 2);
+                out[(int64_t)n * n_in + k] = bf2f(v);
+            }
+            continue;
+        }
         for (int k = 0; k < n_in; ++k) {
             uint32_t q = qcode(wrow, k, L->bits);
             int g = k / L->gs;
@@ -319,7 +336,16 @@ static void orc_gemv(const orc_layer* L, const uint8_t* expert, const orc_off* o
         for (int g = 0; g < G; ++g) {
             const float* xg = x + (int64_t)g * gs;
             const uint8_t* wg = wrow + (int64_t)g * gs / 2;
-            if (L->quant_mode == 0) {
+            if (L->quant_mode == 2) {
+                /* unquantized bf16: fp32 sum per chunk of gs, like the scaled modes */
+                float sw = 0.0f;
+                for (int i = 0; i < gs; ++i) {
+                    uint16_t v;
+                    memcpy(&v, wrow + 2 * ((int64_t)g * gs + i), 2);
+                    sw += bf2f(v) * xg[i];
+                }
+                acc += (double)sw;
+            } else if (L->quant_mode == 0) {
                 float sqx = 0.0f, sx = 0.0f;
                 for (int i = 0; i < gs / 2; ++i) {
                     const int k = g * gs + 2 * i;
@@ -381,7 +407,7 @@ int orc_moe_forward(const orc_layer* L, const uint8_t* const* experts, int k,
                     const uint8_t* shared, int shared_inter, const uint16_t* x,
                     const int32_t* idx, const float* w, const float* sgate, int T,
                     uint16_t* out, uint16_t* yun, int nthreads) {
-    if (L->bits < 2 || L->bits > 8 || (L->quant_mode != 0 && L->bits != 4)) return -1;
+    if (!orc_quant_ok(L)) return -1;
     int H = L->H;
     int maxI = L->I > shared_inter ? L->I : shared_inter;
     int P = T * k;

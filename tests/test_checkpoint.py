@@ -129,6 +129,23 @@ def test_routing_rule_follows_the_adapter():
         small(QWEN3_30B_A3B, n_experts=100, n_group=8, topk_group=2)
 
 
+def test_unquantized_checkpoint_layer(tmp_path):
+    """A bf16 checkpoint (expert weights with no scales, config.json with or without a
+    quantization block): the layer is unquantized, its shape comes from the bf16 weight and each
+    expert reads back as the bytes a blob holds."""
+    q = F.QuantSpec(16, 0, "none")
+    for cfg in ({"model_type": "qwen3_moe", "num_experts_per_tok": 2},
+                {"model_type": "qwen3_moe", "num_experts_per_tok": 2, "quantization": {"bits": 4, "group_size": 64}}):
+        d = str(tmp_path / f"bf16_{len(cfg)}")
+        made = make_checkpoint(d, {0: (256, 128, 4, q, False)}, config=cfg, seed=3)
+        man = CK.expert_manifest(d)
+        spec = CK.layer_spec(man, 0)
+        assert spec.quant == q and (spec.hidden, spec.inter, spec.n_experts) == (256, 128, 4)
+        assert spec.bytes_per_expert == 3 * 256 * 128 * 2
+        for e in range(4):
+            assert CK.read_expert(man, 0, e) == made[0][2][e]
+
+
 def test_quantisation_is_decided_by_the_tensors(tmp_path):
     spec = {"gate_proj": {"weight": {}}}
     assert CK.quant_for({"quantization": {"bits": 4, "group_size": 64}}, "x", spec) == {}

@@ -95,6 +95,34 @@ def test_pack_blob_roundtrip(tmp_path):
     assert man.regions == man2.regions
 
 
+def test_unquantized_layout_and_manifest(tmp_path):
+    """Unquantized experts: each projection is its bf16 weight [n_out, n_in] (+ bias), no
+    scales; the layer's manifest entry carries no quant record (stream.py:145-149) and reading
+    it back, the tensors decide (direct.py:110-142): no scales is the unquantized mode."""
+    rng = np.random.default_rng(5)
+    q = F.QuantSpec(16, 0, "none")
+    spec = F.expert_spec(128, 64, q, has_bias=True)
+    assert spec["gate_proj"] == {"weight": {"shape": [64, 128], "dtype": "bfloat16", "nbytes": 64 * 128 * 2},
+                                 "bias": {"shape": [64], "dtype": "bfloat16", "nbytes": 128}}
+    assert F.spec_bytes(spec) == 3 * 64 * 128 * 2 + 2 * 64 * 2 + 128 * 2
+    experts = [F.make_expert(rng, 128, 64, q, has_bias=True) for _ in range(2)]
+    arrs = F.split_expert(experts[1], spec)
+    w = F.dequantize_projection(arrs, "down_proj", q)
+    assert w.shape == (128, 64) and np.array_equal(w, F.bf16_bits_to_f32(arrs[("down_proj", "weight")]))
+    path = str(tmp_path / "u.experts")
+    F.pack_blob(path, {0: (spec, q, experts)}, top_k=2)
+    man = F.Manifest.load(path)
+    assert "quant" not in man.layers["0"] and man.quant(0) == q
+    # a layer with scales but no quant record keeps the 4-bit default
+    q4 = F.QuantSpec()
+    F.pack_blob(path, {0: (F.expert_spec(128, 64, q4), q4, [F.make_expert(rng, 128, 64, q4)])})
+    d = json.load(open(path + ".manifest.json"))
+    del d["layers"]["0"]["quant"]
+    assert F.Manifest.from_dict(d).quant(0) == q4
+    with pytest.raises(ValueError):
+        F.QuantSpec(16, 64, "none")
+
+
 @pytest.mark.parametrize("bits", [2, 3, 4, 5, 6, 8])
 def test_pack_unpack_roundtrip(bits):
     rng = np.random.default_rng(bits)

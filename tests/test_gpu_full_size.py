@@ -12,7 +12,9 @@ The sizes: Qwen3-30B-A3B shape (hidden 2048, 128 experts, top-8, inter 768, 4-bi
 experts, top-4, inter 2880, MXFP4 + biases, clamped SwiGLU) for a 512-token chunk and one
 decode token; 256 experts + shared expert (inter 512) at batch 8 and batch 1; the OLMoE-1B-7B
 layer (hidden 2048, 64 experts, inter 1024, fp32 router, softmax top-8 without renormalisation)
-at batch 1 and 8. The Qwen3 and 256-expert routers carry the Zipf(1.1) bias, the others none.
+at batch 1 and 8; the Qwen3 shape with unquantized bf16 experts (Qwen3-30B-A3B-bf16, 9.4 MB per
+expert) for a 2048-token chunk and decode at batch 1 and 8. The Qwen3 and 256-expert routers
+carry the Zipf(1.1) bias, the others none.
 """
 import numpy as np
 import pytest
@@ -20,7 +22,7 @@ import pytest
 import oracle
 from bigrig_amd import formats as F
 from bigrig_amd import layer as ops
-from bigrig_amd.spec import E256_SHARED, GPT_OSS_120B, OLMOE_1B_7B, QWEN3_30B_A3B
+from bigrig_amd.spec import E256_SHARED, GPT_OSS_120B, OLMOE_1B_7B, QWEN3_30B_A3B, QWEN3_30B_A3B_BF16
 from tests.gpu_util import per_token_rel_l2, tile_edge_tokens
 
 pytestmark = pytest.mark.gpu
@@ -35,7 +37,7 @@ def _bits(t):
 
 # the configurations with a Zipf-biased router (Qwen3-30B-A3B shape and the 256-expert layer);
 # the OLMoE and gpt-oss layers route on the plain logits
-ZIPF = {QWEN3_30B_A3B: 1.1, E256_SHARED: 1.1}
+ZIPF = {QWEN3_30B_A3B: 1.1, E256_SHARED: 1.1, QWEN3_30B_A3B_BF16: 1.1}
 
 
 def _layer(spec, seed):
@@ -66,10 +68,12 @@ def _layer(spec, seed):
 
 @pytest.mark.parametrize("spec,T", [(QWEN3_30B_A3B, 2048), (QWEN3_30B_A3B, 1), (GPT_OSS_120B, 512),
                                     (GPT_OSS_120B, 1), (E256_SHARED, 8), (E256_SHARED, 1),
-                                    (OLMOE_1B_7B, 1), (OLMOE_1B_7B, 8)],
+                                    (OLMOE_1B_7B, 1), (OLMOE_1B_7B, 8), (QWEN3_30B_A3B_BF16, 2048),
+                                    (QWEN3_30B_A3B_BF16, 1), (QWEN3_30B_A3B_BF16, 8)],
                          ids=["qwen3-prefill2048", "qwen3-decode1", "gptoss-prefill512",
                               "gptoss-decode1", "e256shared-decode8", "e256shared-decode1",
-                              "olmoe-decode1", "olmoe-decode8"])
+                              "olmoe-decode1", "olmoe-decode8", "qwen3bf16-prefill2048",
+                              "qwen3bf16-decode1", "qwen3bf16-decode8"])
 def test_full_size_layer(gpu, spec, T):
     import torch
 

@@ -8,11 +8,11 @@ import pytest
 
 from bigrig_amd import formats as F
 from bigrig_amd import lib as L
-from bigrig_amd.spec import E256_SHARED, GPT_OSS_120B, OLMOE_1B_7B, QWEN3_30B_A3B
+from bigrig_amd.spec import E256_SHARED, GPT_OSS_120B, OLMOE_1B_7B, QWEN3_30B_A3B, QWEN3_30B_A3B_BF16
 
 HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include",
                       "brx.h")
-SPECS = [OLMOE_1B_7B, QWEN3_30B_A3B, E256_SHARED, GPT_OSS_120B]
+SPECS = [OLMOE_1B_7B, QWEN3_30B_A3B, E256_SHARED, GPT_OSS_120B, QWEN3_30B_A3B_BF16]
 
 
 def _declared():
@@ -66,7 +66,7 @@ def test_expert_layout_matches_formats(spec):
     assert out.bytes_per_expert == F.spec_bytes(es) == spec.bytes_per_expert
     for p, proj in enumerate(F.PROJECTIONS):
         assert out.weight[p] == offs[(proj, "weight")]
-        assert out.scales[p] == offs[(proj, "scales")]
+        assert out.scales[p] == offs.get((proj, "scales"), -1)
         assert out.biases[p] == offs.get((proj, "biases"), -1)
         assert out.bias[p] == offs.get((proj, "bias"), -1)
     if spec.shared_inter:
@@ -124,6 +124,21 @@ def test_every_affine_width_is_accepted_with_the_packed_layout(bits, group):
             assert out.weight[p] == offs[(proj, "weight")]
             assert out.scales[p] == offs[(proj, "scales")]
             assert out.biases[p] == offs[(proj, "biases")]
+
+
+def test_unquantized_descriptor_rules():
+    """Unquantized experts are bf16 with no scale groups: bits 16 and group_size 0, nothing else."""
+    lib = L.load()
+    out = L.ExpertLayout()
+    d = QWEN3_30B_A3B_BF16.desc()
+    assert (d.quant_mode, d.bits, d.group_size) == (L.QUANT_NONE, 16, 0)
+    L.check(lib.brx_expert_layout_get(C.byref(d), 0, C.byref(out)))
+    assert out.bytes_per_expert == 3 * 2048 * 768 * 2 and out.scales[0] == out.biases[0] == -1
+    for field, value in (("bits", 4), ("group_size", 64)):
+        d = QWEN3_30B_A3B_BF16.desc()
+        setattr(d, field, value)
+        assert lib.brx_expert_layout_get(C.byref(d), 0, C.byref(out)) == L.BRX_EINVAL
+        assert "unquantized experts are bf16" in lib.brx_last_error().decode()
 
 
 def test_group_of_128_needs_widths_it_divides():

@@ -276,12 +276,16 @@ def test_group_rule_reductions():
 @pytest.mark.parametrize("q", [F.QuantSpec(4, 64, "affine", "bfloat16"),
                                F.QuantSpec(4, 64, "affine", "float16"),
                                F.QuantSpec(4, 32, "mxfp4"),
-                               F.QuantSpec(3, 64, "affine", "bfloat16")],
-                         ids=["bf16", "f16", "mxfp4", "3bit"])
+                               F.QuantSpec(3, 64, "affine", "bfloat16"),
+                               F.QuantSpec(2, 128, "affine", "bfloat16"),
+                               F.QuantSpec(6, 64, "affine", "float16"),
+                               F.QuantSpec(8, 64, "affine", "bfloat16"),
+                               F.QuantSpec(16, 0, "none")],
+                         ids=["bf16", "f16", "mxfp4", "3bit", "2bit-g128", "6bit-f16", "8bit", "unquantized"])
 def test_c_dequant_equals_numpy_bitwise(q):
     """The C dequant and formats.dequantize_projection (pinned by closed form in test_formats)
     agree bit for bit, projection by projection."""
-    base = QWEN3_30B_A3B if q.mode == "affine" else GPT_OSS_120B
+    base = GPT_OSS_120B if q.mode == "mxfp4" else QWEN3_30B_A3B
     spec = small(base, hidden=256, inter=128, quant=q)
     rng = np.random.default_rng(11)
     blob = F.make_expert(rng, 256, 128, q, has_bias=spec.has_bias)
@@ -302,6 +306,8 @@ LAYER_SPECS = {
     "mlp": small(QWEN3_30B_A3B, hidden=256, inter=128, n_experts=16, top_k=4, act="silu_mlp"),
     "3bit": small(QWEN3_30B_A3B, hidden=256, inter=128, n_experts=16, top_k=4,
                   quant=F.QuantSpec(3, 64, "affine", "bfloat16")),
+    "unquantized": small(E256_SHARED, hidden=256, inter=128, n_experts=16, top_k=4, shared_inter=128,
+                         quant=F.QuantSpec(16, 0, "none")),
 }
 
 
@@ -379,6 +385,32 @@ def test_single_expert_is_a_swiglu_mlp_torch():
     bad2 = ((torch.nn.functional.silu(xt @ Bg.T) * (xt @ Bu.T)).to(torch.bfloat16).float()
             @ Bd.T).numpy()
     assert oracle.rel_l2(got, bad2) > 5e-2
+
+
+def test_unquantized_single_expert_is_a_swiglu_mlp_torch():
+    """Unquantized (bf16) experts, k=1 with weight 1: the plain SwiGLU MLP on the bf16 weights
+    themselves (the mx.gather_mm branch, stream.py:1626-1628), torch fp32; the weights are the
+    packed bytes read as bf16 (a planted byte swap of each weight fails the same tolerance)."""
+    import torch
+    q = F.QuantSpec(16, 0, "none")
+    spec = small(QWEN3_30B_A3B, hidden=256, inter=128, n_experts=4, top_k=1, quant=q)
+    lay = make_layer(spec, seed=36)
+    assert len(lay.experts[0]) == 3 * 256 * 128 * 2
+    x = make_x(7, spec.hidden, seed=37)
+    e = 3
+    out, _ = oracle.moe_forward(spec, lay.experts, x, np.full((7, 1), e), np.ones((7, 1)))
+    raw = np.frombuffer(lay.experts[e], np.uint16)
+    Wg, Wu, Wd = (torch.from_numpy(F.bf16_bits_to_f32(raw[i * 256 * 128:(i + 1) * 256 * 128])
+                                   .reshape(s)) for i, s in enumerate([(128, 256), (128, 256), (256, 128)]))
+    xt = torch.from_numpy(F.bf16_bits_to_f32(x))
+    h = (torch.nn.functional.silu(xt @ Wg.T) * (xt @ Wu.T)).to(torch.bfloat16).float()
+    got = F.bf16_bits_to_f32(out)
+    assert oracle.rel_l2(got, (h @ Wd.T).numpy()) < 5e-3
+    swapped = [torch.from_numpy(F.bf16_bits_to_f32(F.f32_to_bf16_bits(W.numpy()).byteswap()))
+               for W in (Wg, Wu, Wd)]
+    bad = ((torch.nn.functional.silu(xt @ swapped[0].T) * (xt @ swapped[1].T)).to(torch.bfloat16).float()
+           @ swapped[2].T).numpy()
+    assert not np.isfinite(bad).all() or oracle.rel_l2(got, bad) > 5e-2
 
 
 def test_single_two_layer_expert_is_a_silu_mlp_torch():
