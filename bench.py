@@ -529,15 +529,16 @@ def config_report(args):
     return rep
 
 
-# affine widths of the reference's per-layer precision candidates (bigrig_engine/precision.py:58)
-WIDTHS = [(2, 128), (2, 64), (3, 128), (3, 64), (4, 128), (4, 64), (6, 64), (8, 64)]
+# affine widths of the reference's per-layer precision candidates (bigrig_engine/precision.py:58),
+# and unquantized bf16 experts (16, 0)
+WIDTHS = [(2, 128), (2, 64), (3, 128), (3, 64), (4, 128), (4, 64), (6, 64), (8, 64), (16, 0)]
 
 
 def widths_report():
     """The Qwen3-30B-A3B-shaped layer (Zipf(1.1) router bias, all experts resident) at every
-    affine width and group size: 8 layers (1.4-5.4 GB, beyond the last-level cache), decode at
-    batch 1 (64 steps, fresh inputs) and 2048-token prefill chunks (4-bit g64 is the headline
-    layer, measured here in the same way as the others)."""
+    affine width and group size, and with bf16 experts: 8 layers (1.4-9.7 GB, beyond the
+    last-level cache), decode at batch 1 (64 steps, fresh inputs) and 2048-token prefill
+    chunks (4-bit g64 is the headline layer, measured here in the same way as the others)."""
     from dataclasses import replace
 
     import torch
@@ -546,11 +547,12 @@ def widths_report():
     from bigrig_amd.spec import QWEN3_30B_A3B
     rep = {}
     for b_, g_ in WIDTHS:
-        spec = replace(QWEN3_30B_A3B, quant=F.QuantSpec(b_, g_))
+        q = F.QuantSpec(16, 0, "none") if b_ == 16 else F.QuantSpec(b_, g_)
+        spec = replace(QWEN3_30B_A3B, quant=q)
         st = Stack(spec, 8, bank=64)
         dec = decode_report(st, 1, steps=64)
         pf = prefill_report(st, 2048, reps=3)
-        rep[f"{b_}bit_g{g_}"] = {
+        rep["bf16" if b_ == 16 else f"{b_}bit_g{g_}"] = {
             "bytes_per_expert": spec.bytes_per_expert,
             "decode_us_per_layer": dec["us_per_layer"], "decode_hbm_frac": dec["hbm_frac"],
             "prefill_us_per_layer": pf["us_per_layer"], "prefill_mfma_frac": pf["mfma_frac"]}
