@@ -276,7 +276,9 @@ static_assert(kNS % 2 == 0, "the paired scale copies follow stage parity through
 // The block's LDS: the ring (A stages, per-stage scale slots or the scale table, then the output
 // tile) takes all of a CU's 160 KB that two blocks can share, less the down kernel's row list.
 constexpr int kRing = 80 * 1024 - kBM * 4;
+constexpr int kBPairLds = 16 * 1024;   // paired-B staging of 32-row tiles, at the ring's end
 static_assert(kNS * kStage <= kRing, "the per-stage ring must fit");
+static_assert(kNS * (2 * 16 * kBK * 2 + kStS) + kBPairLds <= kRing, "a 32-row tile's ring and B staging must fit");
 static_assert(8 * 16 * (kBlockN + 8) * 2 <= kRing, "the widest output tile must fit in the ring");
 
 typedef __attribute__((address_space(3))) void* LDS_PTR;
@@ -545,6 +547,11 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
     // of it and the next stage, unless the tile reads its scales from the table)
     constexpr int NV1 = NA + kNJ * kBLoads<MODE>;
     constexpr int NV0 = NV1 + ((TBL || !kScaled<MODE>) ? 0 : kAffine<MODE> ? 2 : 1);
+    // A (and scale) copies alone, of an even and an odd stage
+    constexpr int NVA1 = NA;
+    constexpr int NVA0 = NV0 - kNJ * kBLoads<MODE>;
+    // 32-row tiles of 4-bit codes (affine or MXFP4) read B by stage pairs (below)
+    constexpr bool BPAIR = MF == 2 && kBW<MODE> == 4;
     constexpr int B = kBits<MODE>;
     const bool sh = e >= a.E;
     const int inter = sh ? a.I_sh : a.I;
@@ -627,8 +634,8 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
     struct BReg {
         uint32_t w[kNJ][kBW<MODE>];
     };
-    // issue every load of stage s: A and scale copies into ring slot s % NS, B into `br`
-    auto issue = [&](int s, BReg& br) __attribute__((always_inline)) {
+    // issue the A and scale copies of stage s into ring slot s % NS
+    auto issue_a = [&](int s) __attribute__((always_inline)) {
         const int g = min(s, nsteps - 1);
         uint8_t* st = ring + (s % NS) * SS;
 #pragma unroll
@@ -655,7 +662,11 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(rb_rsrc, (LDS_PTR)(st + SA + 1024 + wv * 256), 2,
                                                          vsc, bo + (g >> gs) * 2, 0, 0);
         }
-        // the lane's half of the stage segment: 4 B bytes (kBLoads loads per fragment)
+    };
+    // issue the B loads of stage s into `br`: the lane's half of the stage segment, 4 B bytes
+    // (kBLoads loads per fragment)
+    auto issue_b = [&](int s, BReg& br) __attribute__((always_inline)) {
+        const int g = min(s, nsteps - 1);
 #pragma unroll
         for (int nj = 0; nj < kNJ; ++nj) {
             uint32_t* q = br.w[nj];
@@ -800,16 +811,122 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
         }
         asm volatile("" ::: "memory");
     }
-    BReg bq[NS];
-#pragma unroll
-    for (int t = 0; t < NS - 1; ++t) {
-        issue(t, bq[t]);
-        asm volatile("" ::: "memory");
-    }
-    dma_wait_barrier<loads_after(NS, NV0, NV1, 0)>();
     bf16x8_t bop0[kNJ], bop1[kNJ];
     bf16x8_t a0[MR], a1[MR];
     SReg sc, sn;
+    if constexpr (BPAIR) {
+        // ---- B by stage pairs (32-row tiles of 4-bit codes): a load instruction reads 16 rows x
+        // 64 contiguous bytes (lane L: row 16 h + L / 4 of the fragment, bytes [64 q + 16 (L % 4),
+        // + 16) of stage pair q) instead of 32 rows x 32 bytes, and ds_bpermute hands each lane
+        // the 16 bytes the MFMA operand layout gives it: stage 2q + t, half kh of row l32 is piece
+        // 2 t + kh, in lane 4 (l32 % 16) + 2 t + kh of row half l32 / 16. The MFMA operands, and
+        // so every output bit, are those of the per-stage loads. Pairs rotate through three
+        // register sets; pair q is requested at stage 2q - 4, with the A copies of stage 2q - 1.
+        const int npairs = (nsteps + 1) / 2;
+        struct PReg {
+            u32x4_t w[kNJ][2];
+        };
+        uint32_t vbp[kNJ][2];
+#pragma unroll
+        for (int nj = 0; nj < kNJ; ++nj)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int fr = KIND == 0 ? nj * 128 + wv * 32 : wv * 64 + nj * 32;   // fragment's first row
+                const int pj = KIND == 0 ? (mlp ? 0 : nj) : 2;
+                vbp[nj][h] = (uint32_t)L.p[pj].w + (uint32_t)mat_row(fr + 16 * h + (lane >> 2)) * (uint32_t)(K / 2) +
+                             (uint32_t)(lane & 3) * 16u;
+            }
+        auto issue_bp = [&](int q, PReg& pr) __attribute__((always_inline)) {
+            const int qq = min(q, npairs - 1);
+#pragma unroll
+            for (int nj = 0; nj < kNJ; ++nj)
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+                    pr.w[nj][h] = __builtin_amdgcn_raw_buffer_load_b128(rb_rsrc, vbp[nj][h], qq * 64, 0);
+        };
+        // the wave's pair goes through a 4 KB LDS area ([nj][row half][lane] x 16 bytes): written
+        // once a pair, read back in the operand layout once a stage (same wave, in order)
+        uint8_t* const bst = ring + kRing - kBPairLds + wv * (kBPairLds / kGemmWaves);
+        auto stash = [&](const PReg& pr) __attribute__((always_inline)) {
+#pragma unroll
+            for (int nj = 0; nj < kNJ; ++nj)
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+                    *reinterpret_cast<u32x4_t*>(bst + ((nj * 2 + h) * 64 + lane) * 16) = pr.w[nj][h];
+        };
+        const int srow = ((l32 >> 4) * 64 + 4 * (l32 & 15) + kh) * 16;   // piece (0, kh) of row l32
+        auto fetch_b = [&](int t, BReg& out) __attribute__((always_inline)) {
+#pragma unroll
+            for (int nj = 0; nj < kNJ; ++nj) {
+                const u32x4_t v = *reinterpret_cast<const u32x4_t*>(bst + nj * 2 * 64 * 16 + srow + 32 * t);
+#pragma unroll
+                for (int w = 0; w < 4; ++w) out.w[nj][w] = v[w];
+            }
+        };
+        constexpr int NVBP = kNJ * 2;   // loads of one pair
+        PReg pq[3];
+        BReg bs, bsn;
+        issue_bp(0, pq[0]);
+        issue_bp(1, pq[1]);
+#pragma unroll
+        for (int t = 0; t < NS - 1; ++t) {
+            issue_a(t);
+            asm volatile("" ::: "memory");
+        }
+        dma_wait_barrier<NVA0>();   // stages 0 and 1: only stage 2's copies follow theirs
+        fetch_s(sc, 0);
+        stash(pq[0]);
+        fetch_b(0, bs);
+        deq(bop0, bs, sc, 0);
+        lda(0, 0, a0);
+        for (int s0 = 0; s0 < nsteps; s0 += 6) {
+#pragma unroll
+            for (int u = 0; u < 6; ++u) {
+                const int s = s0 + u;
+                if (s >= nsteps) break;
+                // stage s + 1's copies landed in every wave: after them come iteration s - 1's
+                // (B of pair (s + 3) / 2 when s - 1 is even, then A of stage s + 2), as far as
+                // they were issued
+                if (s + 2 < nsteps) {
+                    if (u & 1) {
+                        if ((s + 3) / 2 < npairs) dma_wait_barrier<NVBP + NVA1>();
+                        else dma_wait_barrier<NVA1>();
+                    } else {
+                        dma_wait_barrier<NVA0>();
+                    }
+                } else {
+                    dma_wait_barrier<0>();
+                }
+                if (!(u & 1) && s / 2 + 2 < npairs) issue_bp(s / 2 + 2, pq[((u >> 1) + 2) % 3]);
+                if (s + NS - 1 < nsteps) issue_a(s + NS - 1);
+                fetch_s(sn, s + 1);
+                lda(s, 1, a1);
+                mma(a0, bop0);
+                deq(bop1, bs, sc, 1);
+                lda(s, 2, a0);
+                mma(a1, bop1);
+                deq(bop0, bs, sc, 2);
+                lda(s, 3, a1);
+                mma(a0, bop0);
+                deq(bop1, bs, sc, 3);
+                lda(min(s + 1, nsteps - 1), 0, a0);
+                mma(a1, bop1);
+                if (u & 1) stash(pq[((u + 1) >> 1) % 3]);   // stage s + 1 starts a pair
+                fetch_b((u + 1) & 1, bsn);
+                deq(bop0, bsn, sn, 0);
+                bs = bsn;
+                sc = sn;
+            }
+        }
+    } else {
+    BReg bq[NS];
+#pragma unroll
+    for (int t = 0; t < NS - 1; ++t) {
+        issue_a(t);
+        issue_b(t, bq[t]);
+        asm volatile("" ::: "memory");
+    }
+    dma_wait_barrier<loads_after(NS, NV0, NV1, 0)>();
     fetch_s(sc, 0);
     deq(bop0, bq[0], sc, 0);
     lda(0, 0, a0);
@@ -831,7 +948,10 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
             } else {
                 dma_wait_barrier<0>();
             }
-            if (s + NS - 1 < nsteps) issue(s + NS - 1, bq[(u + NS - 1) % NS]);
+            if (s + NS - 1 < nsteps) {
+                issue_a(s + NS - 1);
+                issue_b(s + NS - 1, bq[(u + NS - 1) % NS]);
+            }
             fetch_s(sn, s + 1);
             lda(s, 1, a1);
             mma(a0, bop0);
@@ -847,6 +967,7 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
             deq(bop0, bq[(u + 1) % NS], sn, 0);
             sc = sn;
         }
+    }
     }
 
     // ---- epilogue: the output tile goes through LDS (the ring, once every copy into it has
@@ -890,7 +1011,9 @@ void k_pf_gemm(FwdArgs a, const int32_t* __restrict__ order, const int32_t* __re
         if (rows <= 32) BRX_TILE(2, false);
         else BRX_TILE(4, false);
     } else if (rows <= 32) {
-        if (tile_lds<MODE>(2, true, sp.pitch) <= kRing) BRX_TILE(2, true);
+        // (32-row tiles of 4-bit codes also keep kBPairLds for their paired B loads)
+        constexpr int stage_b = kBW<MODE> == 4 ? kBPairLds : 0;
+        if (tile_lds<MODE>(2, true, sp.pitch) + stage_b <= kRing) BRX_TILE(2, true);
         else BRX_TILE(2, false);
     } else if (kTileRows<MODE> == 64 || rows <= 64) {
         if (tile_lds<MODE>(4, true, sp.pitch) <= kRing) BRX_TILE(4, true);
