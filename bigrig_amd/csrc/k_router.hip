@@ -344,14 +344,18 @@ hipError_t launch_router(const brx_layer_desc& d, const void* x, const void* w_r
     }
     // many tokens: logits by token tiles, then the same top-k kernel
     // rows per block: 32 (each weight row read once per 16-token tile, by one wave), fewer
-    // when there are too few token tiles for about 512 blocks (a wave then takes fewer rows)
+    // when there are too few token tiles for one round of blocks over the 256 CUs (a wave then
+    // takes fewer rows; every block stages its token tile, so a second round would stage it
+    // again for no more work in flight). Blocks per CU: as many staged tiles as fit in a CU's
+    // 160 KB (two at H 2048, one at H 2880)
     constexpr int TT = 16;
     const int rows = d.n_experts + (sgw ? 1 : 0);
     const int tiles = (T + TT - 1) / TT;
-    int RPB = 32;
-    while (RPB > 4 && tiles * ((rows + RPB - 1) / RPB) < 512) RPB /= 2;
-    dim3 grid(tiles, (rows + RPB - 1) / RPB);
     const size_t lds = sizeof(uint16_t) * (size_t)TT * d.hidden;
+    const int per_cu = (int)(kMaxBlockLds / lds) < 2 ? 1 : 2;
+    int RPB = 32;
+    while (RPB > 4 && tiles * ((rows + RPB - 1) / RPB) < 256 * per_cu) RPB /= 2;
+    dim3 grid(tiles, (rows + RPB - 1) / RPB);
     const float* lbias = d.route_mode >= BRX_ROUTE_SIGMOID_TOPK ? nullptr : bias;
     if (f32)
         hipLaunchKernelGGL((k_router_tiled<true, TT>), grid, dim3(kRouterThreads), lds, s, (const uint16_t*)x,
