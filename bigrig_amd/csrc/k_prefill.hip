@@ -277,6 +277,7 @@ static_assert(kNS % 2 == 0, "the paired scale copies follow stage parity through
 // tile) takes all of a CU's 160 KB that two blocks can share, less the down kernel's row list.
 constexpr int kRing = 80 * 1024 - kBM * 4;
 constexpr int kBPairLds = 16 * 1024;   // paired-B staging of 32-row tiles, at the ring's end
+constexpr int kBPairSets = 3;          // paired-B register sets (pairs in flight + the current)
 static_assert(kNS * kStage <= kRing, "the per-stage ring must fit");
 static_assert(kNS * (2 * 16 * kBK * 2 + kStS) + kBPairLds <= kRing, "a 32-row tile's ring and B staging must fit");
 static_assert(8 * 16 * (kBlockN + 8) * 2 <= kRing, "the widest output tile must fit in the ring");
@@ -820,8 +821,9 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
         // + 16) of stage pair q) instead of 32 rows x 32 bytes, and ds_bpermute hands each lane
         // the 16 bytes the MFMA operand layout gives it: stage 2q + t, half kh of row l32 is piece
         // 2 t + kh, in lane 4 (l32 % 16) + 2 t + kh of row half l32 / 16. The MFMA operands, and
-        // so every output bit, are those of the per-stage loads. Pairs rotate through three
-        // register sets; pair q is requested at stage 2q - 4, with the A copies of stage 2q - 1.
+        // so every output bit, are those of the per-stage loads. Pairs rotate through NPS
+        // register sets; pair q is requested at stage 2q - 2 (NPS - 1), before that stage's A
+        // copies.
         const int npairs = (nsteps + 1) / 2;
         struct PReg {
             u32x4_t w[kNJ][2];
@@ -864,10 +866,11 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
             }
         };
         constexpr int NVBP = kNJ * 2;   // loads of one pair
-        PReg pq[3];
+        constexpr int NPS = kBPairSets;
+        PReg pq[NPS];
         BReg bs, bsn;
-        issue_bp(0, pq[0]);
-        issue_bp(1, pq[1]);
+#pragma unroll
+        for (int q = 0; q < NPS - 1; ++q) issue_bp(q, pq[q]);
 #pragma unroll
         for (int t = 0; t < NS - 1; ++t) {
             issue_a(t);
@@ -879,17 +882,17 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
         fetch_b(0, bs);
         deq(bop0, bs, sc, 0);
         lda(0, 0, a0);
-        for (int s0 = 0; s0 < nsteps; s0 += 6) {
+        for (int s0 = 0; s0 < nsteps; s0 += 2 * NPS) {
 #pragma unroll
-            for (int u = 0; u < 6; ++u) {
+            for (int u = 0; u < 2 * NPS; ++u) {
                 const int s = s0 + u;
                 if (s >= nsteps) break;
                 // stage s + 1's copies landed in every wave: after them come iteration s - 1's
-                // (B of pair (s + 3) / 2 when s - 1 is even, then A of stage s + 2), as far as
-                // they were issued
+                // (B of pair (s - 1) / 2 + NPS - 1 when s - 1 is even, then A of stage s + 2), as
+                // far as they were issued
                 if (s + 2 < nsteps) {
                     if (u & 1) {
-                        if ((s + 3) / 2 < npairs) dma_wait_barrier<NVBP + NVA1>();
+                        if ((s - 1) / 2 + NPS - 1 < npairs) dma_wait_barrier<NVBP + NVA1>();
                         else dma_wait_barrier<NVA1>();
                     } else {
                         dma_wait_barrier<NVA0>();
@@ -897,7 +900,8 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
                 } else {
                     dma_wait_barrier<0>();
                 }
-                if (!(u & 1) && s / 2 + 2 < npairs) issue_bp(s / 2 + 2, pq[((u >> 1) + 2) % 3]);
+                if (!(u & 1) && s / 2 + NPS - 1 < npairs)
+                    issue_bp(s / 2 + NPS - 1, pq[((u >> 1) + NPS - 1) % NPS]);
                 if (s + NS - 1 < nsteps) issue_a(s + NS - 1);
                 fetch_s(sn, s + 1);
                 lda(s, 1, a1);
@@ -911,7 +915,7 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
                 deq(bop1, bs, sc, 3);
                 lda(min(s + 1, nsteps - 1), 0, a0);
                 mma(a1, bop1);
-                if (u & 1) stash(pq[((u + 1) >> 1) % 3]);   // stage s + 1 starts a pair
+                if (u & 1) stash(pq[((u + 1) >> 1) % NPS]);   // stage s + 1 starts a pair
                 fetch_b((u + 1) & 1, bsn);
                 deq(bop0, bsn, sn, 0);
                 bs = bsn;
