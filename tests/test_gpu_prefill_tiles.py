@@ -165,3 +165,36 @@ def test_small_layer_rows_independent_of_tiles(gpu, spec):
     r2 = oracle.rel_l2(F.bf16_bits_to_f32(bits(out)), F.bf16_bits_to_f32(ref))
     assert r2 < TOL, f"block rel L2 {r2:.3e}"
     pool.close()
+
+
+@pytest.mark.parametrize("spec", [
+    small(QWEN3_30B_A3B, hidden=64, inter=64, n_experts=8, top_k=2),
+    small(QWEN3_30B_A3B, hidden=192, inter=192, n_experts=8, top_k=2,
+          quant=F.QuantSpec(4, 32, "mxfp4"), has_bias=True, act="swiglu_clamped", route="topk_softmax"),
+    small(QWEN3_30B_A3B, hidden=128, inter=320, n_experts=8, top_k=2, quant=F.QuantSpec(3, 64, "affine")),
+    small(QWEN3_30B_A3B, hidden=128, inter=64, n_experts=8, top_k=2, quant=F.QuantSpec(8, 64, "affine")),
+    small(QWEN3_30B_A3B, hidden=192, inter=64, n_experts=8, top_k=2, quant=F.QuantSpec(16, 0, "none")),
+], ids=["4bit-K64", "mxfp4-K192", "3bit-K128-I320", "8bit-K64", "bf16-K192"])
+def test_narrow_widths_rows_independent_of_tiles(gpu, spec):
+    """Contractions of one, two and three 64-wide stages (a stage pair cut short by an odd
+    count, a single stage) through every tile height, bit for bit between tile heights and
+    within 1e-2 of the oracle."""
+    T = 600
+    lay = make_layer(spec, seed=91, zipf=4.0)
+    _, _, pool, _ = build_gpu_layer(lay, gpu)
+    import torch
+    pool.g2s_device(torch.cuda.current_stream().cuda_stream)
+    pool.device.sync()
+    x = make_x(T, spec.hidden, seed=92)
+    xd = to_dev_bits(x, gpu)
+    print(f"[tiles] narrow H={spec.hidden} I={spec.inter} {spec.quant.mode} {spec.quant.bits}-bit", flush=True)
+    _, idx, w, _ = oracle.router(x, lay.router, False, lay.bias, spec.top_k, spec.route_mode)
+    whole, split, most = _whole_vs_split(spec, pool, xd, idx)
+    assert most > 128
+    assert np.array_equal(whole, split), \
+        f"{int((whole != split).any(-1).sum())} rows differ between the tile kernels"
+    _, yref = oracle.moe_forward(spec, lay.experts, x, idx, w, want_unreduced=True)
+    nr = idx.size
+    r = oracle.rel_l2(F.bf16_bits_to_f32(whole[:nr]), F.bf16_bits_to_f32(yref.reshape(nr, -1)))
+    assert r < TOL, f"unreduced rows rel L2 {r:.3e}"
+    pool.close()
