@@ -603,33 +603,16 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
-// sum_i c_i x_i over the 8 codes of piece m of `w` (BITS-bit affine), accumulated into acc.
-// xp[i] packs (x_i, x_{i+4}) as bf16x2. Below 8 bits c = 128 + q: the code pair of piece_pair
-// OR'd with 0x43004300 is the bf16 pair (128 + q_i, 128 + q_{i+4}) exactly (q < 128 fills the 7
+// The affine dot product's code values: pair i of piece m of `w` (BITS-bit affine) is the bf16
+// pair (c_i, c_{i+4}) against x packed as (x_i, x_{i+4}). Below 8 bits c = 128 + q: the code pair
+// of piece_pair OR'd with 0x43004300 is (128 + q_i, 128 + q_{i+4}) exactly (q < 128 fills the 7
 // mantissa bits of 128). 8-bit codes do not fit there and take c = q: each code is converted to
 // fp32 (exact) and its upper half kept, exact in bf16 since q has at most 8 significant bits.
 template <int BITS>
 constexpr float kCodeOffset = BITS == 8 ? 0.0f : 128.0f;
-template <int BITS>
-__device__ __forceinline__ float dot8(const uint32_t* w, int m, const uint32_t* xp, float acc) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        uint32_t qp;
-        if constexpr (BITS == 8) {
-            const float c0 = (float)((w[2 * m] >> (8 * i)) & 0xFFu);
-            const float c1 = (float)((w[2 * m + 1] >> (8 * i)) & 0xFFu);
-            qp = (__float_as_uint(c0) >> 16) | (__float_as_uint(c1) & 0xFFFF0000u);
-        } else {
-            qp = piece_pair<BITS>(w, m, i) | 0x43004300u;
-        }
-        acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, qp),
-                                              __builtin_bit_cast(bf16x2_t, xp[i]), acc, false);
-    }
-    return acc;
-}
 
 // Permute 8 natural-order bf16 (4 words: (x0,x1),(x2,x3),(x4,x5),(x6,x7)) into the pair
-// order dot8 expects: (x0,x4),(x1,x5),(x2,x6),(x3,x7).
+// order the affine dot product takes: (x0,x4),(x1,x5),(x2,x6),(x3,x7).
 __device__ __forceinline__ void perm8(const uint32_t in[4], uint32_t out[4]) {
     out[0] = (in[0] & 0xFFFFu) | (in[2] << 16);
     out[1] = (in[0] >> 16) | (in[2] & 0xFFFF0000u);

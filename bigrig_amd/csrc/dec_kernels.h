@@ -260,57 +260,81 @@ __device__ __forceinline__ void units_load(const uint8_t* base, const Proj& P, i
     }
 }
 
+// Piece m of unit j (8 weights) as the 4 bf16 pairs the dot product takes: affine c = 128 + q
+// below 8 bits, c = q at 8 (see kCodeOffset); MXFP4 the hardware's conversion of two e2m1
+// codes; bf16 the weights as stored.
+template <int MODE, int UPL>
+__device__ __forceinline__ void piece_ops(const Units<MODE, UPL>& u, int j, int m, uint32_t (&q)[4]) {
+    const uint32_t* wd = u.w[j];
+    if constexpr (kAffine<MODE>) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if constexpr (kBits<MODE> == 8) {
+                const float c0 = (float)((wd[2 * m] >> (8 * i)) & 0xFFu);
+                const float c1 = (float)((wd[2 * m + 1] >> (8 * i)) & 0xFFu);
+                q[i] = (__float_as_uint(c0) >> 16) | (__float_as_uint(c1) & 0xFFFF0000u);
+            } else {
+                q[i] = piece_pair<kBits<MODE>>(wd, m, i) | 0x43004300u;
+            }
+        }
+    } else if constexpr (MODE == kModeBf16) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) q[i] = wd[4 * m + i];
+    } else {
+        q[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd[m], 1.0f, 0));
+        q[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd[m], 1.0f, 1));
+        q[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd[m], 1.0f, 2));
+        q[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd[m], 1.0f, 3));
+    }
+}
+
+// acc + the 4 pairs of a piece against 16 bytes of staged activations, in order.
+__device__ __forceinline__ float piece_dot(const uint32_t (&q)[4], uint4 xv, float acc) {
+    auto d2 = [](uint32_t w, uint32_t x, float c) __attribute__((always_inline)) {
+        return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w), __builtin_bit_cast(bf16x2_t, x), c,
+                                               false);
+    };
+    acc = d2(q[0], xv.x, acc);
+    acc = d2(q[1], xv.y, acc);
+    acc = d2(q[2], xv.z, acc);
+    return d2(q[3], xv.w, acc);
+}
+
+// MXFP4 units sum their two 32-code groups apart (pieces 0-3 and 4-7).
+template <int MODE>
+constexpr bool kTwoGroups = !kAffine<MODE> && MODE != kModeBf16;
+
+// A unit's value from its piece sums (`hi` over pieces 4-7 for MXFP4, `lo` the rest): affine
+// s lo + (b - c0 s) xsum with c0 the code offset; MXFP4 each group's sum times its e8m0 scale;
+// bf16 the sum as it is.
+template <int MODE, int UPL>
+__device__ __forceinline__ float unit_value(const Units<MODE, UPL>& u, int j, float lo, float hi, float xsum,
+                                            int scale_f16) {
+    if constexpr (kAffine<MODE>) {
+        const float sc = scale_f16 ? h2f(u.s[j]) : bf2f(u.s[j]);
+        const float bi = scale_f16 ? h2f(u.b[j]) : bf2f(u.b[j]);
+        return fmaf(sc, lo, (bi - kCodeOffset<kBits<MODE>> * sc) * xsum);
+    } else if constexpr (MODE == kModeBf16) {
+        return lo;
+    } else {
+        return e8m0_f32(u.s[j] & 0xFFu) * lo + e8m0_f32(u.s[j] >> 8) * hi;
+    }
+}
+
 // Dot of unit j with a staged activation unit `xu` (8 pieces of 16 bytes in LDS) whose sum is
-// `xsum` (affine only). Affine: acc = sum_i c_i x_i with c = 128 + q below 8 bits, c = q at 8
-// (dot8), and the unit's value s acc + (b - c0 s) xsum with c0 the code offset.
+// `xsum` (affine only).
 template <int MODE, int UPL>
 __device__ __forceinline__ float unit_dot(const Units<MODE, UPL>& u, int j, const uint4* xu, float xsum,
                                           int scale_f16) {
-    const uint32_t* wd = u.w[j];
-    if constexpr (kAffine<MODE>) {
-        float acc = 0.0f;
+    float lo = 0.0f, hi = 0.0f;
 #pragma unroll
-        for (int m = 0; m < 8; ++m) {
-            const uint4 xv = xu[m];
-            const uint32_t xp[4] = {xv.x, xv.y, xv.z, xv.w};
-            acc = dot8<kBits<MODE>>(wd, m, xp, acc);
-        }
-        const float sc = scale_f16 ? h2f(u.s[j]) : bf2f(u.s[j]);
-        const float bi = scale_f16 ? h2f(u.b[j]) : bf2f(u.b[j]);
-        return fmaf(sc, acc, (bi - kCodeOffset<kBits<MODE>> * sc) * xsum);
-    } else if constexpr (MODE == kModeBf16) {
-        // unquantized: piece m is 4 words of 8 bf16 weights in natural order, x staged alike
-        float acc = 0.0f;
-#pragma unroll
-        for (int m = 0; m < 8; ++m) {
-            const uint4 xv = xu[m];
-            const uint32_t xp[4] = {xv.x, xv.y, xv.z, xv.w};
-#pragma unroll
-            for (int z = 0; z < 4; ++z)
-                acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, wd[4 * m + z]),
-                                                      __builtin_bit_cast(bf16x2_t, xp[z]), acc, false);
-        }
-        return acc;
-    } else {
-        float a0 = 0.0f, a1 = 0.0f;
-#pragma unroll
-        for (int m = 0; m < 8; ++m) {
-            const uint4 xv = xu[m];
-            const uint32_t xp[4] = {xv.x, xv.y, xv.z, xv.w};
-            const uint32_t v = wd[m];
-            float acc = m < 4 ? a0 : a1;
-            acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(v, 1.0f, 0),
-                                                  __builtin_bit_cast(bf16x2_t, xp[0]), acc, false);
-            acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(v, 1.0f, 1),
-                                                  __builtin_bit_cast(bf16x2_t, xp[1]), acc, false);
-            acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(v, 1.0f, 2),
-                                                  __builtin_bit_cast(bf16x2_t, xp[2]), acc, false);
-            acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(v, 1.0f, 3),
-                                                  __builtin_bit_cast(bf16x2_t, xp[3]), acc, false);
-            if (m < 4) a0 = acc; else a1 = acc;
-        }
-        return e8m0_f32(u.s[j] & 0xFFu) * a0 + e8m0_f32(u.s[j] >> 8) * a1;
+    for (int m = 0; m < 8; ++m) {
+        uint32_t q[4];
+        piece_ops<MODE, UPL>(u, j, m, q);
+        if (kTwoGroups<MODE> && m >= 4) hi = piece_dot(q, xu[m], hi);
+        else lo = piece_dot(q, xu[m], lo);
     }
+    return unit_value<MODE, UPL>(u, j, lo, hi, xsum, scale_f16);
 }
 
 // Sums over aligned groups of 2, 4, 8 and 16 lanes through DPP (quad_perm [1,0,3,2] and
@@ -1345,7 +1369,7 @@ __global__ __launch_bounds__(kThreads) void k_dec_down(FwdArgs a, const uint16_t
 // shapes): each row group reads its item's table row itself, the h rows are staged by pair id,
 // and the item's weights are requested as soon as its slot is known -- two memory round trips
 // in all, no scan and one barrier before the dot products.
-template <int MODE, int UPL>
+template <int MODE, int UPL, int NT>
 __global__ __launch_bounds__(kThreads) void k_dec_down_fit(FwdArgs a, const uint16_t* __restrict__ hbuf,
                                                            int RBD, int hstride,
                                                            const DecTable* __restrict__ table, int lsp,
@@ -1408,14 +1432,34 @@ __global__ __launch_bounds__(kThreads) void k_dec_down_fit(FwdArgs a, const uint
         int ntg = nt;
         ntg = group_max(ntg, SP);
 #pragma unroll
-        for (int i = 0; i < kMaxTok; ++i) {
+        for (int i = 0; i < NT; ++i) {
             if (i >= ntg) break;
             const int hr = min(max(pr[i], 0), PT - 1);
             float p = 0.0f;
 #pragma unroll
             for (int j = 0; j < UPL; ++j) {
                 const int un = sl + SP * j;
-                if (i < nt && un < U) {
+                if constexpr (NT == 1) {
+                    // one pair: each piece's h read sits under the pair test, so the unit's
+                    // reads are not all hoisted ahead of its dots (fewer registers, more waves)
+                    if (un < U) {
+                        const uint4* hu = reinterpret_cast<const uint4*>(hs + ((int64_t)hr * Umax + un) * kXU);
+                        float lo = 0.0f, hi = 0.0f;
+#pragma unroll
+                        for (int m = 0; m < 8; ++m) {
+                            uint32_t q[4];
+                            piece_ops<MODE, UPL>(ud, j, m, q);
+                            if (i < nt) {
+                                if (kTwoGroups<MODE> && m >= 4) hi = piece_dot(q, hu[m], hi);
+                                else lo = piece_dot(q, hu[m], lo);
+                            }
+                        }
+                        if (i < nt) {
+                            const float sx = kAffine<MODE> ? hsum[hr * Umax + un] : 0.0f;
+                            p += unit_value<MODE, UPL>(ud, j, lo, hi, sx, a.scale_f16);
+                        }
+                    }
+                } else if (i < nt && un < U) {
                     const uint4* hu = reinterpret_cast<const uint4*>(hs + ((int64_t)hr * Umax + un) * kXU);
                     const float sx = kAffine<MODE> ? hsum[hr * Umax + un] : 0.0f;
                     p += unit_dot<MODE, UPL>(ud, j, hu, sx, a.scale_f16);
@@ -1536,7 +1580,7 @@ hipError_t launch_downT(const FwdArgs& a, uint16_t* hbuf, DecTable* table, int n
 
 template <int MODE, int UPL>
 hipError_t launch_down(const FwdArgs& a, uint16_t* hbuf, DecTable* table, int nu, int PT, int Imax, int SP,
-                       hipStream_t s) {
+                       bool one_pair, hipStream_t s) {
     // rows per block: enough (entry, row) items to give every row group of the 4 waves one
     const int per_pass = kWaves * (kWave / SP);
     int RBD = 1;
@@ -1551,8 +1595,14 @@ hipError_t launch_down(const FwdArgs& a, uint16_t* hbuf, DecTable* table, int nu
     const size_t ys_b = (((size_t)PT * RBD * 4) + 15) & ~(size_t)15;
     const size_t lds = ys_b + (size_t)hs_bytes + 16;
     if (need <= (size_t)kDownLds)
-        hipLaunchKernelGGL((k_dec_down_fit<MODE, UPL>), dim3((a.H + RBD - 1) / RBD), dim3(kThreads), lds, s, a,
-                           hbuf, RBD, Imax, table, __builtin_ctz(SP), __builtin_ctz(RBD), nu);
+        // (at most NT pairs an entry: one after the one-token gate/up kernel, whose entries are
+        // single pairs; the one-pair form holds fewer registers)
+        if (one_pair)
+            hipLaunchKernelGGL((k_dec_down_fit<MODE, UPL, 1>), dim3((a.H + RBD - 1) / RBD), dim3(kThreads), lds, s,
+                               a, hbuf, RBD, Imax, table, __builtin_ctz(SP), __builtin_ctz(RBD), nu);
+        else
+            hipLaunchKernelGGL((k_dec_down_fit<MODE, UPL, kMaxTok>), dim3((a.H + RBD - 1) / RBD), dim3(kThreads),
+                               lds, s, a, hbuf, RBD, Imax, table, __builtin_ctz(SP), __builtin_ctz(RBD), nu);
     else
         hipLaunchKernelGGL((k_dec_down<MODE, UPL>), dim3((a.H + RBD - 1) / RBD), dim3(kThreads), lds, s, a, hbuf,
                            RBD, Imax, table, __builtin_ctz(SP), __builtin_ctz(RBD), hs_bytes);
@@ -1587,17 +1637,21 @@ hipError_t launch_mode(const FwdArgs& a, uint16_t* hbuf, DecTable* table, uint16
     // in two passes: the plan launch, then one block per (entry, rows). With fewer, every
     // gate/up block ranks and plans the step itself.
     const bool per_entry = a.T > 1 && nu > 2 * kEntryRows;
+    // one token: one unit per lane where the row allows it (twice the waves of two units per
+    // lane, each with half the dequant-dot work and far fewer registers: 11.1 -> 10.2 us per
+    // layer on H = 2048); several tokens: two units per lane, half the blocks, each staging
+    // x once for twice the rows. The split fixes each row's summation order, so both
+    // several-token kernels take the same one: a step's rows do not depend on how many
+    // pairs share its launch (a pool's span calls against the whole step).
+    int SPg, uplg;
+    pick_split(a.H / 64, a.T > 1 && kMaxUpl<MODE> > 2 ? 2 : 1, SPg, uplg, kMaxUpl<MODE>);
+    // the one-token gate/up kernel makes every pair its own entry (pairs given by the caller may
+    // repeat an expert, which the other kernels merge into one entry)
+    const bool one_token = a.T == 1 && !a.ptok && uplg <= 3 && a.E <= 256 && nu <= kWave;
     if (phases & 1) {
-        int SP, upl_;
-        // one token: one unit per lane where the row allows it (twice the waves of two units per
-        // lane, each with half the dequant-dot work and far fewer registers: 11.1 -> 10.2 us per
-        // layer on H = 2048); several tokens: two units per lane, half the blocks, each staging
-        // x once for twice the rows. The split fixes each row's summation order, so both
-        // several-token kernels take the same one: a step's rows do not depend on how many
-        // pairs share its launch (a pool's span calls against the whole step).
-        pick_split(a.H / 64, a.T > 1 && kMaxUpl<MODE> > 2 ? 2 : 1, SP, upl_, kMaxUpl<MODE>);
+        const int SP = SPg, upl_ = uplg;
         hipError_t err;
-        if (a.T == 1 && !a.ptok && upl_ <= 3 && a.E <= 256 && nu <= kWave) {
+        if (one_token) {
             if constexpr (kMaxUpl<MODE> == 2)
                 err = upl_ == 1 ? launch_gateup1<MODE, 1>(a, hbuf, table, nu, Imax, SP, s)
                                 : launch_gateup1<MODE, 2>(a, hbuf, table, nu, Imax, SP, s);
@@ -1624,7 +1678,7 @@ hipError_t launch_mode(const FwdArgs& a, uint16_t* hbuf, DecTable* table, uint16
             uint16_t* yr = a.yun ? a.yun : y_routed;
             err = [&]() -> hipError_t { BRX_UPL_CASES(launch_downT, a, hbuf, table, nu, Imax, SP, yr, y_shared, s); }();
         } else {
-            err = [&]() -> hipError_t { BRX_UPL_CASES(launch_down, a, hbuf, table, nu, PT, Imax, SP, s); }();
+            err = [&]() -> hipError_t { BRX_UPL_CASES(launch_down, a, hbuf, table, nu, PT, Imax, SP, one_token, s); }();
         }
         if (err != hipSuccess) return err;
     }
