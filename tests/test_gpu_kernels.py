@@ -170,6 +170,41 @@ def test_block_forward(gpu, spec, T):
     pool.close()
 
 
+@pytest.mark.parametrize("spec", [SMALL_AFFINE, SMALL_MXFP4], ids=["affine", "mxfp4"])
+def test_one_token_repeated_experts(gpu, spec):
+    """One token whose given pairs repeat experts. brx_moe_forward takes the one-token kernels
+    (every pair its own entry, then the one-pair down kernel); brx_moe_forward_pairs in decode
+    mode, with the pairs' tokens given, merges a repeated expert into one entry of several pairs
+    (the down kernel for several pairs an entry). Both against the oracle pair by pair, and the
+    same bits, since one token fixes one row split."""
+    import torch
+    lay = make_layer(spec, seed=23)
+    _, sw, pool, _ = build_gpu_layer(lay, gpu)
+    pool.g2s_device(torch.cuda.current_stream().cuda_stream)
+    k = spec.top_k
+    x = make_x(1, spec.hidden, seed=41)
+    xd = to_dev_bits(x, gpu)
+    e = [5, 5, 2, 9, 5, 1, 0, 3][:k] if k == 8 else [7, 2, 7, 7][:k]
+    idx = np.array([e], np.int32)
+    print(f"[repeat] {spec.quant.mode} experts {e}", flush=True)
+    w = np.full((1, k), 1.0 / k, np.float32)
+    y1 = torch.empty((1, k, spec.hidden), dtype=torch.bfloat16, device=gpu)
+    ops.moe_forward(spec, pool, xd, torch.from_numpy(idx).to(gpu), torch.from_numpy(w).to(gpu),
+                    y_unreduced=y1, flags=ops.path_flag(1, k))
+    y2 = torch.full((k, spec.hidden), float("nan"), dtype=torch.bfloat16, device=gpu)
+    ops.forward_pairs(spec, pool, xd, torch.zeros(k, dtype=torch.int32, device=gpu),
+                      torch.from_numpy(idx[0]).to(gpu), torch.arange(k, dtype=torch.int32, device=gpu), y2,
+                      ops.path_flag(1, k))
+    torch.cuda.synchronize()
+    _, yref = oracle.moe_forward(spec, lay.experts, x, idx, w, want_unreduced=True)
+    ref = F.bf16_bits_to_f32(yref)[0]
+    got1 = F.bf16_bits_to_f32(bits(y1))[0]
+    for j in range(k):
+        assert oracle.rel_l2(got1[j], ref[j]) < TOL, j
+    assert np.array_equal(bits(y1).reshape(k, -1), bits(y2))
+    pool.close()
+
+
 @pytest.mark.parametrize("T", [1, 16])
 def test_unreduced_rows(gpu, T):
     """The operator's unreduced [T, k, H] rows (the reference boundary) against the oracle."""
