@@ -849,18 +849,24 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
         // the wave's pair goes through a 4 KB LDS area ([nj][row half][lane] x 16 bytes): written
         // once a pair, read back in the operand layout once a stage (same wave, in order)
         uint8_t* const bst = ring + kRing - kBPairLds + wv * (kBPairLds / kGemmWaves);
+        // Load lane L = 4 r + c (row r of the half, piece c) sits in 16-byte slot L ^ (r >> 2) of
+        // its 64: a stage's read (pieces c = 2 t + kh of rows r = 0..15) then touches 16
+        // distinct slots mod 16, so neither the write nor the read has bank conflicts.
         auto stash = [&](const PReg& pr) __attribute__((always_inline)) {
+            const int slot = lane ^ ((lane >> 4) & 3);
 #pragma unroll
             for (int nj = 0; nj < kNJ; ++nj)
 #pragma unroll
                 for (int h = 0; h < 2; ++h)
-                    *reinterpret_cast<u32x4_t*>(bst + ((nj * 2 + h) * 64 + lane) * 16) = pr.w[nj][h];
+                    *reinterpret_cast<u32x4_t*>(bst + ((nj * 2 + h) * 64 + slot) * 16) = pr.w[nj][h];
         };
-        const int srow = ((l32 >> 4) * 64 + 4 * (l32 & 15) + kh) * 16;   // piece (0, kh) of row l32
+        const int srow = ((l32 >> 4) * 64 + 4 * (l32 & 15)) * 16;   // row l32's four slots
+        const int sx = (l32 & 15) >> 2;                              // their swizzle
         auto fetch_b = [&](int t, BReg& out) __attribute__((always_inline)) {
+            const int so = srow + (((2 * t + kh) ^ sx) << 4);
 #pragma unroll
             for (int nj = 0; nj < kNJ; ++nj) {
-                const u32x4_t v = *reinterpret_cast<const u32x4_t*>(bst + nj * 2 * 64 * 16 + srow + 32 * t);
+                const u32x4_t v = *reinterpret_cast<const u32x4_t*>(bst + nj * 2 * 64 * 16 + so);
 #pragma unroll
                 for (int w = 0; w < 4; ++w) out.w[nj][w] = v[w];
             }
