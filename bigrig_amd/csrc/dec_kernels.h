@@ -765,6 +765,8 @@ __global__ __launch_bounds__(kThreads) void k_dec_gateup1(FwdArgs a, uint16_t* _
     int e = pe, eslot = -1;   // wave 0: rank lane's expert and its slot
     float w = 0.0f, sg = 0.0f;
     if (wv == 0) {
+        // the ranking is every wave's wait: it issues ahead of the other blocks' work on the CU
+        __builtin_amdgcn_s_setprio(3);
         if constexpr (KP > 0) {
             const RouteRule rr{a.route_bias, a.route_mode, a.n_group, a.topk_group, a.route_scale};
             float sel_v;
@@ -791,6 +793,7 @@ __global__ __launch_bounds__(kThreads) void k_dec_gateup1(FwdArgs a, uint16_t* _
             }
         }
         if (lane < nu) s_slot[lane] = eslot;
+        __builtin_amdgcn_s_setprio(0);
     }
     __syncthreads();
     if (wv == 0 && blockIdx.x == 0) {
