@@ -723,6 +723,7 @@ template <int MODE, int UPL, int KP>
 __global__ __launch_bounds__(kThreads) void k_dec_gateup1(FwdArgs a, uint16_t* __restrict__ hbuf, int hstride,
                                                           DecTable* __restrict__ table, int lsp, int nu) {
     prefetch_args(a);
+    __builtin_amdgcn_s_setprio(2);
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     __shared__ int32_t s_slot[kMaxU];
     constexpr int kG = 8;                         // slot-table registers per lane (E <= 512)
@@ -793,7 +794,7 @@ __global__ __launch_bounds__(kThreads) void k_dec_gateup1(FwdArgs a, uint16_t* _
             }
         }
         if (lane < nu) s_slot[lane] = eslot;
-        __builtin_amdgcn_s_setprio(0);
+        __builtin_amdgcn_s_setprio(2);
     }
     __syncthreads();
     if (wv == 0 && blockIdx.x == 0) {
@@ -833,6 +834,7 @@ __global__ __launch_bounds__(kThreads) void k_dec_gateup1(FwdArgs a, uint16_t* _
         bg = bf2f(reinterpret_cast<const uint16_t*>(base + L.p[0].bias)[row]);
         if (gated) bu = bf2f(reinterpret_cast<const uint16_t*>(base + L.p[1].bias)[row]);
     }
+    __builtin_amdgcn_s_setprio(0);
     float pg = 0.f, pu = 0.f;
 #pragma unroll
     for (int j = 0; j < UPL; ++j) {
@@ -1048,6 +1050,7 @@ template <int MODE, int UPL>
 __global__ __launch_bounds__(kThreads) void k_dec_gateupT(FwdArgs a, uint16_t* __restrict__ hbuf, int hstride,
                                                           const DecTable* __restrict__ table, int lsp, int nrb) {
     prefetch_args(a);
+    __builtin_amdgcn_s_setprio(2);
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     __shared__ int32_t s_tok[kMaxTok];
     const int SP = 1 << lsp;
@@ -1090,6 +1093,7 @@ __global__ __launch_bounds__(kThreads) void k_dec_gateupT(FwdArgs a, uint16_t* _
     float* xsum = reinterpret_cast<float*>(lds + (size_t)kPlanTok * U * kXU);
     stage_dense<MODE>(a.x, H, nt, [&](int i) { return s_tok[i]; }, xs, xsum);
     __syncthreads();
+    __builtin_amdgcn_s_setprio(0);
     for (int i = 0; i < nt; ++i) {
         const int pair = s_pair[i];
         float pg = 0.f, pu = 0.f;
@@ -1122,6 +1126,7 @@ __global__ __launch_bounds__(kThreads) void k_dec_downT(FwdArgs a, const uint16_
                                                         uint16_t* __restrict__ y_routed,
                                                         uint16_t* __restrict__ y_shared) {
     prefetch_args(a);
+    __builtin_amdgcn_s_setprio(2);
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     __shared__ int32_t s_pair[kMaxTok];
     const int SP = 1 << lsp;
@@ -1153,6 +1158,7 @@ __global__ __launch_bounds__(kThreads) void k_dec_downT(FwdArgs a, const uint16_
     float* hsum = reinterpret_cast<float*>(lds + (size_t)kPlanTok * Us * kXU);
     stage_dense<MODE>(hbuf, hstride, nt, [&](int i) { return s_pair[i]; }, hs, hsum);
     __syncthreads();
+    __builtin_amdgcn_s_setprio(0);
     for (int i = 0; i < nt; ++i) {
         const int pair = s_pair[i];
         float p = 0.f;
@@ -1378,6 +1384,7 @@ __global__ __launch_bounds__(kThreads) void k_dec_down_fit(FwdArgs a, const uint
                                                            const DecTable* __restrict__ table, int lsp,
                                                            int lrbd, int nu) {
     prefetch_args(a);
+    __builtin_amdgcn_s_setprio(2);
     const int SP = 1 << lsp;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int tid = threadIdx.x, lane = tid & 63;
@@ -1427,6 +1434,7 @@ __global__ __launch_bounds__(kThreads) void k_dec_down_fit(FwdArgs a, const uint
             dense_store<MODE, kStageB>(hstride, PT, 0, hrows, hs, hsum);
             stage_dense<MODE>(hbuf, hstride, PT, ident, hs, hsum, kStageB * kThreads);
             __syncthreads();
+            __builtin_amdgcn_s_setprio(0);
         }
         const int pr[kMaxTok] = {(int)p0.x, (int)p0.y, (int)p0.z, (int)p0.w,
                                  (int)p1.x, (int)p1.y, (int)p1.z, (int)p1.w};
