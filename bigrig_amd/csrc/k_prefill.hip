@@ -568,21 +568,26 @@ __device__ __forceinline__ void pf_tile(const FwdArgs& a, const int32_t* __restr
     // ---- A: wave wv fills 1 KB chunks [wv * NA, wv * NA + NA) of a stage's A tile; lane l of
     // chunk ii lands in 16-byte slot ii * 64 + l = (row, physical slot p) and carries the
     // row's logical K chunk p ^ key(row)
-    const __amdgpu_buffer_rsrc_t ra_rsrc = KIND == 0
-        ? make_rsrc(a.x, (uint32_t)((int64_t)a.T * H * 2))
-        : make_rsrc(hbuf, (uint32_t)((int64_t)(m0 + rows) * hstride * 2));
+    // A rows past `rows` (the padding of an expert's last tile) are copied from past the end of
+    // the buffer: the buffer unit's range check returns zeros without touching memory, so they
+    // cost no cache traffic (their outputs are never stored) and every wave still issues the
+    // same copies, which the stage waits count
+    const uint32_t a_bytes = KIND == 0 ? (uint32_t)((int64_t)a.T * H * 2)
+                                       : (uint32_t)((int64_t)(m0 + rows) * hstride * 2);
+    const __amdgpu_buffer_rsrc_t ra_rsrc = make_rsrc(KIND == 0 ? (const void*)a.x : (const void*)hbuf, a_bytes);
     uint32_t va[NA];
 #pragma unroll
     for (int i = 0; i < NA; ++i) {
         const int ci = (wv * NA + i) * 64 + lane;
         const int rl = ci >> 3;                            // LDS row
-        const int r = min(rl, rows - 1);                   // source row (past `rows`: repeat)
+        const int r = min(rl, rows - 1);
         const int c = (ci & 7) ^ a_key(rl);
         if constexpr (KIND == 0) {
             va[i] = (uint32_t)pair_token(a, order[m0 + r]) * (uint32_t)(H * 2) + c * 16;
         } else {
             va[i] = (uint32_t)(m0 + r) * (uint32_t)(hstride * 2) + c * 16;
         }
+        if (rl >= rows) va[i] = a_bytes;
     }
     // ---- B: the block's 256 weight rows (KIND 0: gate rows of features nt * 128 + [0, 128),
     // then the up rows of the same features; KIND 1: down rows nt * 256 + [0, 256)), 8 B bytes
